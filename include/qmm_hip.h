@@ -1,0 +1,160 @@
+/*
+ * qmm_hip.h — C ABI of the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * It replaces the quantized CPU compute layer of the reference engine
+ * (src/v182_r22_breakthrough_engine.c, cited E:<line>): GGUF-packed
+ * Q4_K / Q5_K / Q6_K / Q8_0 weight rows stay in their native block layout in
+ * HBM, fp32 activations go in, fp32 outputs come out. Plain C types only:
+ * device buffers are `void *` / typed pointers obtained from qmm_malloc (or
+ * any HIP allocation on the same device), streams are `void *` hipStream_t.
+ *
+ * All compute entry points are asynchronous on the context's stream and
+ * return a status code (QMM_OK or a QMM_E* value); none fails silently. A
+ * context is not thread-safe: use one context per host thread.
+ *
+ * Numeric contract (fp32 boundary over the reference's fp16 one):
+ *  - activations: each fp32 value is rounded to fp16 (round to nearest even)
+ *    and then quantized exactly as quantize_row_fp16_to_q8_k (E:925-990) /
+ *    quantize_row_fp16_to_q8_0 (E:1016-1064). Inputs must be finite with
+ *    |x| < 65520 (the fp16 range).
+ *  - dots: exact int32 per block, then the reference's fp32 expression per
+ *    block, blocks accumulated in order (eval_single_lm_row_dot
+ *    E:10986-11105, sdot_row_q*_batch E:3109-3408); outputs are the fp32
+ *    sums the reference casts to fp16 at E:3582-3613.
+ */
+#ifndef QMM_HIP_H
+#define QMM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+#define QMM_OK 0
+#define QMM_EINVAL 1  /* null pointer, non-positive size, bad stride */
+#define QMM_ETYPE 2   /* ggml type not supported by this path */
+#define QMM_ESHAPE 3  /* K not a multiple of the block size, cols != K, ... */
+#define QMM_EHIP 4    /* HIP runtime error (message in qmm_last_error) */
+#define QMM_ENOMEM 5  /* device allocation failed */
+#define QMM_EALIGN 6  /* device pointer misaligned for its format */
+
+/* ggml type ids (E:115-120) */
+#define QMM_TYPE_Q8_0 8
+#define QMM_TYPE_Q4_K 12
+#define QMM_TYPE_Q5_K 13
+#define QMM_TYPE_Q6_K 14
+
+typedef struct qmm_context qmm_context;
+
+/* Matrix task: SdotMatrixTask (E:888-899) with fp32 dst/residual and device
+ * pointers. Row r of the task reads w_base + r * row_bytes; output token m,
+ * row r goes to dst[m * dst_stride + r] (+ residual[m * res_stride + r]). */
+typedef struct {
+    const void *w_base;    /* device: rows x row_bytes of packed GGUF blocks */
+    uint32_t type;         /* QMM_TYPE_* */
+    size_t row_bytes;      /* must equal qmm_row_bytes(type, cols) */
+    float *dst;            /* device fp32 [M][dst_stride] */
+    size_t dst_stride;     /* >= rows */
+    const float *residual; /* device fp32 [M][res_stride], or NULL */
+    size_t res_stride;     /* >= rows when residual != NULL */
+    int rows;
+    int cols;              /* must equal the dispatch K */
+    int start_row;         /* written by the dispatcher (concatenated row space) */
+} qmm_matrix_task;
+
+/* ------------------------------------------------------------- lifecycle */
+/* New context on HIP device `device` with its own (default-priority) stream.
+ * Replaces the engine's implicit global state (g_sdot_input E:901, the
+ * thread pool E:3442-3855). */
+int qmm_init(int device, qmm_context **out_ctx);
+int qmm_destroy(qmm_context *ctx);
+/* Use an external hipStream_t (NULL restores the context's own stream). */
+int qmm_set_stream(qmm_context *ctx, void *hip_stream);
+void *qmm_get_stream(qmm_context *ctx);
+int qmm_synchronize(qmm_context *ctx);
+/* Pre-size the internal activation buffers for M x K dispatches so that
+ * later dispatches up to that size allocate nothing (graph capture). */
+int qmm_reserve(qmm_context *ctx, int max_M, int max_K);
+const char *qmm_status_string(int status);
+const char *qmm_last_error(const qmm_context *ctx);
+/* Device facts: compute units, HBM bytes, gfx arch name. */
+int qmm_device_info(qmm_context *ctx, int *cu_count, size_t *hbm_bytes, char *arch,
+                    size_t arch_len);
+
+/* ---------------------------------------------------------------- sizes */
+/* compute_ggml_bytes / ggml_row_bytes (E:364-374, E:3940-3942); 0 if the
+ * type is unsupported or cols is not a multiple of its block size. */
+size_t qmm_row_bytes(uint32_t type, int64_t cols);
+/* Bytes of a device Q8_K activation buffer for M rows of K values
+ * (BlockQ8K E:868-872 as arrays): qs int8[M][K] at 0, d f32[M][K/256] at
+ * qmm_q8k_d_offset, bsum32 i32[M][K/32] at qmm_q8k_bsum_offset. */
+size_t qmm_q8k_bytes(int M, int K);
+size_t qmm_q8k_d_offset(int M, int K);
+size_t qmm_q8k_bsum_offset(int M, int K);
+/* Q8_0 activations (BlockQ8_0_Fast E:874-877): qs int8[M][K] at 0,
+ * d f32[M][K/32] at qmm_q8_0_d_offset. */
+size_t qmm_q8_0_bytes(int M, int K);
+size_t qmm_q8_0_d_offset(int M, int K);
+
+/* --------------------------------------------------------------- memory */
+int qmm_malloc(qmm_context *ctx, size_t bytes, void **dev_ptr); /* 256-B aligned */
+int qmm_free(qmm_context *ctx, void *dev_ptr);
+int qmm_memcpy_h2d(qmm_context *ctx, void *dst_dev, const void *src_host, size_t bytes);
+int qmm_memcpy_d2h(qmm_context *ctx, void *dst_host, const void *src_dev, size_t bytes);
+int qmm_memcpy_d2d(qmm_context *ctx, void *dst_dev, const void *src_dev, size_t bytes);
+
+/* Weight residency: copy rows x qmm_row_bytes(type, cols) bytes of packed
+ * GGUF blocks from host memory into a new HBM allocation, unchanged (the
+ * reference reads them in place from the GGUF mmap, E:4174-4176, E:12377).
+ * Free with qmm_free. */
+int qmm_weight_upload(qmm_context *ctx, const void *host_blocks, uint32_t type, int64_t rows,
+                      int64_t cols, void **dev_blocks);
+
+/* ------------------------------------------------------------- quantize */
+/* quantize_row_fp16_to_q8_k (E:925-990) on M rows of fp32 x [M][K]. */
+int qmm_quantize_q8k(qmm_context *ctx, const float *x, int M, int K, void *q8k_out);
+/* quantize_row_fp16_to_q8_0 (E:1016-1064). */
+int qmm_quantize_q8_0(qmm_context *ctx, const float *x, int M, int K, void *q80_out);
+/* swiglu_chunk_worker (E:4326-4359): h = silu(gate) * up in fp32, then the
+ * Q8_K quantizer per 256 values; gate/up/h are [M][N]. h_out may be NULL. */
+int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, int N,
+                   float *h_out, void *q8k_out);
+
+/* -------------------------------------------------------------- dequant */
+/* dequant_contiguous_fast (E:3856-3902): rows x cols packed blocks -> fp16
+ * bits [rows][cols] (for validation; not on the matmul path). */
+int qmm_dequantize_f16(qmm_context *ctx, const void *w_blocks, uint32_t type, int64_t rows,
+                       int64_t cols, uint16_t *dst);
+
+/* ------------------------------------------------------------- dispatch */
+/* sdot_gemm_multi_dispatch (E:4188-4262): quantize x [M][K] once (Q8_K for
+ * K-quant tasks, Q8_0 for Q8_0 tasks) into the context's buffers, then run
+ * every task on the shared quantized input. */
+int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K,
+                            qmm_matrix_task *tasks, int n_tasks);
+/* The prequantized form (the engine's g_sdot_input_q8k_prequantized flag,
+ * E:4186, E:4207-4208, made explicit): q8k / q80 are device buffers in the
+ * layouts above; either may be NULL when no task needs it. */
+int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80,
+                                         int M, int K, qmm_matrix_task *tasks, int n_tasks);
+
+/* ---------------------------------------------------- graphs and timing */
+/* Capture the context stream's work into a HIP graph (hipStreamBeginCapture
+ * / hipGraphInstantiate) and replay it; for launch-bound loops. */
+int qmm_graph_begin(qmm_context *ctx);
+int qmm_graph_end(qmm_context *ctx, void **graph_exec);
+int qmm_graph_launch(qmm_context *ctx, void *graph_exec);
+int qmm_graph_destroy(void *graph_exec);
+/* HIP events on the context stream: begin records, end records and waits,
+ * returning the elapsed milliseconds. */
+int qmm_timer_begin(qmm_context *ctx);
+int qmm_timer_end(qmm_context *ctx, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMM_HIP_H */

@@ -1,0 +1,154 @@
+// qmm_device.h — device-side helpers shared by the gfx950 kernels, and the
+// launcher interface between the kernel files and the C ABI (qmm_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qmm {
+
+// ggml type ids (E:115-120)
+constexpr uint32_t kQ8_0 = 8;
+constexpr uint32_t kQ4_K = 12;
+constexpr uint32_t kQ5_K = 13;
+constexpr uint32_t kQ6_K = 14;
+
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Q8_K activation buffer layout (all sections 256-B aligned):
+//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32]
+struct Q8KLayout {
+    size_t d_off, bs_off, total;
+    __host__ __device__ Q8KLayout(int M, int K) {
+        const size_t mk = size_t(M) * size_t(K);
+        d_off = align256(mk);
+        bs_off = align256(d_off + 4 * size_t(M) * size_t(K / 256));
+        total = align256(bs_off + 4 * size_t(M) * size_t(K / 32));
+    }
+};
+// Q8_0 activation buffer layout: qs int8[M][K] | d f32[M][K/32]
+struct Q80Layout {
+    size_t d_off, total;
+    __host__ __device__ Q80Layout(int M, int K) {
+        d_off = align256(size_t(M) * size_t(K));
+        total = align256(d_off + 4 * size_t(M) * size_t(K / 32));
+    }
+};
+
+// Activation views handed to the matmul kernels.
+struct Q8KView {
+    const int8_t *qs;   // [M][K]
+    const float *d;     // [M][K/256]
+    const int32_t *bs;  // [M][K/32]
+};
+struct Q80View {
+    const int8_t *qs;  // [M][K]
+    const float *d;    // [M][K/32]
+};
+
+// One matmul launch: a task after validation.
+struct MatArgs {
+    const uint8_t *w;  // packed rows
+    size_t row_bytes;
+    int N;             // rows
+    int K;             // cols
+    int M;             // tokens
+    float *y;          // [M][ldy]
+    size_t ldy;
+    const float *res;  // [M][ldr] or nullptr
+    size_t ldr;
+};
+
+// Launchers (return hipSuccess or the launch error).
+hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s);
+hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStream_t s);
+hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
+                             void *out, hipStream_t s);
+hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
+                              uint16_t *dst, hipStream_t s);
+hipError_t launch_gemv(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
+                       hipStream_t s);
+hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
+                       hipStream_t s);
+
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+
+// ------------------------------------------------------------ fp16 helpers
+__device__ inline float fp16_bits_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+// fp32 -> fp16 (round to nearest even, v_cvt_f16_f32) -> fp32
+__device__ inline float round_to_fp16(float x) { return (float)(_Float16)x; }
+__device__ inline uint16_t f32_to_fp16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// ------------------------------------------------------------ int helpers
+__device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// Per-byte (q - 32) for bytes holding 0..63: ((q | 0x80) - 0x20) ^ 0x80.
+__device__ inline uint32_t sub32_bytes(uint32_t q) {
+    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+__device__ inline uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t byte_shift) {
+    return __builtin_amdgcn_alignbyte(hi, lo, byte_shift);
+}
+
+// ------------------------------------------------------- cross-lane sums
+// DPP sums inside aligned lane groups. All lanes of the group must be active.
+__device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ inline int dpp_half_mirror(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false); }
+__device__ inline int group4_sum(int v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    return v;
+}
+__device__ inline int group8_sum(int v) {
+    v = group4_sum(v);
+    v += dpp_half_mirror(v);
+    return v;
+}
+
+// --------------------------------------------------------- global loads
+// 16 B load of an address that is 16-B aligned.
+__device__ inline uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ inline uint2 ld8(const void *p) { return *reinterpret_cast<const uint2 *>(p); }
+// 8 bytes starting at a 2-B aligned address: the aligned dwords that hold
+// them, then a funnel shift by the misalignment. Every dword read contains
+// at least one requested byte, so the read never leaves the pages of the
+// requested range.
+__device__ inline uint2 ld8_a2(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    const uint32_t sh = uint32_t(a & 3);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[sh ? 2 : 1];
+    return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
+}
+// the 16-bit value at a 2-B aligned address
+__device__ inline uint32_t ld16b_a2(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+    return (w >> ((a & 2) * 8)) & 0xFFFFu;
+}
+
+// get_scale_min_k4 (E:743-749) for sub-block j given the 12 scale bytes
+// as three little-endian dwords s0, s1, s2.
+__device__ inline uint32_t byte_of(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = (i < 4) ? s0 : ((i < 8) ? s1 : s2);
+    return (w >> ((i & 3) * 8)) & 0xFFu;
+}
+__device__ inline void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &m) {
+    if (j < 4) {
+        sc = int(byte_of(s0, s1, s2, j) & 63u);
+        m = int(byte_of(s0, s1, s2, j + 4) & 63u);
+    } else {
+        const uint32_t qj4 = byte_of(s0, s1, s2, j + 4);
+        sc = int((qj4 & 0x0Fu) | ((byte_of(s0, s1, s2, j - 4) >> 6) << 4));
+        m = int((qj4 >> 4) | ((byte_of(s0, s1, s2, j) >> 6) << 4));
+    }
+}
+
+#endif  // device compile
+
+}  // namespace qmm

@@ -1,0 +1,266 @@
+// qmm_mfma.hip — small-M (tree-verify, M = 2..64) and prefill (M = 512)
+// GEMM over GGUF-packed rows with int8 MFMA, gfx950.
+//
+// Tile. A wavefront computes 16 weight rows x (16 * TT) tokens with
+// v_mfma_i32_16x16x32_i8: A = Q8_K (or Q8_0) activation codes (16 tokens x
+// 32 k), B = weight codes unpacked to int8 in registers (32 k x 16 rows).
+// Lane l supplies token / weight row l % 16 and the k-slice l / 16 of both
+// operands, and receives D[token 4 * (l / 16) + r][row l % 16], r = 0..3, so
+// every lane owns one weight row and needs only that row's scales.
+//
+// One MFMA covers one scale unit of the format (a 32-value sub-block of
+// Q4_K / Q5_K, a 16-value group of Q6_K padded with zero weights, a 32-value
+// Q8_0 block), so its int32 result is the unit's exact dot; the unit scales,
+// the min term and the per-block fp32 expression are applied exactly as the
+// reference's scalar kernels do, and blocks are accumulated in order per
+// output — the result equals the reference's fp32 sum bit for bit.
+#include "qmm_device.h"
+
+namespace qmm {
+
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+__device__ inline int4v mfma16x16x32(uint2 a, uint2 b) {
+    const long av = (long)(((uint64_t)a.y << 32) | a.x);
+    const long bv = (long)(((uint64_t)b.y << 32) | b.x);
+    const int4v z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, z, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- formats
+// Each format gives, for lane k-slice c (0..3) of one weight row's block:
+//   NU units; B operand (8 int8) and integer scale of unit u; the k offset
+//   (inside the block) of the lane's 8 activation values for unit u; and
+//   the block's fp32 update.
+
+// Q4_K: unit u = sub-block 2j + h; lane c holds values 64j + 32h + 8c + t.
+struct MQ4K {
+    static constexpr int NU = 8, QK = 256, BB = 144;
+    static constexpr bool kMin = true;
+    struct W { uint4 h; uint2 q[4]; };
+    __device__ static W load(const uint8_t *blk, int c) {
+        W w;
+        w.h = ld16(blk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w.q[j] = ld8(blk + 16 + 32 * j + 8 * c);
+        return w;
+    }
+    __device__ static int koff(int u, int c) { return 64 * (u >> 1) + 32 * (u & 1) + 8 * c; }
+    __device__ static uint2 bop(const W &w, int u, int c) {
+        (void)c;
+        const uint2 q = w.q[u >> 1];
+        const int sh = 4 * (u & 1);
+        return make_uint2((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
+    }
+};
+
+// Q5_K: as Q4_K with the high bit u of qh[8c + t].
+struct MQ5K {
+    static constexpr int NU = 8, QK = 256, BB = 176;
+    static constexpr bool kMin = true;
+    struct W { uint4 h; uint2 qh; uint2 q[4]; };
+    __device__ static W load(const uint8_t *blk, int c) {
+        W w;
+        w.h = ld16(blk);
+        w.qh = ld8(blk + 16 + 8 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w.q[j] = ld8(blk + 48 + 32 * j + 8 * c);
+        return w;
+    }
+    __device__ static int koff(int u, int c) { return MQ4K::koff(u, c); }
+    __device__ static uint2 bop(const W &w, int u, int c) {
+        (void)c;
+        const uint2 q = w.q[u >> 1];
+        const int sh = 4 * (u & 1);
+        return make_uint2(((q.x >> sh) & 0x0F0F0F0Fu) | (((w.qh.x >> u) & 0x01010101u) << 4),
+                          ((q.y >> sh) & 0x0F0F0F0Fu) | (((w.qh.y >> u) & 0x01010101u) << 4));
+    }
+};
+
+// Q6_K: unit u = (hf, i, is) = (u >> 3, (u >> 1) & 3, u & 1), 16 values
+// 128hf + 32i + 16is + l, scale sc[8hf + 2i + is]. Lanes c = 0, 1 hold the
+// 8 values l = 8c + t; lanes c = 2, 3 supply zero weights.
+struct MQ6K {
+    static constexpr int NU = 16, QK = 256, BB = 210;
+    static constexpr bool kMin = false;
+    struct W { uint2 a[4], b[4], qh[4]; uint2 s0, s1; uint32_t d; };
+    __device__ static W load(const uint8_t *blk, int c) {
+        W w;
+        const int c2 = c & 1;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int is = 0; is < 2; ++is) {
+                const int p = 2 * hf + is, l = 16 * is + 8 * c2;
+                w.a[p] = ld8_a2(blk + 64 * hf + l);
+                w.b[p] = ld8_a2(blk + 64 * hf + 32 + l);
+                w.qh[p] = ld8_a2(blk + 128 + 32 * hf + l);
+            }
+        w.s0 = ld8_a2(blk + 192);
+        w.s1 = ld8_a2(blk + 200);
+        w.d = ld16b_a2(blk + 208);
+        return w;
+    }
+    __device__ static int koff(int u, int c) {
+        return 128 * (u >> 3) + 32 * ((u >> 1) & 3) + 16 * (u & 1) + 8 * (c & 1);
+    }
+    __device__ static uint2 bop(const W &w, int u, int c) {
+        if (c >= 2) return make_uint2(0u, 0u);
+        const int hf = u >> 3, i = (u >> 1) & 3, is = u & 1, p = 2 * hf + is;
+        const uint2 src = (i & 1) ? w.b[p] : w.a[p];
+        const int nsh = (i >> 1) * 4;
+        const int hsh = 2 * i;
+        const uint32_t x = ((src.x >> nsh) & 0x0F0F0F0Fu) | (((w.qh[p].x >> hsh) & 0x03030303u) << 4);
+        const uint32_t y = ((src.y >> nsh) & 0x0F0F0F0Fu) | (((w.qh[p].y >> hsh) & 0x03030303u) << 4);
+        return make_uint2(sub32_bytes(x), sub32_bytes(y));
+    }
+    __device__ static int scale(const W &w, int u) {
+        const int idx = 8 * (u >> 3) + 2 * ((u >> 1) & 3) + (u & 1);
+        const uint2 s = (idx < 8) ? w.s0 : w.s1;
+        const uint64_t s64 = (uint64_t(s.y) << 32) | s.x;
+        return int(int8_t(uint8_t(s64 >> (8 * (idx & 7)))));
+    }
+};
+
+// Q8_0: one unit per 32-value block; lane c holds values 8c + t.
+struct MQ80 {
+    static constexpr int NU = 1, QK = 32, BB = 34;
+    static constexpr bool kMin = false;
+    struct W { uint2 q; uint32_t d; };
+    __device__ static W load(const uint8_t *blk, int c) { return {ld8_a2(blk + 2 + 8 * c), ld16b_a2(blk)}; }
+    __device__ static int koff(int u, int c) { (void)u; return 8 * c; }
+    __device__ static uint2 bop(const W &w, int u, int c) { (void)u; (void)c; return w.q; }
+};
+
+template <class F> struct ActOf { using T = Q8KView; };
+template <> struct ActOf<MQ80> { using T = Q80View; };
+
+// Scales / mins of the lane's row for the current block.
+template <class F> struct Scales { int sc[F::NU]; int m[F::NU]; float d, dmin; };
+
+template <class F>
+__device__ inline void decode_scales(const typename F::W &w, Scales<F> &s) {
+    if constexpr (F::NU == 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) scale_min_k4(u, w.h.y, w.h.z, w.h.w, s.sc[u], s.m[u]);
+        s.d = fp16_bits_to_f32(w.h.x & 0xFFFFu);
+        s.dmin = fp16_bits_to_f32(w.h.x >> 16);
+    } else if constexpr (F::NU == 16) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            s.sc[u] = F::scale(w, u);
+            s.m[u] = 0;
+        }
+        s.d = fp16_bits_to_f32(w.d);
+        s.dmin = 0.0f;
+    } else {
+        s.sc[0] = 1;
+        s.m[0] = 0;
+        s.d = fp16_bits_to_f32(w.d);
+        s.dmin = 0.0f;
+    }
+}
+
+// TT token tiles of 16 per wave; 4 waves per workgroup on consecutive
+// 16-row tiles; grid.y walks token groups of 16 * TT.
+template <class F, int TT>
+__global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>::T x) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int nl = lane & 15, c = lane >> 4;
+    const int n0 = (int(blockIdx.x) * 4 + wid) * 16;
+    if (n0 >= a.N) return;
+    const int m0 = int(blockIdx.y) * 16 * TT;
+    const int n = n0 + nl;
+    const int nload = min(n, a.N - 1);
+    const int nb = a.K / F::QK;
+    const uint8_t *wrow = a.w + size_t(nload) * a.row_bytes;
+
+    float acc[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+
+    typename F::W wcur = F::load(wrow, c);
+    for (int b = 0; b < nb; ++b) {
+        typename F::W wnext;
+        if (b + 1 < nb) wnext = F::load(wrow + size_t(b + 1) * F::BB, c);
+        Scales<F> s;
+        decode_scales<F>(wcur, s);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int tokA = m0 + 16 * t + nl;  // A-operand token of this lane
+            const bool okA = tokA < a.M;
+            const int8_t *xa = x.qs + size_t(okA ? tokA : 0) * a.K + size_t(b) * F::QK;
+            int S[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < F::NU; ++u) {
+                const uint2 av = okA ? ld8(xa + F::koff(u, c)) : make_uint2(0u, 0u);
+                const int4v D = mfma16x16x32(av, F::bop(wcur, u, c));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = m0 + 16 * t + 4 * c + r;  // output token of D[r]
+                if (tok >= a.M) continue;
+                if constexpr (F::kMin) {
+                    // E:11024-11026: Mb = sum m_j * bsum32_j; acc += dx * (d*S - dmin*Mb)
+                    const int32_t *bs = x.bs + (size_t(tok) * nb + b) * 8;
+                    const uint4 b0 = ld16(bs), b1 = ld16(bs + 4);
+                    const int bsv[8] = {int(b0.x), int(b0.y), int(b0.z), int(b0.w),
+                                        int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
+                    int Mb = 0;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) Mb += __mul24(s.m[u], bsv[u]);
+                    const float dx = x.d[size_t(tok) * nb + b];
+                    acc[t][r] += dx * (s.d * (float)S[r] - s.dmin * (float)Mb);
+                } else {
+                    // E:11101 / E:3405: acc += (d * dx) * S
+                    const float dx = x.d[size_t(tok) * nb + b];
+                    acc[t][r] += (s.d * dx) * (float)S[r];
+                }
+            }
+        }
+        wcur = wnext;
+    }
+    if (n >= a.N) return;
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = m0 + 16 * t + 4 * c + r;
+            if (tok >= a.M) continue;
+            float v = acc[t][r];
+            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+            a.y[size_t(tok) * a.ldy + n] = v;
+        }
+}
+
+template <class F, int TT>
+static hipError_t launch_mfma_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    const int tiles = (a.N + 15) / 16;
+    const dim3 grid(unsigned((tiles + 3) / 4), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
+    hipLaunchKernelGGL((mfma_kernel<F, TT>), grid, dim3(256), 0, s, a, x);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    if (a.M <= 16) return launch_mfma_t<F, 1>(a, x, s);
+    if (a.M <= 32) return launch_mfma_t<F, 2>(a, x, s);
+    return launch_mfma_t<F, 4>(a, x, s);
+}
+
+hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
+                       hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_mfma_f<MQ4K>(a, xk, s);
+        case kQ5_K: return launch_mfma_f<MQ5K>(a, xk, s);
+        case kQ6_K: return launch_mfma_f<MQ6K>(a, xk, s);
+        case kQ8_0: return launch_mfma_f<MQ80>(a, x0, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace qmm

@@ -1,0 +1,221 @@
+// qmm_quant.hip — activation quantizers (fp32 -> fp16 -> Q8_K / Q8_0), the
+// SwiGLU + Q8_K requant producer, and the validation dequantizer.
+//
+// One wavefront per 256-value block: each lane owns 4 consecutive values
+// (one 16-B load), the block amax is a wave max, bsum32 is an 8-lane DPP sum.
+// Division and rounding follow the reference exactly: d = amax / 127.0f and
+// id = 127.0f / amax correctly rounded, q = rint(x * id) (round to nearest
+// even, as lrintf under the default mode), clamp to [-127, 127].
+#include "qmm_device.h"
+
+namespace qmm {
+
+// Quantize the 4 values a lane owns; returns packed int8 codes, writes the
+// code sum. `amax` is the block's max |x| (already reduced).
+__device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
+    if (amax == 0.0f) {  // E:947-952
+        sum = 0;
+        return 0u;
+    }
+    const float id = 127.0f / amax;  // E:954
+    int q[4];
+    const float h[4] = {h0, h1, h2, h3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int v = (int)rintf(h[i] * id);  // E:979
+        v = v > 127 ? 127 : v;
+        v = v < -127 ? -127 : v;
+        q[i] = v;
+    }
+    sum = q[0] + q[1] + q[2] + q[3];
+    return (uint32_t(q[0]) & 0xFFu) | ((uint32_t(q[1]) & 0xFFu) << 8) |
+           ((uint32_t(q[2]) & 0xFFu) << 16) | ((uint32_t(q[3]) & 0xFFu) << 24);
+}
+
+__device__ inline float wave_max(float a) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    return a;
+}
+
+// Quantize one fp16-rounded 256-value block held 4 values per lane and
+// store it as Q8_K block `blk` (flattened over [M][K/256]).
+__device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
+                                       size_t blk, int8_t *qs, float *d, int32_t *bs) {
+    float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
+    a = wave_max(a);  // E:941-946
+    int sum;
+    const uint32_t packed = quant4(h0, h1, h2, h3, a, sum);
+    reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
+    sum = group8_sum(sum);  // bsum32 over 32 values = 8 lanes
+    if ((lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
+    if (lane == 0) d[blk] = (a == 0.0f) ? 0.0f : a / 127.0f;  // E:953
+}
+
+// x [M][K] fp32, flattened 256-blocks; one wave per block.
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x,
+                                                           size_t nblk, int8_t *__restrict__ qs,
+                                                           float *__restrict__ d,
+                                                           int32_t *__restrict__ bs) {
+    const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const int lane = threadIdx.x & 63;
+    const float4 v = reinterpret_cast<const float4 *>(x + blk * 256)[lane];
+    store_q8k_block(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z),
+                    round_to_fp16(v.w), lane, blk, qs, d, bs);
+}
+
+// Q8_0: 32-value blocks, 8 lanes each, 8 blocks per wave (flattened).
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
+                                                            size_t nblk32,
+                                                            int8_t *__restrict__ qs,
+                                                            float *__restrict__ d) {
+    const size_t wave = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const size_t blk = wave * 8 + (lane >> 3);
+    if (blk >= nblk32) return;  // whole 8-lane groups drop out together
+    const int sub = lane & 7;
+    const float4 v = reinterpret_cast<const float4 *>(x + blk * 32)[sub];
+    const float h0 = round_to_fp16(v.x), h1 = round_to_fp16(v.y);
+    const float h2 = round_to_fp16(v.z), h3 = round_to_fp16(v.w);
+    float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    int sum;
+    const uint32_t packed = quant4(h0, h1, h2, h3, a, sum);
+    reinterpret_cast<uint32_t *>(qs + blk * 32)[sub] = packed;
+    if (sub == 0) d[blk] = (a == 0.0f) ? 0.0f : a / 127.0f;
+}
+
+// swiglu_chunk_worker (E:4349-4357) on fp32 gate/up: h = (g / (1 + expf(-g))) * u,
+// then the same fp16 round + Q8_K quantizer per 256-value block.
+__global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict__ gate,
+                                                         const float *__restrict__ up,
+                                                         size_t nblk, float *__restrict__ h,
+                                                         int8_t *__restrict__ qs,
+                                                         float *__restrict__ d,
+                                                         int32_t *__restrict__ bs) {
+    const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (blk >= nblk) return;
+    const int lane = threadIdx.x & 63;
+    const float4 g = reinterpret_cast<const float4 *>(gate + blk * 256)[lane];
+    const float4 u = reinterpret_cast<const float4 *>(up + blk * 256)[lane];
+    float4 r;
+    r.x = (g.x / (1.0f + expf(-g.x))) * u.x;
+    r.y = (g.y / (1.0f + expf(-g.y))) * u.y;
+    r.z = (g.z / (1.0f + expf(-g.z))) * u.z;
+    r.w = (g.w / (1.0f + expf(-g.w))) * u.w;
+    if (h) reinterpret_cast<float4 *>(h + blk * 256)[lane] = r;
+    store_q8k_block(round_to_fp16(r.x), round_to_fp16(r.y), round_to_fp16(r.z),
+                    round_to_fp16(r.w), lane, blk, qs, d, bs);
+}
+
+// ---------------------------------------------------------------- dequant
+// One thread per 32-value group (a K-quant sub-block or a Q8_0 block);
+// formulas of dequant_block_q4_k/q5_k/q6_k/q8_0 scalar branches
+// (E:786-800, E:837-852, E:712-740, E:613). Validation path only.
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ w,
+                                                      uint32_t type, size_t ngroups,
+                                                      uint16_t *__restrict__ dst) {
+    const size_t gi = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (gi >= ngroups) return;
+    uint16_t *y = dst + gi * 32;
+    if (type == kQ8_0) {
+        const uint8_t *blk = w + gi * 34;
+        const float dd = fp16_bits_to_f32(uint32_t(blk[0]) | (uint32_t(blk[1]) << 8));
+        for (int i = 0; i < 32; ++i) y[i] = f32_to_fp16_bits(dd * (float)(int8_t)blk[2 + i]);
+        return;
+    }
+    const size_t b = gi >> 3;
+    const int s = int(gi & 7);  // 32-value group inside the 256 block
+    if (type == kQ4_K || type == kQ5_K) {
+        const uint8_t *blk = w + b * (type == kQ4_K ? 144 : 176);
+        const float dd = fp16_bits_to_f32(uint32_t(blk[0]) | (uint32_t(blk[1]) << 8));
+        const float mn = fp16_bits_to_f32(uint32_t(blk[2]) | (uint32_t(blk[3]) << 8));
+        uint8_t sc, m;
+        const uint8_t *q = blk + 4;
+        if (s < 4) {
+            sc = q[s] & 63;
+            m = q[s + 4] & 63;
+        } else {
+            sc = (uint8_t)((q[s + 4] & 0x0F) | ((q[s - 4] >> 6) << 4));
+            m = (uint8_t)((q[s + 4] >> 4) | ((q[s] >> 6) << 4));
+        }
+        const float d1 = dd * (float)sc, m1 = mn * (float)m;
+        const int j = s >> 1, hi = s & 1;
+        if (type == kQ4_K) {
+            const uint8_t *qs = blk + 16 + 32 * j;
+            for (int l = 0; l < 32; ++l) {
+                const int v = hi ? (qs[l] >> 4) : (qs[l] & 0x0F);
+                y[l] = f32_to_fp16_bits(d1 * (float)v - m1);
+            }
+        } else {
+            const uint8_t *qh = blk + 16;
+            const uint8_t *ql = blk + 48 + 32 * j;
+            const uint8_t u = uint8_t(1u << s);
+            for (int l = 0; l < 32; ++l) {
+                const int v = (hi ? (ql[l] >> 4) : (ql[l] & 0x0F)) + ((qh[l] & u) ? 16 : 0);
+                y[l] = f32_to_fp16_bits(d1 * (float)v - m1);
+            }
+        }
+        return;
+    }
+    // Q6_K: 32-value group s = 32 outputs y[half*128 + 32*i + l], l < 32.
+    const uint8_t *blk = w + b * 210;
+    const float dd = fp16_bits_to_f32(uint32_t(blk[208]) | (uint32_t(blk[209]) << 8));
+    const int half = s >> 2, i = s & 3;
+    const uint8_t *ql = blk + half * 64 + ((i & 1) ? 32 : 0);
+    const uint8_t *qh = blk + 128 + half * 32;
+    const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192 + half * 8);
+    for (int l = 0; l < 32; ++l) {
+        const int lo = (i < 2) ? (ql[l] & 0x0F) : (ql[l] >> 4);
+        const int q = (lo | (((qh[l] >> (2 * i)) & 3) << 4)) - 32;
+        const float dsc = dd * (float)sc[(l >> 4) + 2 * i];
+        y[l] = f32_to_fp16_bits(dsc * (float)q);
+    }
+}
+
+hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s) {
+    const Q8KLayout L(M, K);
+    uint8_t *base = static_cast<uint8_t *>(out);
+    const size_t nblk = size_t(M) * size_t(K / 256);
+    const unsigned grid = unsigned((nblk + 3) / 4);
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk,
+                       reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
+                       reinterpret_cast<int32_t *>(base + L.bs_off));
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStream_t s) {
+    const Q80Layout L(M, K);
+    uint8_t *base = static_cast<uint8_t *>(out);
+    const size_t nblk = size_t(M) * size_t(K / 32);
+    const size_t waves = (nblk + 7) / 8;
+    const unsigned grid = unsigned((waves + 3) / 4);
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid), dim3(256), 0, s, x, nblk,
+                       reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off));
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
+                             void *out, hipStream_t s) {
+    const Q8KLayout L(M, N);
+    uint8_t *base = static_cast<uint8_t *>(out);
+    const size_t nblk = size_t(M) * size_t(N / 256);
+    const unsigned grid = unsigned((nblk + 3) / 4);
+    hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(grid), dim3(256), 0, s, gate, up, nblk, h,
+                       reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
+                       reinterpret_cast<int32_t *>(base + L.bs_off));
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
+                              uint16_t *dst, hipStream_t s) {
+    const size_t ngroups = size_t(rows) * size_t(cols / 32);
+    const unsigned grid = unsigned((ngroups + 255) / 256);
+    hipLaunchKernelGGL(dequant_kernel, dim3(grid), dim3(256), 0, s, w, type, ngroups, dst);
+    return hipGetLastError();
+}
+
+}  // namespace qmm

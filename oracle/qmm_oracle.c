@@ -1,0 +1,624 @@
+/*
+ * qmm_oracle.c — CPU restatement of the reference engine's quantized-matmul
+ * path.  TEST INFRASTRUCTURE ONLY: the parity tests, the smoke check and the
+ * CPU-baseline leg of the benchmark use it as the checker; the HIP library
+ * never links or calls it.
+ *
+ * Source followed: src/v182_r22_breakthrough_engine.c (E:<line>), scalar
+ * (#else) branches.  Build with -ffp-contract=off so every fp32 operation is
+ * rounded exactly where the reference's C source rounds it.
+ *
+ * How each function is pinned (tests/test_oracle_*.py):
+ *   qo_fp16_to_f32 / qo_f32_to_fp16  exhaustive/boundary sweep vs numpy's
+ *                                    IEEE float16 conversion, and vs the
+ *                                    compiled reference's (__fp16) casts.
+ *   qo_get_scale_min_k4, qo_dequant_* golden vectors from the compiled
+ *                                    reference + closed-form numpy dequant
+ *                                    + special cases (d=0, sc=0, m=63, all
+ *                                    code values).
+ *   qo_quantize_*                    golden vectors + invariants (|q|<=127,
+ *                                    bsum = sum of codes, zero block, single
+ *                                    non-zero, RNE ties).
+ *   qo_dot_row / qo_block_partials   golden vectors (bit-exact), brute force
+ *                                    fp64 sum of dequant(w)*dx*q on tiny K,
+ *                                    integer reduction with unit scales.
+ *   qo_gemm_multi                    task/row/residual semantics vs per-row
+ *                                    qo_dot_row, and vs the compiled
+ *                                    reference's dot functions.
+ *   qo_swiglu_q8k                    composition: h vs numpy fp64 SiLU*up
+ *                                    (tolerance; expf differs between libms),
+ *                                    codes vs qo_quantize_q8k_f32(h).
+ */
+#include "qmm_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- fp16 -- */
+
+/* (float)(__fp16)bits, E:592-596: exact widening. */
+float qo_fp16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    const uint32_t mant = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            /* subnormal: mant * 2^-24, exact in fp32 */
+            float v = (float)mant * 5.9604644775390625e-8f;
+            memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+/* (__fp16)f: IEEE binary32 -> binary16, round to nearest, ties to even. */
+uint16_t qo_f32_to_fp16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t abs = bits & 0x7fffffffu;
+    if (abs > 0x7f800000u) {                 /* NaN: keep it quiet */
+        return (uint16_t)(sign | 0x7e00u | ((abs >> 13) & 0x3ffu));
+    }
+    if (abs >= 0x477ff000u) {                /* >= 65520 rounds to inf */
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    const uint32_t exp = abs >> 23;
+    if (exp < 113) {                          /* below 2^-14: subnormal half */
+        if (exp < 102) return (uint16_t)sign; /* below 2^-25: rounds to 0 */
+        const uint32_t mant = (abs & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - exp;    /* units of 2^-24 */
+        uint32_t r = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((exp - 112u) << 10) | ((abs & 0x7fffffu) >> 13);
+    const uint32_t rem = abs & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+void qo_f32_to_fp16_array(const float *src, uint16_t *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = qo_f32_to_fp16(src[i]);
+}
+
+void qo_fp16_to_f32_array(const uint16_t *src, float *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = qo_fp16_to_f32(src[i]);
+}
+
+static inline uint16_t rd16(const uint8_t *p) {
+    uint16_t v;
+    memcpy(&v, p, 2);
+    return v;
+}
+
+/* ------------------------------------------------------------ formats -- */
+
+/* compute_ggml_bytes, E:364-374 */
+uint64_t qo_row_bytes(uint32_t type, uint64_t cols) {
+    switch (type) {
+        case QO_TYPE_F32: return cols * 4ull;
+        case QO_TYPE_F16: return cols * 2ull;
+        case QO_TYPE_Q8_0: return (cols / 32ull) * 34ull;
+        case QO_TYPE_Q4_K: return (cols / 256ull) * 144ull;
+        case QO_TYPE_Q5_K: return (cols / 256ull) * 176ull;
+        case QO_TYPE_Q6_K: return (cols / 256ull) * 210ull;
+        default: return 0;
+    }
+}
+
+/* get_scale_min_k4, E:743-749 */
+void qo_get_scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* ------------------------------------------------------------ dequant -- */
+
+/* dequant_block_q8_0, scalar branch E:613 */
+void qo_dequant_block_q8_0(const uint8_t *blk, uint16_t *dst) {
+    const float d = qo_fp16_to_f32(rd16(blk));
+    const int8_t *qs = (const int8_t *)(blk + 2);
+    for (int i = 0; i < 32; ++i) dst[i] = qo_f32_to_fp16(d * (float)qs[i]);
+}
+
+/* dequant_block_q6_k, scalar branch E:712-740 */
+void qo_dequant_block_q6_k(const uint8_t *blk, uint16_t *dst) {
+    const uint8_t *ql = blk;
+    const uint8_t *qh = blk + 128;
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    const float d = qo_fp16_to_f32(rd16(blk + 208));
+    for (int half = 0; half < 2; ++half) {
+        const uint8_t *ql_p = ql + half * 64;
+        const uint8_t *qh_p = qh + half * 32;
+        const int8_t *sc_p = sc + half * 8;
+        uint16_t *y = dst + half * 128;
+        for (int is = 0; is < 2; ++is) {
+            const float d_sc0 = d * (float)sc_p[is + 0];
+            const float d_sc2 = d * (float)sc_p[is + 2];
+            const float d_sc4 = d * (float)sc_p[is + 4];
+            const float d_sc6 = d * (float)sc_p[is + 6];
+            const int l_base = is * 16;
+            for (int l = l_base; l < l_base + 16; ++l) {
+                const uint8_t ql0 = ql_p[l], ql1 = ql_p[l + 32], qh0 = qh_p[l];
+                const int q1 = (int)((ql0 & 0x0F) | (((qh0 >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((ql1 & 0x0F) | (((qh0 >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql0 >> 4) | (((qh0 >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql1 >> 4) | (((qh0 >> 6) & 3) << 4)) - 32;
+                y[l + 0] = qo_f32_to_fp16(d_sc0 * (float)q1);
+                y[l + 32] = qo_f32_to_fp16(d_sc2 * (float)q2);
+                y[l + 64] = qo_f32_to_fp16(d_sc4 * (float)q3);
+                y[l + 96] = qo_f32_to_fp16(d_sc6 * (float)q4);
+            }
+        }
+    }
+}
+
+/* dequant_block_q4_k, scalar branch E:786-800 */
+void qo_dequant_block_q4_k(const uint8_t *blk, uint16_t *dst) {
+    const float d = qo_fp16_to_f32(rd16(blk));
+    const float min = qo_fp16_to_f32(rd16(blk + 2));
+    const uint8_t *scales = blk + 4;
+    const uint8_t *q = blk + 16;
+    int is = 0;
+    for (int j = 0; j < 256; j += 64) {
+        uint8_t sc, m;
+        qo_get_scale_min_k4(is + 0, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = min * (float)m;
+        qo_get_scale_min_k4(is + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = min * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t q_v = q[l];
+            dst[j + l] = qo_f32_to_fp16(d1 * (float)(q_v & 0x0F) - m1);
+            dst[j + 32 + l] = qo_f32_to_fp16(d2 * (float)(q_v >> 4) - m2);
+        }
+        q += 32;
+        is += 2;
+    }
+}
+
+/* dequant_block_q5_k, scalar branch E:837-852 */
+void qo_dequant_block_q5_k(const uint8_t *blk, uint16_t *dst) {
+    const float d = qo_fp16_to_f32(rd16(blk));
+    const float min = qo_fp16_to_f32(rd16(blk + 2));
+    const uint8_t *scales = blk + 4;
+    const uint8_t *qh = blk + 16;
+    const uint8_t *ql = blk + 48;
+    int is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < 256; j += 64) {
+        uint8_t sc, m;
+        qo_get_scale_min_k4(is + 0, scales, &sc, &m);
+        const float d1 = d * (float)sc, m1 = min * (float)m;
+        qo_get_scale_min_k4(is + 1, scales, &sc, &m);
+        const float d2 = d * (float)sc, m2 = min * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t ql_v = ql[l], qh_v = qh[l];
+            dst[j + l] = qo_f32_to_fp16(d1 * (float)((ql_v & 0x0F) + ((qh_v & u1) ? 16 : 0)) - m1);
+            dst[j + 32 + l] = qo_f32_to_fp16(d2 * (float)((ql_v >> 4) + ((qh_v & u2) ? 16 : 0)) - m2);
+        }
+        ql += 32;
+        is += 2;
+        u1 <<= 2;
+        u2 <<= 2;
+    }
+}
+
+/* dequant_contiguous_fast, E:3856-3902 (single-threaded here). */
+int qo_dequant_rows(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols,
+                    uint16_t *dst) {
+    const int64_t qk = (type == QO_TYPE_Q8_0) ? 32 : 256;
+    if (cols <= 0 || rows < 0 || cols % qk) return -1;
+    const uint64_t bbytes = qo_row_bytes(type, (uint64_t)qk);
+    if (bbytes == 0 || type == QO_TYPE_F32 || type == QO_TYPE_F16) return -1;
+    const int64_t units = rows * (cols / qk);
+    for (int64_t b = 0; b < units; ++b) {
+        const uint8_t *blk = src + (size_t)b * bbytes;
+        uint16_t *y = dst + (size_t)b * (size_t)qk;
+        switch (type) {
+            case QO_TYPE_Q8_0: qo_dequant_block_q8_0(blk, y); break;
+            case QO_TYPE_Q4_K: qo_dequant_block_q4_k(blk, y); break;
+            case QO_TYPE_Q5_K: qo_dequant_block_q5_k(blk, y); break;
+            case QO_TYPE_Q6_K: qo_dequant_block_q6_k(blk, y); break;
+        }
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------- quantizer -- */
+
+/* quantize_row_fp16_to_q8_k, scalar branches E:941-946 and E:976-988 */
+void qo_quantize_row_q8k_f16(const uint16_t *x, int k, float *d, int8_t *qs,
+                             int32_t *bsum32) {
+    const int nb = k / 256;
+    for (int b = 0; b < nb; ++b) {
+        const uint16_t *xb = x + (size_t)b * 256;
+        float max_abs = 0.0f;
+        for (int i = 0; i < 256; ++i) {
+            const float v = fabsf(qo_fp16_to_f32(xb[i]));
+            if (v > max_abs) max_abs = v;
+        }
+        int8_t *qb = qs + (size_t)b * 256;
+        int32_t *sb = bsum32 + (size_t)b * 8;
+        if (max_abs == 0.0f) {
+            d[b] = 0.0f;
+            memset(qb, 0, 256);
+            memset(sb, 0, 8 * sizeof(int32_t));
+            continue;
+        }
+        d[b] = max_abs / 127.0f;
+        const float id = 127.0f / max_abs;
+        for (int s = 0; s < 8; ++s) {
+            int32_t bsum = 0;
+            for (int l = 0; l < 32; ++l) {
+                int q = (int)lrintf(qo_fp16_to_f32(xb[s * 32 + l]) * id);
+                if (q > 127) q = 127;
+                if (q < -127) q = -127;
+                qb[s * 32 + l] = (int8_t)q;
+                bsum += q;
+            }
+            sb[s] = bsum;
+        }
+    }
+}
+
+/* quantize_row_fp16_to_q8_0, scalar branches E:1030-1035 and E:1056-1062 */
+void qo_quantize_row_q8_0_f16(const uint16_t *x, int k, float *d, int8_t *qs) {
+    const int nb = k / 32;
+    for (int b = 0; b < nb; ++b) {
+        const uint16_t *xb = x + (size_t)b * 32;
+        float max_abs = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float v = fabsf(qo_fp16_to_f32(xb[i]));
+            if (v > max_abs) max_abs = v;
+        }
+        int8_t *qb = qs + (size_t)b * 32;
+        if (max_abs == 0.0f) {
+            d[b] = 0.0f;
+            memset(qb, 0, 32);
+            continue;
+        }
+        d[b] = max_abs / 127.0f;
+        const float id = 127.0f / max_abs;
+        for (int l = 0; l < 32; ++l) {
+            int q = (int)lrintf(qo_fp16_to_f32(xb[l]) * id);
+            if (q > 127) q = 127;
+            if (q < -127) q = -127;
+            qb[l] = (int8_t)q;
+        }
+    }
+}
+
+void qo_quantize_q8k_f32(const float *x, int M, int K, float *d, int8_t *qs,
+                         int32_t *bsum32) {
+    uint16_t h[256];
+    const int nb = K / 256;
+    for (int m = 0; m < M; ++m) {
+        for (int b = 0; b < nb; ++b) {
+            const float *xb = x + (size_t)m * K + (size_t)b * 256;
+            qo_f32_to_fp16_array(xb, h, 256);
+            qo_quantize_row_q8k_f16(h, 256, d + (size_t)m * nb + b,
+                                    qs + (size_t)m * K + (size_t)b * 256,
+                                    bsum32 + ((size_t)m * nb + b) * 8);
+        }
+    }
+}
+
+void qo_quantize_q8_0_f32(const float *x, int M, int K, float *d, int8_t *qs) {
+    uint16_t h[32];
+    const int nb = K / 32;
+    for (int m = 0; m < M; ++m) {
+        for (int b = 0; b < nb; ++b) {
+            const float *xb = x + (size_t)m * K + (size_t)b * 32;
+            qo_f32_to_fp16_array(xb, h, 32);
+            qo_quantize_row_q8_0_f16(h, 32, d + (size_t)m * nb + b,
+                                     qs + (size_t)m * K + (size_t)b * 32);
+        }
+    }
+}
+
+/* --------------------------------------------------------------- dots -- */
+
+/* Integer partials of one 256-value Q4_K block (E:11009-11025). */
+static void q4k_block_int(const uint8_t *blk, const int8_t *q8, const int32_t *bs,
+                          int32_t *S_out, int32_t *Mb_out) {
+    const uint8_t *scales = blk + 4;
+    const uint8_t *q = blk + 16;
+    int32_t sum_sc_dot = 0, sum_m_bsum = 0;
+    int is = 0;
+    for (int j = 0; j < 256; j += 64) {
+        uint8_t sc0, m0, sc1, m1;
+        qo_get_scale_min_k4(is + 0, scales, &sc0, &m0);
+        qo_get_scale_min_k4(is + 1, scales, &sc1, &m1);
+        int32_t dot1 = 0, dot2 = 0;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t q_v = q[l];
+            dot1 += (int)(q_v & 0x0F) * (int32_t)q8[j + l];
+            dot2 += (int)(q_v >> 4) * (int32_t)q8[j + 32 + l];
+        }
+        sum_sc_dot += (int32_t)sc0 * dot1 + (int32_t)sc1 * dot2;
+        sum_m_bsum += (int32_t)m0 * bs[is + 0] + (int32_t)m1 * bs[is + 1];
+        q += 32;
+        is += 2;
+    }
+    *S_out = sum_sc_dot;
+    *Mb_out = sum_m_bsum;
+}
+
+/* Integer partials of one Q5_K block (E:11040-11062). */
+static void q5k_block_int(const uint8_t *blk, const int8_t *q8, const int32_t *bs,
+                          int32_t *S_out, int32_t *Mb_out) {
+    const uint8_t *scales = blk + 4;
+    const uint8_t *qh = blk + 16;
+    const uint8_t *ql_p = blk + 48;
+    int32_t sum_sc_dot = 0, sum_m_bsum = 0;
+    int is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < 256; j += 64) {
+        uint8_t sc0, m0, sc1, m1;
+        qo_get_scale_min_k4(is + 0, scales, &sc0, &m0);
+        qo_get_scale_min_k4(is + 1, scales, &sc1, &m1);
+        int32_t dot1 = 0, dot2 = 0;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t ql_v = ql_p[l], qh_v = qh[l];
+            const int q1 = (int)(ql_v & 0x0F) + ((qh_v & u1) ? 16 : 0);
+            const int q2 = (int)(ql_v >> 4) + ((qh_v & u2) ? 16 : 0);
+            dot1 += q1 * (int32_t)q8[j + l];
+            dot2 += q2 * (int32_t)q8[j + 32 + l];
+        }
+        sum_sc_dot += (int32_t)sc0 * dot1 + (int32_t)sc1 * dot2;
+        sum_m_bsum += (int32_t)m0 * bs[is + 0] + (int32_t)m1 * bs[is + 1];
+        ql_p += 32;
+        is += 2;
+        u1 <<= 2;
+        u2 <<= 2;
+    }
+    *S_out = sum_sc_dot;
+    *Mb_out = sum_m_bsum;
+}
+
+/* Integer partial of one Q6_K block (E:11075-11099). */
+static int32_t q6k_block_int(const uint8_t *blk, const int8_t *q8) {
+    const uint8_t *ql = blk;
+    const uint8_t *qh = blk + 128;
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    int32_t sum_sc_dot = 0;
+    for (int half = 0; half < 2; ++half) {
+        const uint8_t *ql_p = ql + half * 64;
+        const uint8_t *qh_p = qh + half * 32;
+        const int8_t *sc_p = sc + half * 8;
+        const int8_t *q8_p = q8 + half * 128;
+        for (int is = 0; is < 2; ++is) {
+            int32_t dot1 = 0, dot2 = 0, dot3 = 0, dot4 = 0;
+            const int l_base = is * 16;
+            for (int l = l_base; l < l_base + 16; ++l) {
+                const uint8_t ql0 = ql_p[l], ql1 = ql_p[l + 32], qh0 = qh_p[l];
+                const int q1 = (int)((ql0 & 0x0F) | (((qh0 >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((ql1 & 0x0F) | (((qh0 >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql0 >> 4) | (((qh0 >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql1 >> 4) | (((qh0 >> 6) & 3) << 4)) - 32;
+                dot1 += q1 * (int32_t)q8_p[l + 0];
+                dot2 += q2 * (int32_t)q8_p[l + 32];
+                dot3 += q3 * (int32_t)q8_p[l + 64];
+                dot4 += q4 * (int32_t)q8_p[l + 96];
+            }
+            sum_sc_dot += (int32_t)sc_p[is + 0] * dot1 + (int32_t)sc_p[is + 2] * dot2 +
+                          (int32_t)sc_p[is + 4] * dot3 + (int32_t)sc_p[is + 6] * dot4;
+        }
+    }
+    return sum_sc_dot;
+}
+
+/* Integer partial of one Q8_0 block (E:3400-3404). */
+static int32_t q80_block_int(const uint8_t *blk, const int8_t *qs_x) {
+    const int8_t *qs_w = (const int8_t *)(blk + 2);
+    int32_t dot = 0;
+    for (int i = 0; i < 32; ++i) dot += (int32_t)qs_w[i] * (int32_t)qs_x[i];
+    return dot;
+}
+
+float qo_dot_row(uint32_t type, const uint8_t *w_row, int K, const float *dx,
+                 const int8_t *qs, const int32_t *bsum32) {
+    float acc = 0.0f;
+    if (type == QO_TYPE_Q4_K || type == QO_TYPE_Q5_K) {
+        /* E:11026 / E:11063: acc += dx * (d * S - min * Mb) */
+        const int nb = K / 256;
+        const size_t bb = (type == QO_TYPE_Q4_K) ? 144 : 176;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = w_row + (size_t)b * bb;
+            const float d = qo_fp16_to_f32(rd16(blk));
+            const float min = qo_fp16_to_f32(rd16(blk + 2));
+            int32_t S, Mb;
+            if (type == QO_TYPE_Q4_K)
+                q4k_block_int(blk, qs + (size_t)b * 256, bsum32 + (size_t)b * 8, &S, &Mb);
+            else
+                q5k_block_int(blk, qs + (size_t)b * 256, bsum32 + (size_t)b * 8, &S, &Mb);
+            acc += dx[b] * (d * (float)S - min * (float)Mb);
+        }
+    } else if (type == QO_TYPE_Q6_K) {
+        /* E:11101: acc += (d * dx) * S */
+        const int nb = K / 256;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = w_row + (size_t)b * 210;
+            const float d = qo_fp16_to_f32(rd16(blk + 208));
+            const int32_t S = q6k_block_int(blk, qs + (size_t)b * 256);
+            acc += (d * dx[b]) * (float)S;
+        }
+    } else if (type == QO_TYPE_Q8_0) {
+        /* E:3405: out += (d * dx) * dot */
+        const int nb = K / 32;
+        for (int b = 0; b < nb; ++b) {
+            const uint8_t *blk = w_row + (size_t)b * 34;
+            const float d = qo_fp16_to_f32(rd16(blk));
+            const int32_t dot = q80_block_int(blk, qs + (size_t)b * 32);
+            acc += (d * dx[b]) * (float)dot;
+        }
+    } else {
+        return -1e30f; /* E:11104 */
+    }
+    return acc;
+}
+
+int qo_block_partials(uint32_t type, const uint8_t *w_row, int K, const int8_t *qs,
+                      const int32_t *bsum32, int32_t *S, int32_t *Mb) {
+    if (type == QO_TYPE_Q4_K || type == QO_TYPE_Q5_K) {
+        const int nb = K / 256;
+        const size_t bb = (type == QO_TYPE_Q4_K) ? 144 : 176;
+        for (int b = 0; b < nb; ++b) {
+            if (type == QO_TYPE_Q4_K)
+                q4k_block_int(w_row + b * bb, qs + (size_t)b * 256, bsum32 + (size_t)b * 8,
+                              &S[b], &Mb[b]);
+            else
+                q5k_block_int(w_row + b * bb, qs + (size_t)b * 256, bsum32 + (size_t)b * 8,
+                              &S[b], &Mb[b]);
+        }
+        return nb;
+    }
+    if (type == QO_TYPE_Q6_K) {
+        const int nb = K / 256;
+        for (int b = 0; b < nb; ++b) {
+            S[b] = q6k_block_int(w_row + (size_t)b * 210, qs + (size_t)b * 256);
+            Mb[b] = 0;
+        }
+        return nb;
+    }
+    if (type == QO_TYPE_Q8_0) {
+        const int nb = K / 32;
+        for (int b = 0; b < nb; ++b) {
+            S[b] = q80_block_int(w_row + (size_t)b * 34, qs + (size_t)b * 32);
+            Mb[b] = 0;
+        }
+        return nb;
+    }
+    return 0;
+}
+
+/* ----------------------------------------------------------- dispatch -- */
+
+static int is_kquant(uint32_t t) {
+    return t == QO_TYPE_Q4_K || t == QO_TYPE_Q5_K || t == QO_TYPE_Q6_K;
+}
+
+/* exec_sdot_job_work_stealing's row loop (E:3582-3613), fp32 store. */
+static void run_tasks(const float *q8k_d, const int8_t *q8k_qs, const int32_t *q8k_bsum,
+                      const float *q80_d, const int8_t *q80_qs, int M, int K,
+                      const qo_matrix_task *tasks, int n_tasks, int total_rows) {
+    const int nb256 = K / 256, nb32 = K / 32;
+#pragma omp parallel for schedule(dynamic, 64)
+    for (int r = 0; r < total_rows; ++r) {
+        int t = 0;
+        while (t < n_tasks && r >= tasks[t].start_row + tasks[t].rows) ++t;
+        const qo_matrix_task *T = &tasks[t];
+        const int lr = r - T->start_row;
+        const uint8_t *w_row = T->w_base + (size_t)lr * T->row_bytes;
+        for (int m = 0; m < M; ++m) {
+            float s;
+            if (T->type == QO_TYPE_Q8_0)
+                s = qo_dot_row(T->type, w_row, K, q80_d + (size_t)m * nb32,
+                               q80_qs + (size_t)m * K, NULL);
+            else
+                s = qo_dot_row(T->type, w_row, K, q8k_d + (size_t)m * nb256,
+                               q8k_qs + (size_t)m * K, q8k_bsum + (size_t)m * nb256 * 8);
+            if (T->residual) s = s + T->residual[(size_t)m * T->res_stride + lr];
+            T->dst[(size_t)m * T->dst_stride + lr] = s;
+        }
+    }
+}
+
+static int check_tasks(int M, int K, qo_matrix_task *tasks, int n_tasks, int *need_q8k,
+                       int *need_q80, int *total_rows) {
+    if (M <= 0 || K <= 0 || n_tasks <= 0 || !tasks) return -1;
+    int tr = 0;
+    *need_q8k = *need_q80 = 0;
+    for (int t = 0; t < n_tasks; ++t) {
+        if (tasks[t].cols != K) return -1;
+        if (is_kquant(tasks[t].type)) {
+            if (K % 256) return -1;
+            *need_q8k = 1;
+        } else if (tasks[t].type == QO_TYPE_Q8_0) {
+            if (K % 32) return -1;
+            *need_q80 = 1;
+        } else {
+            return -1;
+        }
+        tasks[t].start_row = tr; /* E:4196-4197 */
+        tr += tasks[t].rows;
+    }
+    *total_rows = tr;
+    return 0;
+}
+
+#include <stdlib.h>
+
+int qo_gemm_multi(const float *x, int M, int K, qo_matrix_task *tasks, int n_tasks) {
+    int need_q8k, need_q80, total_rows;
+    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &total_rows)) return -1;
+    float *kd = NULL, *zd = NULL;
+    int8_t *kq = NULL, *zq = NULL;
+    int32_t *ks = NULL;
+    if (need_q8k) {
+        kd = (float *)malloc(sizeof(float) * (size_t)M * (K / 256));
+        kq = (int8_t *)malloc((size_t)M * K);
+        ks = (int32_t *)malloc(sizeof(int32_t) * (size_t)M * (K / 32));
+        qo_quantize_q8k_f32(x, M, K, kd, kq, ks); /* E:4209-4215 */
+    }
+    if (need_q80) {
+        zd = (float *)malloc(sizeof(float) * (size_t)M * (K / 32));
+        zq = (int8_t *)malloc((size_t)M * K);
+        qo_quantize_q8_0_f32(x, M, K, zd, zq);
+    }
+    run_tasks(kd, kq, ks, zd, zq, M, K, tasks, n_tasks, total_rows);
+    free(kd); free(kq); free(ks); free(zd); free(zq);
+    return 0;
+}
+
+int qo_gemm_multi_prequantized(const float *q8k_d, const int8_t *q8k_qs,
+                               const int32_t *q8k_bsum, const float *q80_d,
+                               const int8_t *q80_qs, int M, int K,
+                               qo_matrix_task *tasks, int n_tasks) {
+    int need_q8k, need_q80, total_rows;
+    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &total_rows)) return -1;
+    if (need_q8k && (!q8k_d || !q8k_qs || !q8k_bsum)) return -1;
+    if (need_q80 && (!q80_d || !q80_qs)) return -1;
+    run_tasks(q8k_d, q8k_qs, q8k_bsum, q80_d, q80_qs, M, K, tasks, n_tasks, total_rows);
+    return 0;
+}
+
+/* ------------------------------------------------------------- swiglu -- */
+
+/* swiglu_chunk_worker scalar branch, E:4349-4356, then E:4357 requant. */
+void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
+                   float *d, int8_t *qs, int32_t *bsum32) {
+    float hb[256];
+    const int nb = N / 256;
+    for (int m = 0; m < M; ++m) {
+        for (int b = 0; b < nb; ++b) {
+            const size_t off = (size_t)m * N + (size_t)b * 256;
+            for (int i = 0; i < 256; ++i) {
+                const float g = gate[off + i];
+                const float u = up[off + i];
+                hb[i] = (g / (1.0f + expf(-g))) * u;
+            }
+            if (h) memcpy(h + off, hb, sizeof(hb));
+            qo_quantize_q8k_f32(hb, 1, 256, d + (size_t)m * nb + b, qs + off,
+                                bsum32 + ((size_t)m * nb + b) * 8);
+        }
+    }
+}

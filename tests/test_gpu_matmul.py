@@ -1,0 +1,144 @@
+"""HIP matmul kernels through the C ABI vs the oracle (the reference's
+scalar path restated): GEMV (M = 1), MFMA small-M and prefill GEMMs, all four
+weight formats, the multi-task dispatcher, residuals, prequantized inputs."""
+import numpy as np
+import pytest
+
+import qmm_hip
+import synth
+from gpu_util import check_outputs, say
+from oracle import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0
+
+pytestmark = pytest.mark.gpu
+NAMES = {TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K", TYPE_Q6_K: "Q6_K", TYPE_Q8_0: "Q8_0"}
+
+
+def _run(ctx, oracle, type_id, N, K, M, seed, residual=False):
+    say(f"{NAMES[type_id]} N={N} K={K} M={M} residual={residual}")
+    w = synth.weights(type_id, N, K, seed=seed)
+    x = synth.activations(M, K, seed=seed + 1)
+    res = synth.activations(M, N, seed=seed + 2) if residual else None
+    wb = ctx.weight_upload(w, type_id, N, K)
+    y = ctx.gemm(type_id, wb, N, K, x, res)
+    ctx.free(wb)
+    task = dict(w=w, type=type_id, rows=N)
+    if res is not None:
+        task["residual"] = res
+    ref = oracle.gemm_multi(x, [task])[0]
+    check_outputs(y, ref, f"{NAMES[type_id]} N={N} K={K} M={M}")
+
+
+# ------------------------------------------------------------------ M = 1
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
+@pytest.mark.parametrize("N,K", [(1, 256), (7, 512), (64, 2560), (1001, 2560)])
+def test_gemv_small_shapes(ctx, oracle, type_id, N, K):
+    _run(ctx, oracle, type_id, N, K, 1, seed=N + K + type_id)
+
+
+def test_gemv_q4k_decode_shape(ctx, oracle):
+    _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, 1, seed=1000)
+
+
+def test_gemv_q6k_lm_head_shape(ctx, oracle):
+    _run(ctx, oracle, TYPE_Q6_K, 151936, 2560, 1, seed=1001)
+
+
+@pytest.mark.parametrize("type_id,N,K", [(TYPE_Q6_K, 2560, 9728), (TYPE_Q5_K, 4096, 2560),
+                                         (TYPE_Q8_0, 2560, 2560), (TYPE_Q4_K, 2560, 4096)])
+def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
+    _run(ctx, oracle, type_id, N, K, 1, seed=N + type_id)
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K])
+def test_gemv_residual(ctx, oracle, type_id):
+    _run(ctx, oracle, type_id, 300, 2560, 1, seed=5, residual=True)
+
+
+# ------------------------------------------------------------- M >= 2 MFMA
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
+@pytest.mark.parametrize("M", [2, 5, 16, 17, 40, 64])
+def test_mfma_small_shapes(ctx, oracle, type_id, M):
+    _run(ctx, oracle, type_id, 77, 512, M, seed=M * 13 + type_id)
+
+
+@pytest.mark.parametrize("M", [8, 16, 32, 64])
+def test_tree_verify_q4k(ctx, oracle, M):
+    _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
+
+
+def test_tree_verify_q5k_qkv(ctx, oracle):
+    _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, 64, seed=2100)
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K])
+def test_mfma_residual(ctx, oracle, type_id):
+    _run(ctx, oracle, type_id, 200, 2560, 9, seed=7, residual=True)
+
+
+@pytest.mark.parametrize("name", ["qkv", "o", "gate", "down", "q8_0"])
+def test_prefill_m512_row_subsets(ctx, oracle, name):
+    """Full prefill tensors at M = 512 on the GPU; the oracle checks the first
+    and last 128 rows (a full check of 512 x 9728 x 2560 on the CPU is slow)."""
+    type_id, N, K = synth.PREFILL_LAYER["tensors"][name]
+    M = 512
+    say(f"prefill {name} {NAMES[type_id]} N={N} K={K} M={M}")
+    w = synth.weights(type_id, N, K, seed=3000 + N)
+    x = synth.activations(M, K, seed=3001)
+    wb = ctx.weight_upload(w, type_id, N, K)
+    y = ctx.gemm(type_id, wb, N, K, x)
+    ctx.free(wb)
+    rb = synth.row_bytes(type_id, K)
+    for r0 in (0, N - 128):
+        ref = oracle.gemm_multi(x, [dict(w=w[r0 * rb:(r0 + 128) * rb], type=type_id, rows=128)])[0]
+        check_outputs(y[:, r0:r0 + 128], ref, f"prefill {name} rows {r0}..{r0 + 128}")
+
+
+# ---------------------------------------------------------------- dispatch
+@pytest.mark.parametrize("M", [1, 6])
+def test_multi_task_dispatch_mixed_types(ctx, oracle, M):
+    """Four tasks sharing one input (the E:7959 / E:8114 call pattern), one
+    with a residual, with Q8_K and Q8_0 activations both needed."""
+    K = 2560
+    say(f"multi-task dispatch M={M}")
+    specs = [(TYPE_Q4_K, 300), (TYPE_Q5_K, 64), (TYPE_Q6_K, 32), (TYPE_Q8_0, 96)]
+    x = synth.activations(M, K, seed=9)
+    ws = [synth.weights(t, n, K, seed=40 + i) for i, (t, n) in enumerate(specs)]
+    res = synth.activations(M, 64, seed=11)
+    xb = ctx.upload(x)
+    wbs = [ctx.weight_upload(w, t, n, K) for w, (t, n) in zip(ws, specs)]
+    ybs = [ctx.malloc(M * n * 4) for _, n in specs]
+    rb = ctx.upload(res)
+    tasks = [qmm_hip.MatrixTask(wb, t, n, K, yb, n, rb if i == 1 else None, n)
+             for i, (wb, yb, (t, n)) in enumerate(zip(wbs, ybs, specs))]
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    assert [t.start_row for t in tasks] == [0, 300, 364, 396]
+    refs = oracle.gemm_multi(x, [dict(w=w, type=t, rows=n, **({"residual": res} if i == 1 else {}))
+                                 for i, (w, (t, n)) in enumerate(zip(ws, specs))])
+    for i, ((t, n), yb) in enumerate(zip(specs, ybs)):
+        check_outputs(ctx.d2h(yb, np.float32, (M, n)), refs[i], f"task {i}")
+    for b in [xb, rb] + wbs + ybs:
+        ctx.free(b)
+
+
+def test_prequantized_dispatch_and_strides(ctx, oracle):
+    """Oracle-quantized Q8_K activations fed to the prequantized entry point;
+    the output written with a row stride wider than the task."""
+    M, K, N, ld = 3, 2560, 100, 130
+    say("prequantized dispatch")
+    x = synth.activations(M, K, seed=12)
+    w = synth.weights(TYPE_Q4_K, N, K, seed=13)
+    d, qs, bs = oracle.quantize_q8k(x)
+    qb = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.write_q8k(qb, d, qs, bs)
+    wb = ctx.weight_upload(w, TYPE_Q4_K, N, K)
+    yb = ctx.malloc(M * ld * 4)
+    ctx.h2d(yb, np.full((M, ld), 7.0, np.float32))
+    ctx.gemm_multi_dispatch_prequantized(qb, None, M, K, [qmm_hip.MatrixTask(wb, TYPE_Q4_K, N, K, yb, ld)])
+    ctx.sync()
+    y = ctx.d2h(yb, np.float32, (M, ld))
+    ref = oracle.gemm_multi(x, [dict(w=w, type=TYPE_Q4_K, rows=N)], prequantized=((d, qs, bs), None))[0]
+    check_outputs(y[:, :N], ref, "prequantized")
+    assert np.all(y[:, N:] == 7.0)  # nothing written past the task's rows
+    for b in (qb, wb, yb):
+        ctx.free(b)
