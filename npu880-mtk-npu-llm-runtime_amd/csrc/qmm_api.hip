@@ -102,6 +102,8 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
             if (!aligned(T.w_base, wa)) return fail(ctx, QMM_EALIGN, "task " + std::to_string(t) + ": weight base misaligned for its format");
             if (!aligned(T.dst, 4) || (T.residual && !aligned(T.residual, 4))) return fail(ctx, QMM_EALIGN, "task " + std::to_string(t) + ": dst/residual not 4-B aligned");
         }
+        if (M == 1 && qmm::gemv_lds_bytes(T.type, K) > 65536)
+            return fail(ctx, QMM_ESHAPE, "task " + std::to_string(t) + ": K too large for the batch-1 kernel");
         if (T.type == qmm::kQ8_0) *need_q80 = true;
         else *need_q8k = true;
         T.start_row = total;  // E:4196-4197
@@ -110,7 +112,8 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
     return QMM_OK;
 }
 
-int run_tasks(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
+// x32 != nullptr (M = 1 only): the GEMV kernels quantize x themselves.
+int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q80, int M, int K,
               const qmm_matrix_task *tasks, int n_tasks) {
     qmm::Q8KView xk{nullptr, nullptr, nullptr};
     qmm::Q80View x0{nullptr, nullptr};
@@ -138,7 +141,7 @@ int run_tasks(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
         a.ldy = M > 1 ? T.dst_stride : size_t(T.rows);
         a.res = T.residual;
         a.ldr = M > 1 ? T.res_stride : size_t(T.rows);
-        const hipError_t e = (M == 1) ? qmm::launch_gemv(T.type, a, xk, x0, ctx->stream)
+        const hipError_t e = (M == 1) ? qmm::launch_gemv(T.type, a, x32, xk, x0, ctx->stream)
                                       : qmm::launch_mfma(T.type, a, xk, x0, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
@@ -380,6 +383,7 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
     if (rc) return rc;
     if (!aligned(x, 16)) return fail(ctx, QMM_EALIGN, "x must be 16-B aligned");
     if ((rc = use_device(ctx))) return rc;
+    if (M == 1) return run_tasks(ctx, x, nullptr, nullptr, M, K, tasks, n_tasks);
     const size_t k_bytes = need_q8k ? qmm::Q8KLayout(M, K).total : 0;
     const size_t z_bytes = need_q80 ? qmm::Q80Layout(M, K).total : 0;
     if ((rc = ensure_act(ctx, k_bytes + z_bytes))) return rc;
@@ -390,7 +394,7 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
         return hip_fail(ctx, e, "quantize_q8k launch");
     if (need_q80 && (e = qmm::launch_quantize_q8_0(x, M, K, q80, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "quantize_q8_0 launch");
-    return run_tasks(ctx, q8k, q80, M, K, tasks, n_tasks);
+    return run_tasks(ctx, nullptr, q8k, q80, M, K, tasks, n_tasks);
 }
 
 int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80, int M,
@@ -404,7 +408,8 @@ int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, cons
     if ((q8k && !aligned(q8k, 16)) || (q80 && !aligned(q80, 16)))
         return fail(ctx, QMM_EALIGN, "activation buffers must be 16-B aligned");
     if ((rc = use_device(ctx))) return rc;
-    return run_tasks(ctx, need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, M, K, tasks, n_tasks);
+    return run_tasks(ctx, nullptr, need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, M, K, tasks,
+                     n_tasks);
 }
 
 int qmm_graph_begin(qmm_context *ctx) {

@@ -47,6 +47,15 @@ struct Q80View {
     const float *d;    // [M][K/32]
 };
 
+// LDS-resident activation row of the GEMV: codes padded by 16 B per 256
+// values (lds_pad), d per block, bsum32 per 32 values (Q8_K only).
+struct LdsAct {
+    const int8_t *qs;
+    const float *d;
+    const int32_t *bs;
+};
+__host__ __device__ inline int lds_pad(int v) { return v + ((v >> 8) << 4); }
+
 // One matmul launch: a task after validation.
 struct MatArgs {
     const uint8_t *w;  // packed rows
@@ -67,8 +76,12 @@ hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, f
                              void *out, hipStream_t s);
 hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
                               uint16_t *dst, hipStream_t s);
-hipError_t launch_gemv(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
-                       hipStream_t s);
+// M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;
+// otherwise xk / x0 hold the prequantized row.
+hipError_t launch_gemv(uint32_t type, const MatArgs &a, const float *x32, const Q8KView &xk,
+                       const Q80View &x0, hipStream_t s);
+// dynamic LDS bytes the GEMV needs for K (must stay <= 64 KiB)
+size_t gemv_lds_bytes(uint32_t type, int K);
 hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s);
 
@@ -111,25 +124,81 @@ __device__ inline int group8_sum(int v) {
 }
 
 // --------------------------------------------------------- global loads
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 // 16 B load of an address that is 16-B aligned.
 __device__ inline uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+// streaming (non-temporal) 16 B load: weights are read exactly once
+__device__ inline uint4 ld16_nt(const void *p) {
+    const v4u32 v = __builtin_nontemporal_load(reinterpret_cast<const v4u32 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// accesses (not its outstanding global loads) before s_barrier.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ inline uint2 ld8(const void *p) { return *reinterpret_cast<const uint2 *>(p); }
 // 8 bytes starting at a 2-B aligned address: the aligned dwords that hold
 // them, then a funnel shift by the misalignment. Every dword read contains
 // at least one requested byte, so the read never leaves the pages of the
 // requested range.
+// (The aligned address is formed by pointer arithmetic on p, not through an
+// integer, so the compiler keeps the global address space: global_load, not
+// flat_load.)
 __device__ inline uint2 ld8_a2(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[sh ? 2 : 1];
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1);
+    const uint32_t w2 = __builtin_nontemporal_load(q + (sh ? 2 : 1));
     return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
 }
 // the 16-bit value at a 2-B aligned address
 __device__ inline uint32_t ld16b_a2(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
-    return (w >> ((a & 2) * 8)) & 0xFFFFu;
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p - sh));
+    return (w >> (sh * 8)) & 0xFFFFu;
+}
+
+// ------------------------------------------------------ Q8 quantization
+// Quantize the 4 fp16-rounded values a lane owns given the block's max |x|
+// (quantize_row_fp16_to_q8_k E:947-988): id = 127 / amax (correctly rounded),
+// q = rint(x * id) (round to nearest even, as lrintf in the default mode),
+// clamp to [-127, 127]. Returns the packed int8 codes and their sum.
+__device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
+    if (amax == 0.0f) {  // E:947-952
+        sum = 0;
+        return 0u;
+    }
+    const float id = 127.0f / amax;  // E:954
+    int q[4];
+    const float h[4] = {h0, h1, h2, h3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int v = (int)rintf(h[i] * id);  // E:979
+        v = v > 127 ? 127 : v;
+        v = v < -127 ? -127 : v;
+        q[i] = v;
+    }
+    sum = q[0] + q[1] + q[2] + q[3];
+    return (uint32_t(q[0]) & 0xFFu) | ((uint32_t(q[1]) & 0xFFu) << 8) |
+           ((uint32_t(q[2]) & 0xFFu) << 16) | ((uint32_t(q[3]) & 0xFFu) << 24);
+}
+// d = amax / 127 (E:953), 0 for an all-zero block
+__device__ inline float q8_scale(float amax) { return amax == 0.0f ? 0.0f : amax / 127.0f; }
+
+__device__ inline float wave_max(float a) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
+    return a;
+}
+__device__ inline float group8_max(float a) {
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    return a;
 }
 
 // get_scale_min_k4 (E:743-749) for sub-block j given the 12 scale bytes

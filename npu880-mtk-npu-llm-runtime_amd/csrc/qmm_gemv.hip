@@ -1,20 +1,60 @@
 // qmm_gemv.hip — batch-1 (M = 1) GEMV over GGUF-packed rows, gfx950.
 //
 // Work mapping. A wavefront owns R consecutive weight rows; since rows are
-// contiguous, its R * nb blocks form one contiguous byte span. Lanes are
-// grouped G per block (SLOTS = 64 / G blocks in flight per wave step); each
-// lane streams its share of a block straight from HBM (16-B loads for the
-// 16-B aligned Q4_K / Q5_K blocks, realigned dword loads for the 2-B aligned
-// Q6_K / Q8_0 blocks), unpacks the codes in registers, and forms int32 dot
-// partials with v_dot4_i32_i8. The per-block integer partials (S, Mb) are
-// summed over the G lanes with DPP — exact and order free — and the block's
-// fp32 term is evaluated once with the reference's expression. Block terms
-// go to LDS; one lane per row then adds them in block order, the order of
+// contiguous, its R * nb blocks form one contiguous byte span, processed in
+// wave steps of SLOTS = 64 / G blocks (G lanes per block). Each lane unpacks
+// its share of a block in registers and forms int32 dot partials with
+// v_dot4_i32_i8; the per-block integer partials (S, Mb) are summed over the
+// G lanes with DPP — exact and order free — and the block's fp32 term is
+// evaluated once with the reference's expression. Block terms go to LDS;
+// one lane per row then adds them in block order, the order of
 // eval_single_lm_row_dot (E:10986-11105), so the result equals the
 // reference's fp32 sum bit for bit.
+//
+// Weight bytes. Q4_K / Q5_K blocks (144 / 176 B) are 16-B aligned: lanes
+// load their pieces straight from HBM with 16-B loads. Q6_K / Q8_0 blocks
+// (210 / 34 B) are only 2-B aligned: the wave loads the contiguous bytes of
+// U wave steps with 16-B loads into an LDS stage and lanes read their
+// pieces from there (two-byte realignment costs LDS reads, not HBM
+// transactions).
+//
+// Activations live in LDS for the whole workgroup. The fp32 input (or the
+// prequantized row) is requested first, then the first batch of weights;
+// while those are in flight the workgroup quantizes the input to Q8_K /
+// Q8_0 itself — 16 lanes per 256 values, DPP reductions, the reference's
+// exact arithmetic — so one launch covers quantize + GEMV. Codes are stored
+// with 16 B of padding per 256 values so lanes on consecutive blocks hit
+// different banks. Vector-memory counters retire in order, so the fill
+// waits only for the input loads; the workgroup barrier orders LDS only.
 #include "qmm_device.h"
 
 namespace qmm {
+
+// ------------------------------------------------------------ DPP on fp32
+template <int CTRL>
+__device__ inline float dppf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// max over each 16-lane row (all 16 lanes active): xor1, xor2, half-mirror, mirror
+__device__ inline float row16_max(float v) {
+    v = fmaxf(v, dppf<0xB1>(v));
+    v = fmaxf(v, dppf<0x4E>(v));
+    v = fmaxf(v, dppf<0x141>(v));
+    v = fmaxf(v, dppf<0x140>(v));
+    return v;
+}
+
+// LDS reads at 2-B aligned offsets (stage of 2-B aligned blocks)
+__device__ inline uint2 lds8_a2(const uint8_t *p) {
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[sh ? 2 : 1];
+    return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
+}
+__device__ inline uint32_t lds16b_a2(const uint8_t *p) {
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    return (*reinterpret_cast<const uint32_t *>(p - sh) >> (sh * 8)) & 0xFFFFu;
+}
 
 // ----------------------------------------------------------------- Q4_K
 // Block (144 B): d f16 @0, dmin f16 @2, scales[12] @4, codes[128] @16.
@@ -23,15 +63,16 @@ namespace qmm {
 // (sub-block 2j), high nibbles = 64j + 32 + 16lh + (0..15) (sub-block 2j+1).
 struct FmtQ4K {
     static constexpr int G = 8, BB = 144, QK = 256;
+    static constexpr bool kStaged = false;
     struct Raw { uint4 h, c; };
     struct Act { uint4 xl, xh; uint2 bs; float dx; };
     __device__ static Raw load(const uint8_t *blk, int k) {
-        return {ld16(blk), ld16(blk + 16 + 16 * k)};
+        return {ld16_nt(blk), ld16_nt(blk + 16 + 16 * k)};
     }
-    __device__ static Act load_act(const Q8KView &x, int b, int k) {
+    __device__ static Act load_act(const LdsAct &x, int b, int k) {
         const int j = k >> 1, lh = k & 1;
-        const int8_t *xb = x.qs + size_t(b) * 256 + 64 * j + 16 * lh;
-        return {ld16(xb), ld16(xb + 32), ld8(x.bs + size_t(b) * 8 + 2 * j), x.d[b]};
+        const int8_t *xb = x.qs + b * 272 + 64 * j + 16 * lh;
+        return {ld16(xb), ld16(xb + 32), ld8(x.bs + b * 8 + 2 * j), x.d[b]};
     }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
         const int j = k >> 1, lh = k & 1;
@@ -64,13 +105,14 @@ struct FmtQ4K {
 // of value 64j + 32 + l bit 2j+1.
 struct FmtQ5K {
     static constexpr int G = 8, BB = 176, QK = 256;
+    static constexpr bool kStaged = false;
     struct Raw { uint4 h, qh, ql; };
     using Act = FmtQ4K::Act;
     __device__ static Raw load(const uint8_t *blk, int k) {
         const int j = k >> 1, lh = k & 1;
-        return {ld16(blk), ld16(blk + 16 + 16 * lh), ld16(blk + 48 + 32 * j + 16 * lh)};
+        return {ld16_nt(blk), ld16_nt(blk + 16 + 16 * lh), ld16_nt(blk + 48 + 32 * j + 16 * lh)};
     }
-    __device__ static Act load_act(const Q8KView &x, int b, int k) { return FmtQ4K::load_act(x, b, k); }
+    __device__ static Act load_act(const LdsAct &x, int b, int k) { return FmtQ4K::load_act(x, b, k); }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
         const int j = k >> 1, lh = k & 1;
         int sc0, m0, sc1, m1;
@@ -104,26 +146,25 @@ struct FmtQ5K {
 // Block (210 B, 2-B aligned): ql[128] @0, qh[64] @128, int8 sc[16] @192,
 // d f16 @208. Lane k: half hf = k/4, l0 = 8 * (k%4), is = (k%4)/2. For
 // l in [l0, l0+8): values 128hf + 32i + l (i = 0..3) with scale
-// sc[8hf + is + 2i] (E:712-740 / E:11075-11099).
+// sc[8hf + is + 2i] (E:712-740 / E:11075-11099). Read from the LDS stage.
 struct FmtQ6K {
     static constexpr int G = 8, BB = 210, QK = 256;
+    static constexpr bool kStaged = true;
     struct Raw { uint2 a, b, h, s; uint32_t d; };
     struct Act { uint2 x[4]; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) {
+    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into LDS
         const int hf = k >> 2, l0 = 8 * (k & 3);
         Raw r;
-        r.a = ld8_a2(blk + 64 * hf + l0);
-        r.b = ld8_a2(blk + 64 * hf + 32 + l0);
-        r.h = ld8_a2(blk + 128 + 32 * hf + l0);
-        // the 8 scale bytes of this half, sc[8hf .. 8hf+7]; the lane uses
-        // bytes is + {0, 2, 4, 6}
-        r.s = ld8_a2(blk + 192 + 8 * hf);
-        r.d = ld16b_a2(blk + 208);
+        r.a = lds8_a2(blk + 64 * hf + l0);
+        r.b = lds8_a2(blk + 64 * hf + 32 + l0);
+        r.h = lds8_a2(blk + 128 + 32 * hf + l0);
+        r.s = lds8_a2(blk + 192 + 8 * hf);  // sc[8hf .. 8hf+7]
+        r.d = lds16b_a2(blk + 208);
         return r;
     }
-    __device__ static Act load_act(const Q8KView &x, int b, int k) {
+    __device__ static Act load_act(const LdsAct &x, int b, int k) {
         const int hf = k >> 2, l0 = 8 * (k & 3);
-        const int8_t *xb = x.qs + size_t(b) * 256 + 128 * hf + l0;
+        const int8_t *xb = x.qs + b * 272 + 128 * hf + l0;
         return {{ld8(xb), ld8(xb + 32), ld8(xb + 64), ld8(xb + 96)}, x.d[b]};
     }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
@@ -159,14 +200,15 @@ struct FmtQ6K {
 
 // ----------------------------------------------------------------- Q8_0
 // Block (34 B, 2-B aligned): d f16 @0, int8 qs[32] @2. Lane k of 4: values
-// [8k, 8k+8). Activations are Q8_0 (E:3394-3406).
+// [8k, 8k+8). Activations are Q8_0 (E:3394-3406). Read from the LDS stage.
 struct FmtQ80 {
     static constexpr int G = 4, BB = 34, QK = 32;
+    static constexpr bool kStaged = true;
     struct Raw { uint2 q; uint32_t d; };
     struct Act { uint2 x; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) { return {ld8_a2(blk + 2 + 8 * k), ld16b_a2(blk)}; }
-    __device__ static Act load_act(const Q80View &x, int b, int k) {
-        return {ld8(x.qs + size_t(b) * 32 + 8 * k), x.d[b]};
+    __device__ static Raw load(const uint8_t *blk, int k) { return {lds8_a2(blk + 2 + 8 * k), lds16b_a2(blk)}; }
+    __device__ static Act load_act(const LdsAct &x, int b, int k) {
+        return {ld8(x.qs + lds_pad(b * 32 + 8 * k)), x.d[b]};
     }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
         (void)k;
@@ -178,45 +220,246 @@ struct FmtQ80 {
     }
 };
 
-template <class F> struct XViewOf { using T = Q8KView; };
-template <> struct XViewOf<FmtQ80> { using T = Q80View; };
+template <class F> struct IsQ80 { static constexpr bool v = false; };
+template <> struct IsQ80<FmtQ80> { static constexpr bool v = true; };
 
-// R rows per wave, U wave steps of SLOTS blocks loaded ahead of use.
+// ------------------------------------------------------ activation fill
+// 16 lanes per 256-value chunk: lane sub of row r in wave w handles values
+// 16 * sub .. +16 of chunk c = 16 * round + 4w + r. Round 0 is loaded before
+// the weights are requested.
+struct XPre { float4 v[4]; };
+
+__device__ inline int x_chunk(int round, int K) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int nc = (K + 255) >> 8;
+    return min(16 * round + 4 * wid + (lane >> 4), nc - 1);
+}
+// clamped to the last 16 values of x for a partial last Q8_0 chunk; such
+// lanes' results are never stored
+__device__ inline void x_load(const float *__restrict__ x, int K, int c, XPre &p) {
+    const int v0 = min(c * 256 + 16 * int(threadIdx.x & 15), K - 16);
+    const float4 *q = reinterpret_cast<const float4 *>(x + v0);
+    p.v[0] = q[0];
+    p.v[1] = q[1];
+    p.v[2] = q[2];
+    p.v[3] = q[3];
+}
+
+// Quantize the lane's 16 values of chunk c into the LDS row: Q8_K
+// (quantize_row_fp16_to_q8_k, E:925-990) or Q8_0 (E:1016-1064), after
+// rounding each value to fp16. `store` is false for clamped duplicates.
+template <bool Q80>
+__device__ inline void x_quant(const XPre &p, int c, int K, bool store, const LdsAct &a) {
+    const int sub = threadIdx.x & 15;
+    float h[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[4 * i + 0] = round_to_fp16(p.v[i].x);
+        h[4 * i + 1] = round_to_fp16(p.v[i].y);
+        h[4 * i + 2] = round_to_fp16(p.v[i].z);
+        h[4 * i + 3] = round_to_fp16(p.v[i].w);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(h[i]));
+    // block max: 256 values = the 16-lane row; 32 values (Q8_0) = a lane pair
+    const float amax = Q80 ? fmaxf(m, dppf<0xB1>(m)) : row16_max(m);
+    int s0, s1, s2, s3;
+    uint4 q;
+    q.x = quant4(h[0], h[1], h[2], h[3], amax, s0);
+    q.y = quant4(h[4], h[5], h[6], h[7], amax, s1);
+    q.z = quant4(h[8], h[9], h[10], h[11], amax, s2);
+    q.w = quant4(h[12], h[13], h[14], h[15], amax, s3);
+    int sum = s0 + s1 + s2 + s3;
+    sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);  // the 32-value pair
+    const int v0 = c * 256 + 16 * sub;
+    store = store && v0 < K;
+    if (store) {
+        *reinterpret_cast<uint4 *>(const_cast<int8_t *>(a.qs) + lds_pad(v0)) = q;
+        if ((sub & 1) == 0) {
+            if constexpr (Q80) {
+                const_cast<float *>(a.d)[v0 >> 5] = q8_scale(amax);
+            } else {
+                const_cast<int32_t *>(a.bs)[v0 >> 5] = sum;
+                if (sub == 0) const_cast<float *>(a.d)[c] = q8_scale(amax);
+            }
+        }
+    }
+}
+
+template <bool Q80>
+__device__ inline void x_fill(const XPre &p0, const float *__restrict__ x, int K, const LdsAct &a) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int nc = (K + 255) >> 8;
+    x_quant<Q80>(p0, x_chunk(0, K), K, 4 * wid + (lane >> 4) < nc, a);
+    for (int round = 1; 16 * round < nc; ++round) {
+        XPre p;
+        const int c = x_chunk(round, K);
+        x_load(x, K, c, p);
+        x_quant<Q80>(p, c, K, 16 * round + 4 * wid + (lane >> 4) < nc, a);
+    }
+}
+
+// Prequantized row: 16-B code chunks, scales and bsum32 per thread.
+struct CPre { uint4 q[4]; int32_t bs[2]; float d[2]; };
+
+template <bool Q80>
+__device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t *bs, int K, CPre &p) {
+    const int t = threadIdx.x;
+    const int nq = K >> 4, nd = Q80 ? (K >> 5) : (K >> 8);
+    // clamped indices: every load is issued (duplicates are never stored)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.q[i] = ld16(qs + 16 * min(t + 256 * i, nq - 1));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if constexpr (!Q80) p.bs[i] = bs[min(t + 256 * i, (K >> 5) - 1)];
+        p.d[i] = d[min(t + 256 * i, nd - 1)];
+    }
+}
+
+template <bool Q80>
+__device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d, const int32_t *bs,
+                                 int K, const LdsAct &a) {
+    const int t = threadIdx.x;
+    const int nq = K >> 4, nd = Q80 ? (K >> 5) : (K >> 8), nbs = Q80 ? 0 : (K >> 5);
+    int8_t *lq = const_cast<int8_t *>(a.qs);
+    float *ld = const_cast<float *>(a.d);
+    int32_t *lb = const_cast<int32_t *>(a.bs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (t + 256 * i < nq) *reinterpret_cast<uint4 *>(lq + lds_pad(16 * (t + 256 * i))) = p.q[i];
+    for (int i = t + 1024; i < nq; i += 256)
+        *reinterpret_cast<uint4 *>(lq + lds_pad(16 * i)) = ld16(qs + 16 * i);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (t + 256 * i < nbs) lb[t + 256 * i] = p.bs[i];
+        if (t + 256 * i < nd) ld[t + 256 * i] = p.d[i];
+    }
+    for (int i = t + 512; i < nbs; i += 256) lb[i] = bs[i];
+    for (int i = t + 512; i < nd; i += 256) ld[i] = d[i];
+}
+
+// ------------------------------------------------------------ the kernel
+constexpr int kGemvR = 4, kGemvU = 5;
+
+// LDS carve-up: padded codes | d | bsum32 (Q8_K only) | per-wave block
+// terms | per-wave weight stage (staged formats)
+__host__ __device__ inline size_t gemv_act_lds_bytes(bool q80, int K) {
+    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
+    const size_t nd = q80 ? size_t(K / 32) : size_t(K / 256);
+    const size_t nbs = q80 ? 0 : size_t(K / 32);
+    return (codes + 4 * nd + 4 * nbs + 15) & ~size_t(15);
+}
+template <class F, int U>
+__host__ __device__ constexpr int stage_chunks() {  // 16-B loads per lane per batch
+    return F::kStaged ? ((64 / F::G) * U * F::BB + 16 + 1023) / 1024 : 0;
+}
 template <class F, int R, int U>
-__global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, typename XViewOf<F>::T x) {
-    extern __shared__ float contrib_all[];
-    constexpr int G = F::G, SLOTS = 64 / G;
+__host__ __device__ inline size_t gemv_lds_bytes_t(int K) {
+    const size_t terms = (size_t(4) * R * (K / F::QK) * sizeof(float) + 15) & ~size_t(15);
+    return gemv_act_lds_bytes(IsQ80<F>::v, K) + terms + size_t(4) * stage_chunks<F, U>() * 1024;
+}
+
+// R rows per wave, U wave steps of SLOTS blocks per batch.
+// FUSED: x32 is quantized in the kernel; otherwise prek / pre0 hold the
+// prequantized activation row.
+template <class F, int R, int U, bool FUSED>
+__global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, const float *__restrict__ x32,
+                                                   Q8KView prek, Q80View pre0) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
+    constexpr bool q80 = IsQ80<F>::v;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / G, k = lane % G;
-    const int nb = a.K / F::QK;
+    const int K = a.K;
+    const int nb = K / F::QK;
     const int row0 = (int(blockIdx.x) * 4 + wid) * R;
     const int nrows = max(0, min(R, a.N - row0));
     const int nblk = nrows * nb;
-    float *contrib = contrib_all + wid * R * nb;
-    const uint8_t *span = a.w + size_t(max(row0, 0)) * a.row_bytes;
+    // waves past the last row still issue (discarded) loads of row 0 so the
+    // load sequence has no branches
+    const uint8_t *span = a.w + size_t(nrows > 0 ? row0 : 0) * a.row_bytes;
+    const int flast = max(nblk, 1) - 1;
 
-    for (int t0 = 0; t0 < nblk; t0 += SLOTS * U) {
-        typename F::Raw raw[U];
-        typename F::Act act[U];
+    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
+    LdsAct act;
+    act.qs = reinterpret_cast<const int8_t *>(lds);
+    act.d = reinterpret_cast<const float *>(lds + codes);
+    act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
+    const size_t act_bytes = gemv_act_lds_bytes(q80, K);
+    const size_t terms_bytes = (size_t(4) * R * nb * sizeof(float) + 15) & ~size_t(15);
+    float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * R * nb;
+    uint8_t *stage = lds + act_bytes + terms_bytes + size_t(wid) * NST * 1024;
+
+    const int8_t *pq = q80 ? pre0.qs : prek.qs;
+    const float *pd = q80 ? pre0.d : prek.d;
+    const int32_t *pb = prek.bs;
+
+    // Staged formats: the bytes of blocks [t0, t0 + SLOTS*U) of the span, from
+    // the 16-B boundary at or below their start; chunk indices are clamped so
+    // that every lane issues its loads (duplicates rewrite identical bytes).
+    const int span_mis = int(reinterpret_cast<uintptr_t>(span) & 15);
+    uint4 st[NST > 0 ? NST : 1];
+    auto stage_load = [&](int t0) {
+        const int nb_batch = max(min(SLOTS * U, nblk - t0), 1);
+        const uint8_t *base = span + size_t(t0) * F::BB - span_mis;
+        const int nchunks = (span_mis + nb_batch * F::BB + 15) >> 4;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int f = t0 + u * SLOTS + g;
-            if (f < nblk) {
-                raw[u] = F::load(span + size_t(f) * F::BB, k);
-                act[u] = F::load_act(x, f % nb, k);
+        for (int j = 0; j < NST; ++j) st[j] = ld16_nt(base + 16 * min(64 * j + lane, nchunks - 1));
+    };
+    auto stage_store = [&]() {
+#pragma unroll
+        for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+    };
+
+    // 1. the activation row into registers
+    XPre xp;
+    CPre cp;
+    if constexpr (FUSED) x_load(x32, K, x_chunk(0, K), xp);
+    else cpre_load<q80>(pq, pd, pb, K, cp);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first in issue order
+    // 2. weights of the first batch
+    typename F::Raw raw[U];
+    if constexpr (F::kStaged) {
+        stage_load(0);
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = F::load(span + size_t(min(u * SLOTS + g, flast)) * F::BB, k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. activations into LDS while the weights are in flight
+    if constexpr (FUSED) x_fill<q80>(xp, x32, K, act);
+    else cpre_fill<q80>(cp, pq, pd, pb, K, act);
+    if constexpr (F::kStaged) stage_store();
+    lds_barrier();
+    // 4. block terms
+    for (int t0 = 0; t0 < nblk; t0 += SLOTS * U) {
+        if (t0 > 0) {
+            if constexpr (F::kStaged) {
+                stage_load(t0);
+                // all lanes of this wave are done reading the previous batch
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+                stage_store();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
             } else {
-                raw[u] = typename F::Raw{};
-                act[u] = typename F::Act{};
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    raw[u] = F::load(span + size_t(min(t0 + u * SLOTS + g, flast)) * F::BB, k);
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int f = t0 + u * SLOTS + g;
-            const float c = F::compute(raw[u], act[u], k);
+            const int b = f - (f / nb) * nb;
+            typename F::Raw r;
+            if constexpr (F::kStaged) r = F::load(stage + span_mis + (u * SLOTS + g) * F::BB, k);
+            else r = raw[u];
+            const float c = F::compute(r, F::load_act(act, f < nblk ? b : 0, k), k);
             if (k == 0 && f < nblk) contrib[f] = c;
         }
     }
-    __syncthreads();
+    lds_barrier();
+    // 5. per row, blocks in order (eval_single_lm_row_dot's accumulation)
     if (lane < nrows) {
         float acc = 0.0f;
         const float *cr = contrib + lane * nb;
@@ -227,23 +470,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, typename XViewOf<F
     }
 }
 
+size_t gemv_lds_bytes(uint32_t type, int K) {
+    switch (type) {
+        case kQ4_K: return gemv_lds_bytes_t<FmtQ4K, kGemvR, kGemvU>(K);
+        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, kGemvR, kGemvU>(K);
+        case kQ6_K: return gemv_lds_bytes_t<FmtQ6K, kGemvR, kGemvU>(K);
+        case kQ8_0: return gemv_lds_bytes_t<FmtQ80, kGemvR, kGemvU>(K);
+        default: return 0;
+    }
+}
+
 template <class F, int R, int U>
-static hipError_t launch_gemv_t(const MatArgs &a, const typename XViewOf<F>::T &x, hipStream_t s) {
-    const int nb = a.K / F::QK;
+static hipError_t launch_gemv_t(const MatArgs &a, const float *x32, const Q8KView &xk,
+                                const Q80View &x0, hipStream_t s) {
     const int waves = (a.N + R - 1) / R;
     const unsigned grid = unsigned((waves + 3) / 4);
-    const size_t lds = size_t(4) * R * nb * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<F, R, U>), dim3(grid), dim3(256), lds, s, a, x);
+    const size_t lds = gemv_lds_bytes_t<F, R, U>(a.K);
+    if (x32)
+        hipLaunchKernelGGL((gemv_kernel<F, R, U, true>), dim3(grid), dim3(256), lds, s, a, x32, xk, x0);
+    else
+        hipLaunchKernelGGL((gemv_kernel<F, R, U, false>), dim3(grid), dim3(256), lds, s, a, x32, xk, x0);
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
-                       hipStream_t s) {
+hipError_t launch_gemv(uint32_t type, const MatArgs &a, const float *x32, const Q8KView &xk,
+                       const Q80View &x0, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_gemv_t<FmtQ4K, 4, 5>(a, xk, s);
-        case kQ5_K: return launch_gemv_t<FmtQ5K, 4, 5>(a, xk, s);
-        case kQ6_K: return launch_gemv_t<FmtQ6K, 4, 5>(a, xk, s);
-        case kQ8_0: return launch_gemv_t<FmtQ80, 4, 5>(a, x0, s);
+        case kQ4_K: return launch_gemv_t<FmtQ4K, kGemvR, kGemvU>(a, x32, xk, x0, s);
+        case kQ5_K: return launch_gemv_t<FmtQ5K, kGemvR, kGemvU>(a, x32, xk, x0, s);
+        case kQ6_K: return launch_gemv_t<FmtQ6K, kGemvR, kGemvU>(a, x32, xk, x0, s);
+        case kQ8_0: return launch_gemv_t<FmtQ80, kGemvR, kGemvU>(a, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

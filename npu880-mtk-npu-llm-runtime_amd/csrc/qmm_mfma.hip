@@ -161,10 +161,23 @@ __device__ inline void decode_scales(const typename F::W &w, Scales<F> &s) {
     }
 }
 
+__device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
+    const long av = (long)(((uint64_t)a.y << 32) | a.x);
+    const long bv = (long)(((uint64_t)b.y << 32) | b.x);
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, c, 0, 0, 0);
+}
+
 // TT token tiles of 16 per wave; 4 waves per workgroup on consecutive
 // 16-row tiles; grid.y walks token groups of 16 * TT.
+//
+// Per block and token tile: NU MFMAs give the unit dots D_u; S = sum sc_u *
+// D_u on the VALU (exact int32). For the formats with mins the min term
+// Mb = sum_j m_j * bsum32_j is itself an int8 contraction — sum_k x_k *
+// m_{unit(k)} — so it runs on the MFMA unit as one accumulating chain over
+// the units with a B operand of broadcast 6-bit mins (exact, no bsum reads).
 template <class F, int TT>
 __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>::T x) {
+    constexpr bool kPrefetchA = (TT == 1);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int nl = lane & 15, c = lane >> 4;
     const int n0 = (int(blockIdx.x) * 4 + wid) * 16;
@@ -181,48 +194,79 @@ __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>:
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
+    // A-operand rows of this lane (token m0 + 16t + nl), zero past M
+    const int8_t *xa_row[TT];
+    bool okA[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        const int tokA = m0 + 16 * t + nl;
+        okA[t] = tokA < a.M;
+        xa_row[t] = x.qs + size_t(okA[t] ? tokA : 0) * a.K;
+    }
+    auto load_a = [&](int b, int t, uint2 (&dst)[F::NU]) {
+#pragma unroll
+        for (int u = 0; u < F::NU; ++u)
+            dst[u] = okA[t] ? ld8(xa_row[t] + size_t(b) * F::QK + F::koff(u, c)) : make_uint2(0u, 0u);
+    };
+
     typename F::W wcur = F::load(wrow, c);
+    uint2 acur[F::NU];
+    if constexpr (kPrefetchA) load_a(0, 0, acur);
     for (int b = 0; b < nb; ++b) {
         typename F::W wnext;
-        if (b + 1 < nb) wnext = F::load(wrow + size_t(b + 1) * F::BB, c);
+        uint2 anext[F::NU];
+        if (b + 1 < nb) {
+            wnext = F::load(wrow + size_t(b + 1) * F::BB, c);
+            if constexpr (kPrefetchA) load_a(b + 1, 0, anext);
+        }
+        // dx of the lane's output tokens 16t + 4c + r for this block
+        float dx[TT][4];
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = m0 + 16 * t + 4 * c + r;
+                dx[t][r] = tok < a.M ? x.d[size_t(tok) * nb + b] : 0.0f;
+            }
         Scales<F> s;
         decode_scales<F>(wcur, s);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
-            const int tokA = m0 + 16 * t + nl;  // A-operand token of this lane
-            const bool okA = tokA < a.M;
-            const int8_t *xa = x.qs + size_t(okA ? tokA : 0) * a.K + size_t(b) * F::QK;
+            uint2 av[F::NU];
+            if constexpr (kPrefetchA) {
+#pragma unroll
+                for (int u = 0; u < F::NU; ++u) av[u] = acur[u];
+            } else {
+                load_a(b, t, av);
+            }
             int S[4] = {0, 0, 0, 0};
+            int4v Mb = {0, 0, 0, 0};
 #pragma unroll
             for (int u = 0; u < F::NU; ++u) {
-                const uint2 av = okA ? ld8(xa + F::koff(u, c)) : make_uint2(0u, 0u);
-                const int4v D = mfma16x16x32(av, F::bop(wcur, u, c));
+                const int4v D = mfma16x16x32(av[u], F::bop(wcur, u, c));
+                if constexpr (F::kMin) {
+                    const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
+                    Mb = mfma16x16x32_acc(av[u], make_uint2(mb, mb), Mb);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int tok = m0 + 16 * t + 4 * c + r;  // output token of D[r]
-                if (tok >= a.M) continue;
                 if constexpr (F::kMin) {
-                    // E:11024-11026: Mb = sum m_j * bsum32_j; acc += dx * (d*S - dmin*Mb)
-                    const int32_t *bs = x.bs + (size_t(tok) * nb + b) * 8;
-                    const uint4 b0 = ld16(bs), b1 = ld16(bs + 4);
-                    const int bsv[8] = {int(b0.x), int(b0.y), int(b0.z), int(b0.w),
-                                        int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
-                    int Mb = 0;
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) Mb += __mul24(s.m[u], bsv[u]);
-                    const float dx = x.d[size_t(tok) * nb + b];
-                    acc[t][r] += dx * (s.d * (float)S[r] - s.dmin * (float)Mb);
+                    // E:11026: acc += dx * (d * S - dmin * Mb)
+                    acc[t][r] += dx[t][r] * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);
                 } else {
                     // E:11101 / E:3405: acc += (d * dx) * S
-                    const float dx = x.d[size_t(tok) * nb + b];
-                    acc[t][r] += (s.d * dx) * (float)S[r];
+                    acc[t][r] += (s.d * dx[t][r]) * (float)S[r];
                 }
             }
         }
         wcur = wnext;
+        if constexpr (kPrefetchA) {
+#pragma unroll
+            for (int u = 0; u < F::NU; ++u) acur[u] = anext[u];
+        }
     }
     if (n >= a.N) return;
 #pragma unroll
@@ -247,8 +291,7 @@ static hipError_t launch_mfma_t(const MatArgs &a, const typename ActOf<F>::T &x,
 
 template <class F>
 static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    if (a.M <= 16) return launch_mfma_t<F, 1>(a, x, s);
-    if (a.M <= 32) return launch_mfma_t<F, 2>(a, x, s);
+    if (a.M <= 64) return launch_mfma_t<F, 1>(a, x, s);
     return launch_mfma_t<F, 4>(a, x, s);
 }
 

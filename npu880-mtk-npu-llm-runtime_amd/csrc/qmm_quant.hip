@@ -10,34 +10,6 @@
 
 namespace qmm {
 
-// Quantize the 4 values a lane owns; returns packed int8 codes, writes the
-// code sum. `amax` is the block's max |x| (already reduced).
-__device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
-    if (amax == 0.0f) {  // E:947-952
-        sum = 0;
-        return 0u;
-    }
-    const float id = 127.0f / amax;  // E:954
-    int q[4];
-    const float h[4] = {h0, h1, h2, h3};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int v = (int)rintf(h[i] * id);  // E:979
-        v = v > 127 ? 127 : v;
-        v = v < -127 ? -127 : v;
-        q[i] = v;
-    }
-    sum = q[0] + q[1] + q[2] + q[3];
-    return (uint32_t(q[0]) & 0xFFu) | ((uint32_t(q[1]) & 0xFFu) << 8) |
-           ((uint32_t(q[2]) & 0xFFu) << 16) | ((uint32_t(q[3]) & 0xFFu) << 24);
-}
-
-__device__ inline float wave_max(float a) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off));
-    return a;
-}
-
 // Quantize one fp16-rounded 256-value block held 4 values per lane and
 // store it as Q8_K block `blk` (flattened over [M][K/256]).
 __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
@@ -49,7 +21,7 @@ __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, i
     reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
     sum = group8_sum(sum);  // bsum32 over 32 values = 8 lanes
     if ((lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
-    if (lane == 0) d[blk] = (a == 0.0f) ? 0.0f : a / 127.0f;  // E:953
+    if (lane == 0) d[blk] = q8_scale(a);  // E:953
 }
 
 // x [M][K] fp32, flattened 256-blocks; one wave per block.
@@ -79,13 +51,11 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     const float h0 = round_to_fp16(v.x), h1 = round_to_fp16(v.y);
     const float h2 = round_to_fp16(v.z), h3 = round_to_fp16(v.w);
     float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
-    a = fmaxf(a, __shfl_xor(a, 1));
-    a = fmaxf(a, __shfl_xor(a, 2));
-    a = fmaxf(a, __shfl_xor(a, 4));
+    a = group8_max(a);
     int sum;
     const uint32_t packed = quant4(h0, h1, h2, h3, a, sum);
     reinterpret_cast<uint32_t *>(qs + blk * 32)[sub] = packed;
-    if (sub == 0) d[blk] = (a == 0.0f) ? 0.0f : a / 127.0f;
+    if (sub == 0) d[blk] = q8_scale(a);
 }
 
 // swiglu_chunk_worker (E:4349-4357) on fp32 gate/up: h = (g / (1 + expf(-g))) * u,
