@@ -167,34 +167,38 @@ __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, c, 0, 0, 0);
 }
 
-// TT token tiles of 16 per wave; 4 waves per workgroup on consecutive
-// 16-row tiles; grid.y walks token groups of 16 * TT.
+// Workgroup = 16 weight rows x 16*TT tokens; its 4 waves split the K
+// blocks (wave w takes blocks w, w+4, ...), each wave keeping PF of its
+// blocks' weight bytes in flight. Per group of 4 consecutive blocks every
+// wave writes its block's fp32 terms to LDS, and after a barrier each
+// output's owner thread adds the 4 terms in block order — the sequential
+// accumulation of the reference, so outputs stay bit-identical while the
+// K loop runs 4 waves wide.
 //
 // Per block and token tile: NU MFMAs give the unit dots D_u; S = sum sc_u *
 // D_u on the VALU (exact int32). For the formats with mins the min term
 // Mb = sum_j m_j * bsum32_j is itself an int8 contraction — sum_k x_k *
 // m_{unit(k)} — so it runs on the MFMA unit as one accumulating chain over
 // the units with a B operand of broadcast 6-bit mins (exact, no bsum reads).
-template <class F, int TT>
+template <class F, int TT> struct ActBlock {
+    uint2 a[TT][F::NU];  // A operands, per token tile and unit
+    float dx[TT][4];     // activation scales of the lane's output tokens
+};
+
+template <class F, int TT, int PF, int PA>
 __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>::T x) {
-    constexpr bool kPrefetchA = (TT == 1);
+    __shared__ float part[4][16 * TT * 16];  // [wave][token * 16 + row]
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int nl = lane & 15, c = lane >> 4;
-    const int n0 = (int(blockIdx.x) * 4 + wid) * 16;
-    if (n0 >= a.N) return;
+    const int n0 = int(blockIdx.x) * 16;
     const int m0 = int(blockIdx.y) * 16 * TT;
-    const int n = n0 + nl;
-    const int nload = min(n, a.N - 1);
+    const int nload = min(n0 + nl, a.N - 1);
     const int nb = a.K / F::QK;
+    const int ngroups = (nb + 3) / 4;
     const uint8_t *wrow = a.w + size_t(nload) * a.row_bytes;
 
-    float acc[TT][4];
-#pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
-
-    // A-operand rows of this lane (token m0 + 16t + nl), zero past M
+    // A-operand rows of this lane (token m0 + 16t + nl), zero past M; output
+    // tokens m0 + 16t + 4c + r for the activation scales
     const int8_t *xa_row[TT];
     bool okA[TT];
 #pragma unroll
@@ -203,96 +207,107 @@ __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>:
         okA[t] = tokA < a.M;
         xa_row[t] = x.qs + size_t(okA[t] ? tokA : 0) * a.K;
     }
-    auto load_a = [&](int b, int t, uint2 (&dst)[F::NU]) {
+    auto load_act = [&](int b, ActBlock<F, TT> &ab) {
+        const int bl = min(b, nb - 1);
 #pragma unroll
-        for (int u = 0; u < F::NU; ++u)
-            dst[u] = okA[t] ? ld8(xa_row[t] + size_t(b) * F::QK + F::koff(u, c)) : make_uint2(0u, 0u);
-    };
-
-    typename F::W wcur = F::load(wrow, c);
-    uint2 acur[F::NU];
-    if constexpr (kPrefetchA) load_a(0, 0, acur);
-    for (int b = 0; b < nb; ++b) {
-        typename F::W wnext;
-        uint2 anext[F::NU];
-        if (b + 1 < nb) {
-            wnext = F::load(wrow + size_t(b + 1) * F::BB, c);
-            if constexpr (kPrefetchA) load_a(b + 1, 0, anext);
-        }
-        // dx of the lane's output tokens 16t + 4c + r for this block
-        float dx[TT][4];
+        for (int t = 0; t < TT; ++t) {
 #pragma unroll
-        for (int t = 0; t < TT; ++t)
+            for (int u = 0; u < F::NU; ++u)
+                ab.a[t][u] = okA[t] ? ld8(xa_row[t] + size_t(bl) * F::QK + F::koff(u, c)) : make_uint2(0u, 0u);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int tok = m0 + 16 * t + 4 * c + r;
-                dx[t][r] = tok < a.M ? x.d[size_t(tok) * nb + b] : 0.0f;
+                ab.dx[t][r] = x.d[size_t(min(tok, a.M - 1)) * nb + bl];
             }
-        Scales<F> s;
-        decode_scales<F>(wcur, s);
+        }
+    };
+
+    // weights (PF deep) and activations (PA deep) of this wave's blocks
+    // b = wid + 4i, clamped to the last block (never stored past nb)
+    typename F::W wq[PF];
+    ActBlock<F, TT> aq[PA];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            uint2 av[F::NU];
-            if constexpr (kPrefetchA) {
+    for (int i = 0; i < PF; ++i) wq[i] = F::load(wrow + size_t(min(wid + 4 * i, nb - 1)) * F::BB, c);
 #pragma unroll
-                for (int u = 0; u < F::NU; ++u) av[u] = acur[u];
-            } else {
-                load_a(b, t, av);
-            }
-            int S[4] = {0, 0, 0, 0};
-            int4v Mb = {0, 0, 0, 0};
+    for (int i = 0; i < PA; ++i) load_act(wid + 4 * i, aq[i]);
+
+    float acc[TT];
 #pragma unroll
-            for (int u = 0; u < F::NU; ++u) {
-                const int4v D = mfma16x16x32(av[u], F::bop(wcur, u, c));
-                if constexpr (F::kMin) {
-                    const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
-                    Mb = mfma16x16x32_acc(av[u], make_uint2(mb, mb), Mb);
+    for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
+
+    for (int grp = 0; grp < ngroups; ++grp) {
+        const int b = 4 * grp + wid;
+        const typename F::W wcur = wq[0];
+        const ActBlock<F, TT> acur = aq[0];
+#pragma unroll
+        for (int i = 0; i + 1 < PF; ++i) wq[i] = wq[i + 1];
+        wq[PF - 1] = F::load(wrow + size_t(min(b + 4 * PF, nb - 1)) * F::BB, c);
+#pragma unroll
+        for (int i = 0; i + 1 < PA; ++i) aq[i] = aq[i + 1];
+        load_act(b + 4 * PA, aq[PA - 1]);
+        if (b < nb) {
+            Scales<F> s;
+            decode_scales<F>(wcur, s);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                int S[4] = {0, 0, 0, 0};
+                int4v Mb = {0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < F::NU; ++u) {
+                    const int4v D = mfma16x16x32(acur.a[t][u], F::bop(wcur, u, c));
+                    if constexpr (F::kMin) {
+                        const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
+                        Mb = mfma16x16x32_acc(acur.a[t][u], make_uint2(mb, mb), Mb);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
                 }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if constexpr (F::kMin) {
-                    // E:11026: acc += dx * (d * S - dmin * Mb)
-                    acc[t][r] += dx[t][r] * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);
-                } else {
-                    // E:11101 / E:3405: acc += (d * dx) * S
-                    acc[t][r] += (s.d * dx[t][r]) * (float)S[r];
+                for (int r = 0; r < 4; ++r) {
+                    const float dx = acur.dx[t][r];
+                    float v;
+                    if constexpr (F::kMin) v = dx * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);  // E:11026
+                    else v = (s.d * dx) * (float)S[r];                                            // E:11101 / E:3405
+                    part[wid][(16 * t + 4 * c + r) * 16 + nl] = v;
                 }
             }
         }
-        wcur = wnext;
-        if constexpr (kPrefetchA) {
+        lds_barrier();
+        // blocks 4grp .. 4grp+3 in order
 #pragma unroll
-            for (int u = 0; u < F::NU; ++u) acur[u] = anext[u];
+        for (int j = 0; j < TT; ++j) {
+            const int o = int(threadIdx.x) + 256 * j;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                if (4 * grp + w < nb) acc[j] += part[w][o];
         }
+        lds_barrier();
     }
-    if (n >= a.N) return;
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = m0 + 16 * t + 4 * c + r;
-            if (tok >= a.M) continue;
-            float v = acc[t][r];
+    for (int j = 0; j < TT; ++j) {
+        const int o = int(threadIdx.x) + 256 * j;
+        const int tok = m0 + (o >> 4), n = n0 + (o & 15);
+        if (tok < a.M && n < a.N) {
+            float v = acc[j];
             if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
             a.y[size_t(tok) * a.ldy + n] = v;
         }
+    }
 }
 
-template <class F, int TT>
+template <class F, int TT, int PF, int PA>
 static hipError_t launch_mfma_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    const int tiles = (a.N + 15) / 16;
-    const dim3 grid(unsigned((tiles + 3) / 4), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
-    hipLaunchKernelGGL((mfma_kernel<F, TT>), grid, dim3(256), 0, s, a, x);
+    const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
+    hipLaunchKernelGGL((mfma_kernel<F, TT, PF, PA>), grid, dim3(256), 0, s, a, x);
     return hipGetLastError();
 }
 
 template <class F>
 static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    if (a.M <= 64) return launch_mfma_t<F, 1>(a, x, s);
-    return launch_mfma_t<F, 4>(a, x, s);
+    // large M: 4 token tiles per wave (2 for Q6_K, whose 16 units would spill)
+    constexpr int kTT = F::NU > 8 ? 2 : 4;
+    if (a.M <= 64) return launch_mfma_t<F, 1, 3, 1>(a, x, s);
+    return launch_mfma_t<F, kTT, 1, 1>(a, x, s);
 }
 
 hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
