@@ -44,18 +44,6 @@ __device__ inline float row16_max(float v) {
     return v;
 }
 
-// LDS reads at 2-B aligned offsets (stage of 2-B aligned blocks)
-__device__ inline uint2 lds8_a2(const uint8_t *p) {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[sh ? 2 : 1];
-    return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
-}
-__device__ inline uint32_t lds16b_a2(const uint8_t *p) {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
-    return (*reinterpret_cast<const uint32_t *>(p - sh) >> (sh * 8)) & 0xFFFFu;
-}
-
 // ----------------------------------------------------------------- Q4_K
 // Block (144 B): d f16 @0, dmin f16 @2, scales[12] @4, codes[128] @16.
 // Lane k of 8: chunk j = k/2 (64 values), half lh = k%2 -> code bytes

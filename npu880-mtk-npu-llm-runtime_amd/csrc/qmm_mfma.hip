@@ -45,6 +45,7 @@ struct MQ4K {
         for (int j = 0; j < 4; ++j) w.q[j] = ld8(blk + 16 + 32 * j + 8 * c);
         return w;
     }
+    __device__ static W load_lds(const uint8_t *blk, int c) { return load(blk, c); }
     __device__ static int koff(int u, int c) { return 64 * (u >> 1) + 32 * (u & 1) + 8 * c; }
     __device__ static uint2 bop(const W &w, int u, int c) {
         (void)c;
@@ -67,6 +68,7 @@ struct MQ5K {
         for (int j = 0; j < 4; ++j) w.q[j] = ld8(blk + 48 + 32 * j + 8 * c);
         return w;
     }
+    __device__ static W load_lds(const uint8_t *blk, int c) { return load(blk, c); }
     __device__ static int koff(int u, int c) { return MQ4K::koff(u, c); }
     __device__ static uint2 bop(const W &w, int u, int c) {
         (void)c;
@@ -101,6 +103,23 @@ struct MQ6K {
         w.d = ld16b_a2(blk + 208);
         return w;
     }
+    __device__ static W load_lds(const uint8_t *blk, int c) {
+        W w;
+        const int c2 = c & 1;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int is = 0; is < 2; ++is) {
+                const int p = 2 * hf + is, l = 16 * is + 8 * c2;
+                w.a[p] = lds8_a2(blk + 64 * hf + l);
+                w.b[p] = lds8_a2(blk + 64 * hf + 32 + l);
+                w.qh[p] = lds8_a2(blk + 128 + 32 * hf + l);
+            }
+        w.s0 = lds8_a2(blk + 192);
+        w.s1 = lds8_a2(blk + 200);
+        w.d = lds16b_a2(blk + 208);
+        return w;
+    }
     __device__ static int koff(int u, int c) {
         return 128 * (u >> 3) + 32 * ((u >> 1) & 3) + 16 * (u & 1) + 8 * (c & 1);
     }
@@ -128,6 +147,7 @@ struct MQ80 {
     static constexpr bool kMin = false;
     struct W { uint2 q; uint32_t d; };
     __device__ static W load(const uint8_t *blk, int c) { return {ld8_a2(blk + 2 + 8 * c), ld16b_a2(blk)}; }
+    __device__ static W load_lds(const uint8_t *blk, int c) { return {lds8_a2(blk + 2 + 8 * c), lds16b_a2(blk)}; }
     __device__ static int koff(int u, int c) { (void)u; return 8 * c; }
     __device__ static uint2 bop(const W &w, int u, int c) { (void)u; (void)c; return w.q; }
 };
@@ -295,6 +315,190 @@ __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>:
     }
 }
 
+// ---------------------------------------------------------------- small M
+// Workgroup = one 16-row tile x all M <= 64 tokens (TT = ceil(M / 16)
+// tiles). K is processed in chunks of KCB blocks. For each chunk the
+// workgroup loads the 16 weight-row segments (KCB * BB contiguous bytes
+// each) and the token segments (KCB * QK bytes each) with coalesced 16-B
+// loads — one chunk ahead, into registers — and stores them to LDS; the 4
+// waves share the chunk's (block, token tile) items, read their MFMA
+// operands from LDS and write each block's fp32 terms to LDS, where every
+// output's owner thread adds them in block order (bit-identical to the
+// reference's sequential accumulation).
+template <class F, int TT>
+struct SmallM {
+    static constexpr int TM = 16 * TT;
+    // blocks per chunk: about 48 KiB of LDS per workgroup
+    static constexpr int per_block = 16 * F::BB + TM * F::QK + TM * 4 + TM * 64;
+    static constexpr int KCB0 = (48 * 1024) / per_block;
+    static constexpr int KCB = KCB0 < 1 ? 1 : (KCB0 > 32 ? 32 : KCB0);
+    static constexpr int WSEG = KCB * F::BB;           // weight bytes per row per chunk
+    static constexpr int WCR = (WSEG + 30) / 16;       // 16-B loads per row, any alignment
+    static constexpr int WS = WCR * 16 + 16;           // LDS row stride
+    static constexpr int ASEG = KCB * F::QK;           // activation bytes per token per chunk
+    static constexpr int ACR = ASEG / 16;
+    static constexpr int AS = ASEG + 16;               // LDS token stride
+    static constexpr int NW = (16 * WCR + 255) / 256;  // loads per thread
+    static constexpr int NA = (TM * ACR + 255) / 256;
+    static constexpr int ND = (TM * KCB + 255) / 256;
+    static constexpr int OFF_A = 16 * WS;
+    static constexpr int OFF_D = OFF_A + TM * AS;
+    static constexpr int OFF_P = OFF_D + ((TM * KCB * 4 + 15) & ~15);
+    static constexpr int LDS = OFF_P + KCB * TM * 16 * 4;
+};
+
+template <class F, int TT>
+__global__ __launch_bounds__(256) void mfma_small_kernel(MatArgs a, typename ActOf<F>::T x) {
+    using C = SmallM<F, TT>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *lw = lds;
+    int8_t *la = reinterpret_cast<int8_t *>(lds + C::OFF_A);
+    float *ld = reinterpret_cast<float *>(lds + C::OFF_D);
+    float *part = reinterpret_cast<float *>(lds + C::OFF_P);
+    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    const int nl = lane & 15, cl = lane >> 4;
+    const int n0 = int(blockIdx.x) * 16;
+    const int K = a.K, nb = K / F::QK;
+    const int nchunks = (nb + C::KCB - 1) / C::KCB;
+
+    uint4 rw[C::NW], ra[C::NA];
+    float rd[C::ND];
+    // chunk ch: weight bytes [ch*KCB*BB, +WSEG) of rows n0..n0+15 (clamped
+    // to the last row), token bytes [ch*KCB*QK, +ASEG) of tokens 0..TM-1
+    // (clamped to the last token); load indices past the valid bytes repeat
+    // the last valid 16 B, which is stored to the same place.
+    auto w_src = [&](int ch, int idx, int &dst) -> const uint8_t * {
+        const int row = min(idx / C::WCR, 15), piece = idx - row * C::WCR;
+        const size_t off = size_t(ch) * C::KCB * F::BB;
+        const uint8_t *rp = a.w + size_t(min(n0 + row, a.N - 1)) * a.row_bytes + off;
+        const int mis = int(reinterpret_cast<uintptr_t>(rp) & 15);
+        const int nbytes = int(min(size_t(C::WSEG), a.row_bytes - off));
+        const int pc = min(piece, (mis + nbytes + 15) / 16 - 1);
+        dst = row * C::WS + 16 * pc;
+        return rp - mis + 16 * pc;
+    };
+    auto a_src = [&](int ch, int idx, int &dst) -> const int8_t * {
+        const int tok = min(idx / C::ACR, C::TM - 1), piece = idx - tok * C::ACR;
+        const int off = ch * C::ASEG;
+        const int pc = min(piece, min(C::ASEG, K - off) / 16 - 1);
+        dst = tok * C::AS + 16 * pc;
+        return x.qs + size_t(min(tok, a.M - 1)) * K + off + 16 * pc;
+    };
+    auto load_chunk = [&](int ch) {
+        int dummy;
+#pragma unroll
+        for (int i = 0; i < C::NW; ++i) rw[i] = ld16_nt(w_src(ch, min(t + 256 * i, 16 * C::WCR - 1), dummy));
+#pragma unroll
+        for (int i = 0; i < C::NA; ++i) ra[i] = ld16(a_src(ch, min(t + 256 * i, C::TM * C::ACR - 1), dummy));
+#pragma unroll
+        for (int i = 0; i < C::ND; ++i) {
+            const int idx = min(t + 256 * i, C::TM * C::KCB - 1);
+            const int tok = idx / C::KCB, j = idx - tok * C::KCB;
+            rd[i] = x.d[size_t(min(tok, a.M - 1)) * nb + min(ch * C::KCB + j, nb - 1)];
+        }
+    };
+    auto store_chunk = [&](int ch) {
+        int dst;
+#pragma unroll
+        for (int i = 0; i < C::NW; ++i) {
+            const int idx = t + 256 * i;
+            (void)w_src(ch, min(idx, 16 * C::WCR - 1), dst);
+            if (idx < 16 * C::WCR) *reinterpret_cast<uint4 *>(lw + dst) = rw[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::NA; ++i) {
+            const int idx = t + 256 * i;
+            (void)a_src(ch, min(idx, C::TM * C::ACR - 1), dst);
+            if (idx < C::TM * C::ACR) *reinterpret_cast<uint4 *>(la + dst) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::ND; ++i) {
+            const int idx = t + 256 * i;
+            if (idx < C::TM * C::KCB) ld[idx] = rd[i];
+        }
+    };
+
+    float acc[TT];
+#pragma unroll
+    for (int i = 0; i < TT; ++i) acc[i] = 0.0f;
+
+    load_chunk(0);
+    for (int ch = 0; ch < nchunks; ++ch) {
+        store_chunk(ch);
+        lds_barrier();
+        if (ch + 1 < nchunks) load_chunk(ch + 1);
+        // the lane's weight row in LDS for this chunk (its 16-B misalignment)
+        const size_t off = size_t(ch) * C::KCB * F::BB;
+        const int mis = int(reinterpret_cast<uintptr_t>(a.w + size_t(min(n0 + nl, a.N - 1)) * a.row_bytes + off) & 15);
+        const uint8_t *wrow = lw + nl * C::WS + mis;
+        for (int it = wid; it < C::KCB * TT; it += 4) {
+            const int j = it / TT, tt = it - j * TT;
+            if (ch * C::KCB + j >= nb) continue;
+            const typename F::W wv = F::load_lds(wrow + j * F::BB, cl);
+            Scales<F> s;
+            decode_scales<F>(wv, s);
+            const int8_t *arow = la + (16 * tt + nl) * C::AS + j * F::QK;
+            int S[4] = {0, 0, 0, 0};
+            int4v Mb = {0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < F::NU; ++u) {
+                const uint2 av = ld8(arow + F::koff(u, cl));
+                const int4v D = mfma16x16x32(av, F::bop(wv, u, cl));
+                if constexpr (F::kMin) {
+                    const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
+                    Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tok = 16 * tt + 4 * cl + r;
+                const float dx = ld[tok * C::KCB + j];
+                float v;
+                if constexpr (F::kMin) v = dx * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);  // E:11026
+                else v = (s.d * dx) * (float)S[r];                                            // E:11101 / E:3405
+                part[(j * C::TM + tok) * 16 + nl] = v;
+            }
+        }
+        lds_barrier();
+        // this chunk's blocks, in order
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+            const int o = t + 256 * i;  // token o / 16, row o % 16
+            for (int j = 0; j < C::KCB && ch * C::KCB + j < nb; ++j) acc[i] += part[j * C::TM * 16 + o];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TT; ++i) {
+        const int o = t + 256 * i;
+        const int tok = o >> 4, n = n0 + (o & 15);
+        if (tok < a.M && n < a.N) {
+            float v = acc[i];
+            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+            a.y[size_t(tok) * a.ldy + n] = v;
+        }
+    }
+}
+
+template <class F, int TT>
+static hipError_t launch_small_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    using C = SmallM<F, TT>;
+    hipLaunchKernelGGL((mfma_small_kernel<F, TT>), dim3(unsigned((a.N + 15) / 16)), dim3(256),
+                       size_t(C::LDS), s, a, x);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t launch_small(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    switch ((a.M + 15) / 16) {
+        case 1: return launch_small_t<F, 1>(a, x, s);
+        case 2: return launch_small_t<F, 2>(a, x, s);
+        case 3: return launch_small_t<F, 3>(a, x, s);
+        default: return launch_small_t<F, 4>(a, x, s);
+    }
+}
+
 template <class F, int TT, int PF, int PA>
 static hipError_t launch_mfma_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
     const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
@@ -306,7 +510,7 @@ template <class F>
 static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
     // large M: 4 token tiles per wave (2 for Q6_K, whose 16 units would spill)
     constexpr int kTT = F::NU > 8 ? 2 : 4;
-    if (a.M <= 64) return launch_mfma_t<F, 1, 3, 1>(a, x, s);
+    if (a.M <= 64) return launch_small<F>(a, x, s);
     return launch_mfma_t<F, kTT, 1, 1>(a, x, s);
 }
 
