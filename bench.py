@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 DECODE_BYTES_PER_TOKEN = 36 * 72_120_320 + 319_065_600  # 36 layers + Q6_K LM head
 ROTATE_BYTES = 512 << 20
+DIRECT = False  # --direct: launch steps one by one instead of replaying a HIP graph
 
 
 def log(msg):
@@ -74,11 +75,19 @@ class Workload:
         self.ctx.gemm_multi_dispatch_prequantized(self.q, None, self.M, self.K, [self.task(i)])
 
     def time(self, fn, steps, warmup):
-        """ms per step over exactly `steps` graph-captured calls of fn."""
+        """ms per step over exactly `steps` graph-captured calls of fn (or, with
+        DIRECT set, `steps` direct calls: for profilers that do not follow
+        graph launches; per-kernel durations are the same, the gaps between
+        kernels are host launch time)."""
         ctx = self.ctx
         for i in range(warmup):
             fn(i)
         ctx.sync()
+        if DIRECT:
+            ctx.timer_begin()
+            for i in range(steps):
+                fn(i)
+            return ctx.timer_end() / steps
         ctx.graph_begin()
         for i in range(steps):
             fn(i)
@@ -108,6 +117,26 @@ def check_against_oracle(wl):
     exact = bool(np.array_equal(y.view(np.uint32), ref.view(np.uint32)))
     log(f"parity {qmm_hip.TYPE_NAMES[wl.type]} {wl.N}x{wl.K} M={wl.M}: norm err {err:.2e}, bit-exact {exact}")
     return {"norm_err": err, "bit_exact": exact}
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_fused_9728x2560_pmc.txt")
+
+
+def traffic(path):
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per dispatch, each
+    scaled by the counter's reading on a copy of known size); None if the
+    summary is absent."""
+    try:
+        vals = {}
+        with open(path) as f:
+            for ln in f:
+                if ":" in ln and not ln.startswith("#"):
+                    k, v = ln.split(":", 1)
+                    vals[k.strip()] = v.strip()
+        return int(float(vals["hbm_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline(N, K, seconds):
@@ -156,7 +185,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--direct", action="store_true",
+                    help="launch steps directly, not from a HIP graph (for rocprofv3 runs)")
     args = ap.parse_args()
+    global DIRECT
+    DIRECT = args.direct
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build measures the single-GPU hot path "
               "(row-sharding across GPUs is a design note, not built)", file=sys.stderr)
@@ -174,9 +207,12 @@ def main():
     ms = wl.time(wl.step, args.steps, args.warmup)
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"step (quantize + GEMV), {wl.R} replicas: {ms * 1e3:.2f} us/step, {value:.1f} GB/s")
+    # the step is one launch of the fused kernel (quantizer + GEMV): its
+    # roofline is the step's algorithmic bytes over the step's duration
+    ach = value
     ms_k = wl.time(wl.kernel_only, args.steps, args.warmup)
-    ach = kern_bytes / (ms_k * 1e-3) / 1e9
-    log(f"GEMV kernel alone: {ms_k * 1e3:.2f} us/launch, {ach:.1f} GB/s")
+    ach_pre = kern_bytes / (ms_k * 1e-3) / 1e9
+    log(f"GEMV on prequantized Q8_K activations: {ms_k * 1e3:.2f} us/launch, {ach_pre:.1f} GB/s")
     hot = Workload(ctx, synth.TYPE_Q4_K, N, K, 1, 1, seed=0)
     ms_hot = hot.time(hot.kernel_only, args.steps, args.warmup)
     hot.free()
@@ -226,13 +262,16 @@ def main():
         "config": {"workload": "Q4_K GEMV batch 1 (fp32 x -> Q8_K on device, then GEMV), "
                                "weight 9728 x 2560 GGUF super-blocks, fp32 out",
                    "N": N, "K": K, "M": 1, "replicas": wl.R,
-                   "replica_bytes": wl.wbytes, "timing": "HIP graph of all steps, HIP events"},
+                   "replica_bytes": wl.wbytes,
+                   "timing": "direct launches, HIP events" if DIRECT else "HIP graph of all steps, HIP events"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "tokens_per_s_equiv": round(value * 1e9 / DECODE_BYTES_PER_TOKEN, 1),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<FmtQ4K>", "us_per_launch": round(ms_k * 1e3, 3),
-                     "algorithmic_bytes": kern_bytes},
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic(TRAFFIC_PROFILE),
+                     "kernel": "gemv_kernel<FmtQ4K, fused Q8_K quantizer>",
+                     "us_per_launch": round(ms * 1e3, 3), "algorithmic_bytes": step_bytes},
+        "gemv_prequantized": {"kernel": "gemv_kernel<FmtQ4K> on Q8_K input", "us_per_launch": round(ms_k * 1e3, 3),
+                              "algorithmic_bytes": kern_bytes, "gbs": round(ach_pre, 1)},
         "cache_resident_us_per_launch": round(ms_hot * 1e3, 3),
         "parity": parity,
         "cpu_baseline": cpu,
