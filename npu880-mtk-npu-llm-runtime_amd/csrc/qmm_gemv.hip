@@ -388,14 +388,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, const float *__res
     // that every lane issues its loads (duplicates rewrite identical bytes).
     const int span_mis = int(reinterpret_cast<uintptr_t>(span) & 15);
     uint4 st[NST > 0 ? NST : 1];
-    auto stage_load = [&](int t0) {
+    auto stage_load = [&](int t0) __attribute__((always_inline)) {
         const int nb_batch = max(min(SLOTS * U, nblk - t0), 1);
         const uint8_t *base = span + size_t(t0) * F::BB - span_mis;
         const int nchunks = (span_mis + nb_batch * F::BB + 15) >> 4;
 #pragma unroll
         for (int j = 0; j < NST; ++j) st[j] = ld16_nt(base + 16 * min(64 * j + lane, nchunks - 1));
     };
-    auto stage_store = [&]() {
+    auto stage_store = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
     };

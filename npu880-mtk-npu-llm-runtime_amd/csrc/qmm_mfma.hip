@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>:
         okA[t] = tokA < a.M;
         xa_row[t] = x.qs + size_t(okA[t] ? tokA : 0) * a.K;
     }
-    auto load_act = [&](int b, ActBlock<F, TT> &ab) {
+    auto load_act = [&](int b, ActBlock<F, TT> &ab) __attribute__((always_inline)) {
         const int bl = min(b, nb - 1);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256) void mfma_small_kernel(MatArgs a, typename Act
     // to the last row), token bytes [ch*KCB*QK, +ASEG) of tokens 0..TM-1
     // (clamped to the last token); load indices past the valid bytes repeat
     // the last valid 16 B, which is stored to the same place.
-    auto w_src = [&](int ch, int idx, int &dst) -> const uint8_t * {
+    auto w_src = [&](int ch, int idx, int &dst) __attribute__((always_inline)) -> const uint8_t * {
         const int row = min(idx / C::WCR, 15), piece = idx - row * C::WCR;
         const size_t off = size_t(ch) * C::KCB * F::BB;
         const uint8_t *rp = a.w + size_t(min(n0 + row, a.N - 1)) * a.row_bytes + off;
@@ -377,14 +377,14 @@ __global__ __launch_bounds__(256) void mfma_small_kernel(MatArgs a, typename Act
         dst = row * C::WS + 16 * pc;
         return rp - mis + 16 * pc;
     };
-    auto a_src = [&](int ch, int idx, int &dst) -> const int8_t * {
+    auto a_src = [&](int ch, int idx, int &dst) __attribute__((always_inline)) -> const int8_t * {
         const int tok = min(idx / C::ACR, C::TM - 1), piece = idx - tok * C::ACR;
         const int off = ch * C::ASEG;
         const int pc = min(piece, min(C::ASEG, K - off) / 16 - 1);
         dst = tok * C::AS + 16 * pc;
         return x.qs + size_t(min(tok, a.M - 1)) * K + off + 16 * pc;
     };
-    auto load_chunk = [&](int ch) {
+    auto load_chunk = [&](int ch) __attribute__((always_inline)) {
         int dummy;
 #pragma unroll
         for (int i = 0; i < C::NW; ++i) rw[i] = ld16_nt(w_src(ch, min(t + 256 * i, 16 * C::WCR - 1), dummy));
@@ -397,7 +397,7 @@ __global__ __launch_bounds__(256) void mfma_small_kernel(MatArgs a, typename Act
             rd[i] = x.d[size_t(min(tok, a.M - 1)) * nb + min(ch * C::KCB + j, nb - 1)];
         }
     };
-    auto store_chunk = [&](int ch) {
+    auto store_chunk = [&](int ch) __attribute__((always_inline)) {
         int dst;
 #pragma unroll
         for (int i = 0; i < C::NW; ++i) {
