@@ -105,6 +105,122 @@ class Workload:
             self.ctx.free(b)
 
 
+class Replicated:
+    """One tensor replicated R times in one allocation (rotation defeats the
+    256 MB Infinity Cache for multi-tensor steps)."""
+
+    def __init__(self, ctx, type_id, N, K, R, seed):
+        self.type, self.N, self.K = type_id, N, K
+        self.bytes = N * synth.row_bytes(type_id, K)
+        self.stride = (self.bytes + 4095) // 4096 * 4096
+        self.R = R
+        self.buf = ctx.malloc(R * self.stride)
+        ctx.h2d(self.buf, synth.weights(type_id, N, K, seed=seed))
+        for r in range(1, R):
+            ctx.d2d(self.buf.ptr + r * self.stride, self.buf.ptr, self.bytes)
+
+    def task(self, i, dst, ldy, res=None):
+        return qmm_hip.MatrixTask(self.buf.ptr + (i % self.R) * self.stride, self.type, self.N,
+                                  self.K, dst, ldy, residual=res, res_stride=ldy if res is not None else 0)
+
+
+def timed(ctx, fn, steps, warmup):
+    """ms per call of fn(i) over exactly `steps` calls, graph-captured (or direct)."""
+    for i in range(warmup):
+        fn(i)
+    ctx.sync()
+    if DIRECT:
+        ctx.timer_begin()
+        for i in range(steps):
+            fn(i)
+        return ctx.timer_end() / steps
+    ctx.graph_begin()
+    for i in range(steps):
+        fn(i)
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    ctx.timer_begin()
+    ctx.graph_launch(g)
+    ms = ctx.timer_end()
+    ctx.graph_destroy(g)
+    return ms / steps
+
+
+def bench_ffn(ctx, steps):
+    """FFN block at batch 1: gate+up Q4_K 9728x2560 on one shared Q8_K input
+    (one dispatch), SiLU(gate)*up -> Q8_K, down Q6_K 2560x9728 (prequantized)."""
+    H, F = 2560, 9728
+    tg, tu, td = synth.FFN["gate"], synth.FFN["up"], synth.FFN["down"]
+    block = 2 * F * synth.row_bytes(tg[0], H) + H * synth.row_bytes(td[0], F)
+    R = max(1, math.ceil(ROTATE_BYTES / block))
+    wg = Replicated(ctx, tg[0], F, H, R, 71)
+    wu = Replicated(ctx, tu[0], F, H, R, 72)
+    wd = Replicated(ctx, td[0], H, F, R, 73)
+    x = ctx.upload(synth.activations(1, H, seed=70))
+    g, u, h, y = ctx.malloc(F * 4), ctx.malloc(F * 4), ctx.malloc(F * 4), ctx.malloc(H * 4)
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, F))
+    ctx.reserve(1, F)
+
+    def step(i):
+        ctx.gemm_multi_dispatch(x, 1, H, [wg.task(i, g, F), wu.task(i, u, F)])
+        ctx.swiglu_q8k(g, u, 1, F, h, q)
+        ctx.gemm_multi_dispatch_prequantized(q, None, 1, F, [wd.task(i, y, H)])
+
+    ms = timed(ctx, step, steps, 10)
+    alg = block + H * 4 + H * 4  # weights + fp32 x in + fp32 y out (SURVEY-style fused minimum)
+    for b in (wg.buf, wu.buf, wd.buf, x, g, u, h, y, q):
+        ctx.free(b)
+    return {"us_per_block": round(ms * 1e3, 3), "algorithmic_bytes": alg,
+            "gbs": round(alg / (ms * 1e-3) / 1e9, 1), "replicas": R,
+            "launches": "gemv(gate), gemv(up), swiglu+Q8_K, gemv(down)"}
+
+
+def bench_prefill(ctx, steps):
+    """One prefill layer's projections at M = 512 tokens: QKV Q5_K 6144x2560,
+    O Q4_K 2560x4096, gate+up Q4_K 9728x2560 (one dispatch), down Q6_K
+    2560x9728, Q8_0 2560x2560; each dispatch quantizes its fp32 input."""
+    M = synth.PREFILL_LAYER["M"]
+    T = synth.PREFILL_LAYER["tensors"]
+    layer = sum(N * synth.row_bytes(t, K) for t, N, K in T.values())
+    R = max(1, math.ceil(ROTATE_BYTES / layer))
+    W = {name: Replicated(ctx, t, N, K, R, 100 + j) for j, (name, (t, N, K)) in enumerate(T.items())}
+    xs = {K: ctx.upload(synth.activations(M, K, seed=200 + K)) for K in (2560, 4096, 9728)}
+    ys = {name: ctx.malloc(M * N * 4) for name, (t, N, K) in T.items()}
+    ctx.reserve(M, 9728)
+
+    def step(i):
+        ctx.gemm_multi_dispatch(xs[2560], M, 2560, [W["qkv"].task(i, ys["qkv"], 6144)])
+        ctx.gemm_multi_dispatch(xs[4096], M, 4096, [W["o"].task(i, ys["o"], 2560)])
+        ctx.gemm_multi_dispatch(xs[2560], M, 2560, [W["gate"].task(i, ys["gate"], 9728),
+                                                     W["up"].task(i, ys["up"], 9728)])
+        ctx.gemm_multi_dispatch(xs[9728], M, 9728, [W["down"].task(i, ys["down"], 2560)])
+        ctx.gemm_multi_dispatch(xs[2560], M, 2560, [W["q8_0"].task(i, ys["q8_0"], 2560)])
+
+    ms = timed(ctx, step, steps, 3)
+    ops = sum(2.0 * M * N * K for t, N, K in T.values())
+    for w in W.values():
+        ctx.free(w.buf)
+    for b in list(xs.values()) + list(ys.values()):
+        ctx.free(b)
+    per_layer = ms * 1e-3
+    return {"us_per_layer": round(ms * 1e3, 2), "tops": round(ops / per_layer / 1e12, 2),
+            "mfma_frac": round(ops / per_layer / 1e12 / INT8_PEAK_TOPS, 4),
+            "prefill_36_layers_ms": round(36 * ms, 3),
+            "prefill_tokens_per_s": round(M / (36 * per_layer), 1), "replicas": R}
+
+
+def launch_floor(ctx, steps):
+    """µs per launch of the smallest kernel the library has (Q8_K quantizer
+    of one 256-value block), graph-captured: the per-launch floor."""
+    x = ctx.upload(synth.activations(1, 256, seed=5))
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, 256))
+    ms = timed(ctx, lambda i: ctx.quantize_q8k(x, 1, 256, q), steps, 10)
+    ctx.free(x)
+    ctx.free(q)
+    return round(ms * 1e3, 3)
+
+
 def check_against_oracle(wl):
     """The benchmarked path gives the oracle's result (bit-exact) on replica 0."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -234,6 +350,20 @@ def main():
             log(f"tree-verify Q4_K M={M}: {tv[f'M{M}']}")
             t.free()
         extra["tree_verify_q4k_9728x2560"] = tv
+        t5 = synth.TREE_VERIFY["q5k"]
+        t = Workload(ctx, t5[0], t5[1], t5[2], 64, 0, seed=80)
+        m_k = t.time(t.kernel_only, max(50, args.steps // 4), 10)
+        extra["tree_verify_q5k_4096x2560_M64"] = {
+            "us_gemm_kernel": round(m_k * 1e3, 3),
+            "tops": round(2.0 * 64 * t5[1] * t5[2] / (m_k * 1e-3) / 1e12, 3)}
+        log(f"tree-verify Q5_K 4096x2560 M=64: {extra['tree_verify_q5k_4096x2560_M64']}")
+        t.free()
+        extra["ffn_block_q4k_q6k"] = bench_ffn(ctx, max(50, args.steps // 10))
+        log(f"FFN block: {extra['ffn_block_q4k_q6k']}")
+        extra["prefill_layer_m512"] = bench_prefill(ctx, max(5, args.steps // 200))
+        log(f"prefill layer M=512: {extra['prefill_layer_m512']}")
+        extra["launch_floor_us"] = launch_floor(ctx, max(200, args.steps // 4))
+        log(f"launch floor: {extra['launch_floor_us']} us")
         lm = Workload(ctx, synth.TYPE_Q6_K, 151936, 2560, 1, 2, seed=20)
         m_lm = lm.time(lm.kernel_only, max(20, args.steps // 20), 5)
         lm_bytes = 151936 * 2100 + (2560 + 40 + 320) + 151936 * 4

@@ -14,6 +14,13 @@
 // the min term and the per-block fp32 expression are applied exactly as the
 // reference's scalar kernels do, and blocks are accumulated in order per
 // output — the result equals the reference's fp32 sum bit for bit.
+//
+// The min term Mb = sum_j m_j * bsum32_j of Q4_K / Q5_K is itself an int8
+// contraction, sum_k x_k * m_unit(k), so it runs on the matrix unit as one
+// accumulating MFMA chain over the block's units against a B operand of
+// broadcast 6-bit mins (exact; equal to the reference's bsum form for every
+// Q8_K row whose block sums are the sums of its codes, which the quantizer
+// guarantees).
 #include "qmm_device.h"
 
 namespace qmm {
@@ -187,331 +194,323 @@ __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, c, 0, 0, 0);
 }
 
-// Workgroup = 16 weight rows x 16*TT tokens; its 4 waves split the K
-// blocks (wave w takes blocks w, w+4, ...), each wave keeping PF of its
-// blocks' weight bytes in flight. Per group of 4 consecutive blocks every
-// wave writes its block's fp32 terms to LDS, and after a barrier each
-// output's owner thread adds the 4 terms in block order — the sequential
-// accumulation of the reference, so outputs stay bit-identical while the
-// K loop runs 4 waves wide.
+// ================================================================ tile GEMM
+// Workgroup tile = ROWS weight rows x TOK tokens, 4 waves arranged as
+// PR row groups x PT token groups x KS K phases; a wave computes WR x WT
+// MFMA tiles of 16 x 16 over the blocks j = kp (mod KS) of every chunk.
 //
-// Per block and token tile: NU MFMAs give the unit dots D_u; S = sum sc_u *
-// D_u on the VALU (exact int32). For the formats with mins the min term
-// Mb = sum_j m_j * bsum32_j is itself an int8 contraction — sum_k x_k *
-// m_{unit(k)} — so it runs on the MFMA unit as one accumulating chain over
-// the units with a B operand of broadcast 6-bit mins (exact, no bsum reads).
-template <class F, int TT> struct ActBlock {
-    uint2 a[TT][F::NU];  // A operands, per token tile and unit
-    float dx[TT][4];     // activation scales of the lane's output tokens
+// Operands reach LDS by direct buffer -> LDS transfers (buffer_load ... lds,
+// 16 B per lane): no registers, no address clamps. Every transfer goes
+// through a buffer descriptor whose range is exactly the workgroup's rows,
+// the M tokens' codes or their scales, so a lane past the end reads zeros
+// and touches no memory. The K loop walks chunks of KCB blocks through PD
+// LDS slots: the transfers of chunk ch + PD - 1 are issued before chunk ch
+// is computed, and an explicit vmcnt wait (transfers retire in order)
+// releases chunk ch. Every wave issues the same number of transfers per
+// chunk (surplus ones target a dump line), so the wait counts are static.
+// The transfers are written as inline assembly: the compiler tracks the
+// builtin form as an LDS store and answers every later LDS read with a
+// full vmcnt(0) wait (it cannot tell the slots apart), which would wait for
+// the chunk still in flight. The kernel orders them itself with explicit
+// vmcnt waits and barriers; inside the asm, M0 (the LDS destination) is set
+// and given its one wait state.
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// buffer descriptor: base, stride 0, num_records bytes, raw 32-bit dwords
+__device__ inline v4i32 buf_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    v4i32 r;
+    r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(b)));
+    r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane(int(bytes));
+    r.w = 0x00020000;
+    return r;
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane(
+        uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p)));
+}
+// M0 is reserved to the compiler, which uses it in these kernels for nothing
+// else (no LDS transfers of its own, no message or interpolation ops).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// lane l's 16 B at byte offset voff of the buffer land at LDS byte address lds + 16 l
+__device__ inline void dma16(const v4i32 &r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
+}
+// lane l's 4 B land at lds + 4 l
+__device__ inline void dma4(const v4i32 &r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt vmcnt(N) (lgkmcnt and expcnt not waited on)
+template <int N> __device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0) only
+
+constexpr uint32_t kFar = 0x80000000u;  // a byte offset past every descriptor's range
+
+template <class F, int WR_, int WT_, int PR_, int PT_, int KS_, int TR_, int PD_, int BUDGET>
+struct TileCfg {
+    static constexpr int WR = WR_, WT = WT_, PR = PR_, PT = PT_, KS = KS_, TR = TR_, PD = PD_;
+    static_assert(PR * PT * KS == 4, "4 waves");
+    static_assert(TR == 16 || (TR == 8 && WT == 1 && PT == 1), "8 resident tokens: one token tile");
+    static constexpr int ROWS = 16 * WR * PR;
+    static constexpr int TOK = TR * WT * PT;  // tokens resident per chunk
+    static constexpr int wcr(int k) { return ((k * F::BB + 30) / 16) | 1; }  // odd: rows 4 banks apart
+    static constexpr int acr(int k) { return k * F::QK / 16 + 1; }
+    static constexpr int nwi(int k) { return (ROWS * wcr(k) + 63) / 64; }
+    static constexpr int nai(int k) { return (TOK * acr(k) + 63) / 64; }
+    static constexpr int ndi(int k) { return (k * TOK + 63) / 64; }
+    static constexpr int slot(int k) { return nwi(k) * 1024 + nai(k) * 1024 + ndi(k) * 256; }
+    static constexpr int per_wave(int k) { return (nwi(k) + 3) / 4 + (nai(k) + 3) / 4 + (ndi(k) + 3) / 4; }
+    static constexpr int part(int k) { return KS > 1 ? k * TOK * ROWS * 4 : 0; }
+    static constexpr int total(int k) { return PD * slot(k) + part(k) + 1024; }
+    static constexpr bool fits(int k) { return total(k) <= BUDGET && (PD - 1) * per_wave(k) <= 63; }
+    static constexpr int pick() {
+        int k = KS;
+        while (k + KS <= 16 && fits(k + KS)) k += KS;
+        return k;
+    }
+    static constexpr int KCB = pick();
+    static constexpr int WCR = wcr(KCB), ACR = acr(KCB);
+    static constexpr int NWI = nwi(KCB), NAI = nai(KCB), NDI = ndi(KCB);
+    static constexpr int NWW = (NWI + 3) / 4, NAW = (NAI + 3) / 4, NDW = (NDI + 3) / 4;
+    static constexpr int L = NWW + NAW + NDW;  // transfers per wave per chunk
+    static constexpr int OFF_A = NWI * 1024, OFF_D = OFF_A + NAI * 1024, SLOT = slot(KCB);
+    static constexpr int OFF_P = PD * SLOT, OFF_DUMP = OFF_P + part(KCB), LDS = total(KCB);
+    static_assert(fits(KCB), "tile does not fit the LDS budget");
+    static_assert(KS == 1 || TOK * ROWS <= 4 * 256, "K-split tiles: at most 4 outputs per thread");
 };
 
-template <class F, int TT, int PF, int PA>
-__global__ __launch_bounds__(256) void mfma_kernel(MatArgs a, typename ActOf<F>::T x) {
-    __shared__ float part[4][16 * TT * 16];  // [wave][token * 16 + row]
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int nl = lane & 15, c = lane >> 4;
-    const int n0 = int(blockIdx.x) * 16;
-    const int m0 = int(blockIdx.y) * 16 * TT;
-    const int nload = min(n0 + nl, a.N - 1);
-    const int nb = a.K / F::QK;
-    const int ngroups = (nb + 3) / 4;
-    const uint8_t *wrow = a.w + size_t(nload) * a.row_bytes;
+template <class C, class F>
+__global__ __launch_bounds__(256) void tile_kernel(MatArgs a, typename ActOf<F>::T x) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int WR = C::WR, WT = C::WT, KS = C::KS, TR = C::TR, KCB = C::KCB;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nl = lane & 15, cl = lane >> 4;
+    const int kp = wid % KS, pt = (wid / KS) % C::PT, pr = wid / (KS * C::PT);
+    const int n0 = int(blockIdx.x) * C::ROWS, m0 = int(blockIdx.y) * C::TOK;
+    const int K = a.K, nb = K / F::QK;
+    const int nchunks = (nb + KCB - 1) / KCB;
 
-    // A-operand rows of this lane (token m0 + 16t + nl), zero past M; output
-    // tokens m0 + 16t + 4c + r for the activation scales
-    const int8_t *xa_row[TT];
-    bool okA[TT];
+    // descriptors: this workgroup's rows (from the 16-B boundary at or below
+    // the first), the M tokens' codes, their block scales
+    const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
+    const uint32_t bl = uint32_t(wstart & 15);
+    const int rows_valid = min(C::ROWS, a.N - n0);
+    const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
+                              bl + uint32_t(rows_valid) * uint32_t(a.row_bytes));
+    const v4i32 ra = buf_rsrc(x.qs, uint32_t(a.M) * uint32_t(K));
+    const v4i32 rd = buf_rsrc(x.d, uint32_t(a.M) * uint32_t(nb) * 4u);
+    const uint32_t lds0 = lds_addr(lds);
+
+    // per-lane transfer offsets (chunk 0); lanes past a region's pieces get kFar
+    uint32_t wo[C::NWW], wp[C::NWW], ao[C::NAW], dof[C::NDW];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        const int tokA = m0 + 16 * t + nl;
-        okA[t] = tokA < a.M;
-        xa_row[t] = x.qs + size_t(okA[t] ? tokA : 0) * a.K;
+    for (int s = 0; s < C::NWW; ++s) {
+        const int p = (s * 4 + wid) * 64 + lane;
+        const int row = p / C::WCR, pc = p - row * C::WCR;
+        wo[s] = row < C::ROWS ? uint32_t(row) * uint32_t(a.row_bytes) + bl : kFar;
+        wp[s] = 16u * uint32_t(pc);
     }
-    auto load_act = [&](int b, ActBlock<F, TT> &ab) __attribute__((always_inline)) {
-        const int bl = min(b, nb - 1);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
+    for (int s = 0; s < C::NAW; ++s) {
+        const int p = (s * 4 + wid) * 64 + lane;
+        const int tok = p / C::ACR, pc = p - tok * C::ACR;
+        ao[s] = tok < C::TOK ? uint32_t(m0 + tok) * uint32_t(K) + 16u * uint32_t(pc) : kFar;
+    }
 #pragma unroll
-            for (int u = 0; u < F::NU; ++u)
-                ab.a[t][u] = okA[t] ? ld8(xa_row[t] + size_t(bl) * F::QK + F::koff(u, c)) : make_uint2(0u, 0u);
+    for (int s = 0; s < C::NDW; ++s) {
+        const int p = (s * 4 + wid) * 64 + lane;
+        const int j = p / C::TOK, tok = p - j * C::TOK;
+        dof[s] = j < KCB ? (uint32_t(m0 + tok) * uint32_t(nb) + uint32_t(j)) * 4u : kFar;
+    }
+    // issue chunk ch into slot sl; a chunk past the end reads nothing
+    auto issue = [&](int ch, int sl) __attribute__((always_inline)) {
+        const bool live = ch < nchunks;
+        const uint32_t base = lds0 + uint32_t(sl * C::SLOT), dump = lds0 + uint32_t(C::OFF_DUMP);
+        const uint32_t cw = uint32_t(ch) * uint32_t(KCB * F::BB);
+        const uint32_t ca = uint32_t(ch) * uint32_t(KCB * F::QK);
+        const uint32_t cd = uint32_t(ch) * uint32_t(KCB) * 4u;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = m0 + 16 * t + 4 * c + r;
-                ab.dx[t][r] = x.d[size_t(min(tok, a.M - 1)) * nb + bl];
-            }
+        for (int s = 0; s < C::NWW; ++s) {
+            const int i = s * 4 + wid;
+            const uint32_t v = ((wo[s] + cw) & ~15u) + wp[s];
+            dma16(rw, live ? v : kFar, i < C::NWI ? base + uint32_t(i * 1024) : dump);
+        }
+#pragma unroll
+        for (int s = 0; s < C::NAW; ++s) {
+            const int i = s * 4 + wid;
+            dma16(ra, live ? ao[s] + ca : kFar, i < C::NAI ? base + uint32_t(C::OFF_A + i * 1024) : dump);
+        }
+#pragma unroll
+        for (int s = 0; s < C::NDW; ++s) {
+            const int i = s * 4 + wid;
+            dma4(rd, live ? dof[s] + cd : kFar, i < C::NDI ? base + uint32_t(C::OFF_D + i * 256) : dump);
         }
     };
 
-    // weights (PF deep) and activations (PA deep) of this wave's blocks
-    // b = wid + 4i, clamped to the last block (never stored past nb)
-    typename F::W wq[PF];
-    ActBlock<F, TT> aq[PA];
+    float acc[WR][WT][4];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) wq[i] = F::load(wrow + size_t(min(wid + 4 * i, nb - 1)) * F::BB, c);
+    for (int wr = 0; wr < WR; ++wr)
 #pragma unroll
-    for (int i = 0; i < PA; ++i) load_act(wid + 4 * i, aq[i]);
+        for (int wt = 0; wt < WT; ++wt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[wr][wt][r] = 0.0f;
+    float *part = reinterpret_cast<float *>(lds + C::OFF_P);
+    float *dump4 = reinterpret_cast<float *>(lds + C::OFF_DUMP);
 
-    float acc[TT];
+    // one chunk: wait for it, compute its blocks of this wave's phase
+    auto step = [&](int ch, int sl) __attribute__((always_inline)) {
+        issue(ch + C::PD - 1, (sl + C::PD - 1) % C::PD);
+        wait_vmcnt<(C::PD - 1) * C::L>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *ws = lds + sl * C::SLOT;
+        const int8_t *as = reinterpret_cast<const int8_t *>(ws + C::OFF_A);
+        const float *ds = reinterpret_cast<const float *>(ws + C::OFF_D);
+        const uint32_t cw = uint32_t(ch) * uint32_t(KCB * F::BB);
 #pragma unroll
-    for (int j = 0; j < TT; ++j) acc[j] = 0.0f;
-
-    for (int grp = 0; grp < ngroups; ++grp) {
-        const int b = 4 * grp + wid;
-        const typename F::W wcur = wq[0];
-        const ActBlock<F, TT> acur = aq[0];
+        for (int jj = 0; jj < KCB / KS; ++jj) {
+            const int j = jj * KS + kp;
+            const bool valid = ch * KCB + j < nb;
 #pragma unroll
-        for (int i = 0; i + 1 < PF; ++i) wq[i] = wq[i + 1];
-        wq[PF - 1] = F::load(wrow + size_t(min(b + 4 * PF, nb - 1)) * F::BB, c);
+            for (int wr = 0; wr < WR; ++wr) {
+                const int rl = (pr * WR + wr) * 16 + nl;  // lane's weight row in the tile
+                const int mis = int((uint32_t(rl) * uint32_t(a.row_bytes) + bl + cw) & 15u);
+                const typename F::W wv = F::load_lds(ws + rl * (C::WCR * 16) + mis + j * F::BB, cl);
+                Scales<F> sc;
+                decode_scales<F>(wv, sc);
+                // a block past the end of K holds stale bytes: its d, dmin and
+                // dx are zeroed, its term is a signed zero, the sums are
+                // unchanged (a sum starting at +0 is never -0)
+                const float d = valid ? sc.d : 0.0f, dmin = valid ? sc.dmin : 0.0f;
 #pragma unroll
-        for (int i = 0; i + 1 < PA; ++i) aq[i] = aq[i + 1];
-        load_act(b + 4 * PA, aq[PA - 1]);
-        if (b < nb) {
-            Scales<F> s;
-            decode_scales<F>(wcur, s);
+                for (int wt = 0; wt < WT; ++wt) {
+                    const int tl = (pt * WT + wt) * TR + (nl & (TR - 1));  // lane's A token
+                    const int8_t *arow = as + tl * (C::ACR * 16) + j * F::QK;
+                    int S[4] = {0, 0, 0, 0};
+                    int4v Mb = {0, 0, 0, 0};
 #pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                int S[4] = {0, 0, 0, 0};
-                int4v Mb = {0, 0, 0, 0};
+                    for (int u = 0; u < F::NU; ++u) {
+                        const uint2 av = ld8(arow + F::koff(u, cl));
+                        const int4v D = mfma16x16x32(av, F::bop(wv, u, cl));
+                        if constexpr (F::kMin) {
+                            const uint32_t mb = __builtin_amdgcn_perm(0u, uint32_t(sc.m[u]), 0u);  // byte broadcast
+                            Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
+                        }
 #pragma unroll
-                for (int u = 0; u < F::NU; ++u) {
-                    const int4v D = mfma16x16x32(acur.a[t][u], F::bop(wcur, u, c));
-                    if constexpr (F::kMin) {
-                        const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
-                        Mb = mfma16x16x32_acc(acur.a[t][u], make_uint2(mb, mb), Mb);
+                        for (int r = 0; r < 4; ++r) S[r] += __mul24(sc.sc[u], D[r]);
                     }
+                    // dx of output tokens 4 cl + r of this token tile (tokens
+                    // past TR read neighbouring scales; their outputs are not kept)
+                    const float4 dx4 = *reinterpret_cast<const float4 *>(ds + j * C::TOK + (pt * WT + wt) * TR + 4 * cl);
+                    const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
+                    for (int r = 0; r < 4; ++r) {
+                        const float dx = valid ? dxr[r] : 0.0f;
+                        float v;
+                        if constexpr (F::kMin) v = dx * (d * (float)S[r] - dmin * (float)Mb[r]);  // E:11026
+                        else v = (d * dx) * (float)S[r];                                        // E:11101 / E:3405
+                        if constexpr (KS == 1) {
+                            acc[wr][wt][r] += v;
+                        } else {
+                            const int tok = (pt * WT + wt) * TR + 4 * cl + r;
+                            float *dst = tok < (pt * WT + wt + 1) * TR
+                                             ? part + (j * C::TOK + tok) * C::ROWS + rl
+                                             : dump4 + lane;
+                            *dst = v;
+                        }
+                    }
                 }
+            }
+        }
+        if constexpr (KS > 1) {
+            wait_lgkm0();
+            __builtin_amdgcn_s_barrier();
+            // outputs (token o / ROWS, row o % ROWS): this chunk's blocks in order
+#pragma unroll
+            for (int q = 0; q < (C::TOK * C::ROWS + 255) / 256; ++q) {
+                const int o = int(threadIdx.x) + 256 * q;
+                if (o < C::TOK * C::ROWS) {
+                    float s = acc[0][0][q & 3];
+                    for (int j = 0; j < KCB; ++j) s += part[j * C::TOK * C::ROWS + o];
+                    acc[0][0][q & 3] = s;
+                }
+            }
+        }
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();  // every wave is done with slot sl
+    };
+
+#pragma unroll
+    for (int p = 0; p + 1 < C::PD; ++p) issue(p, p);
+    int ch = 0;
+    for (; ch + C::PD <= nchunks; ch += C::PD)
+#pragma unroll
+        for (int q = 0; q < C::PD; ++q) step(ch + q, q);
+    for (int q = 0; ch < nchunks; ++ch, ++q) step(ch, q);
+    wait_vmcnt<0>();  // the tail's transfers (zeros into a free slot) land before the workgroup ends
+
+    if constexpr (KS == 1) {
+#pragma unroll
+        for (int wr = 0; wr < WR; ++wr) {
+            const int n = n0 + (pr * WR + wr) * 16 + nl;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int wt = 0; wt < WT; ++wt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float dx = acur.dx[t][r];
-                    float v;
-                    if constexpr (F::kMin) v = dx * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);  // E:11026
-                    else v = (s.d * dx) * (float)S[r];                                            // E:11101 / E:3405
-                    part[wid][(16 * t + 4 * c + r) * 16 + nl] = v;
+                    const int tok = m0 + (pt * WT + wt) * TR + 4 * cl + r;
+                    if (tok >= a.M) continue;
+                    float v = acc[wr][wt][r];
+                    if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+                    a.y[size_t(tok) * a.ldy + n] = v;
                 }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < (C::TOK * C::ROWS + 255) / 256; ++q) {
+            const int o = int(threadIdx.x) + 256 * q;
+            const int tok = m0 + o / C::ROWS, n = n0 + o % C::ROWS;
+            if (o < C::TOK * C::ROWS && tok < a.M && n < a.N) {
+                float v = acc[0][0][q & 3];
+                if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+                a.y[size_t(tok) * a.ldy + n] = v;
             }
-        }
-        lds_barrier();
-        // blocks 4grp .. 4grp+3 in order
-#pragma unroll
-        for (int j = 0; j < TT; ++j) {
-            const int o = int(threadIdx.x) + 256 * j;
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                if (4 * grp + w < nb) acc[j] += part[w][o];
-        }
-        lds_barrier();
-    }
-#pragma unroll
-    for (int j = 0; j < TT; ++j) {
-        const int o = int(threadIdx.x) + 256 * j;
-        const int tok = m0 + (o >> 4), n = n0 + (o & 15);
-        if (tok < a.M && n < a.N) {
-            float v = acc[j];
-            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
-            a.y[size_t(tok) * a.ldy + n] = v;
         }
     }
 }
 
-// ---------------------------------------------------------------- small M
-// Workgroup = one 16-row tile x all M <= 64 tokens (TT = ceil(M / 16)
-// tiles). K is processed in chunks of KCB blocks. For each chunk the
-// workgroup loads the 16 weight-row segments (KCB * BB contiguous bytes
-// each) and the token segments (KCB * QK bytes each) with coalesced 16-B
-// loads — one chunk ahead, into registers — and stores them to LDS; the 4
-// waves share the chunk's (block, token tile) items, read their MFMA
-// operands from LDS and write each block's fp32 terms to LDS, where every
-// output's owner thread adds them in block order (bit-identical to the
-// reference's sequential accumulation).
-template <class F, int TT>
-struct SmallM {
-    static constexpr int TM = 16 * TT;
-    // blocks per chunk: about 48 KiB of LDS per workgroup
-    static constexpr int per_block = 16 * F::BB + TM * F::QK + TM * 4 + TM * 64;
-    static constexpr int KCB0 = (48 * 1024) / per_block;
-    static constexpr int KCB = KCB0 < 1 ? 1 : (KCB0 > 32 ? 32 : KCB0);
-    static constexpr int WSEG = KCB * F::BB;           // weight bytes per row per chunk
-    static constexpr int WCR = (WSEG + 30) / 16;       // 16-B loads per row, any alignment
-    static constexpr int WS = WCR * 16 + 16;           // LDS row stride
-    static constexpr int ASEG = KCB * F::QK;           // activation bytes per token per chunk
-    static constexpr int ACR = ASEG / 16;
-    static constexpr int AS = ASEG + 16;               // LDS token stride
-    static constexpr int NW = (16 * WCR + 255) / 256;  // loads per thread
-    static constexpr int NA = (TM * ACR + 255) / 256;
-    static constexpr int ND = (TM * KCB + 255) / 256;
-    static constexpr int OFF_A = 16 * WS;
-    static constexpr int OFF_D = OFF_A + TM * AS;
-    static constexpr int OFF_P = OFF_D + ((TM * KCB * 4 + 15) & ~15);
-    static constexpr int LDS = OFF_P + KCB * TM * 16 * 4;
-};
-
-template <class F, int TT>
-__global__ __launch_bounds__(256) void mfma_small_kernel(MatArgs a, typename ActOf<F>::T x) {
-    using C = SmallM<F, TT>;
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *lw = lds;
-    int8_t *la = reinterpret_cast<int8_t *>(lds + C::OFF_A);
-    float *ld = reinterpret_cast<float *>(lds + C::OFF_D);
-    float *part = reinterpret_cast<float *>(lds + C::OFF_P);
-    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-    const int nl = lane & 15, cl = lane >> 4;
-    const int n0 = int(blockIdx.x) * 16;
-    const int K = a.K, nb = K / F::QK;
-    const int nchunks = (nb + C::KCB - 1) / C::KCB;
-
-    uint4 rw[C::NW], ra[C::NA];
-    float rd[C::ND];
-    // chunk ch: weight bytes [ch*KCB*BB, +WSEG) of rows n0..n0+15 (clamped
-    // to the last row), token bytes [ch*KCB*QK, +ASEG) of tokens 0..TM-1
-    // (clamped to the last token); load indices past the valid bytes repeat
-    // the last valid 16 B, which is stored to the same place.
-    auto w_src = [&](int ch, int idx, int &dst) __attribute__((always_inline)) -> const uint8_t * {
-        const int row = min(idx / C::WCR, 15), piece = idx - row * C::WCR;
-        const size_t off = size_t(ch) * C::KCB * F::BB;
-        const uint8_t *rp = a.w + size_t(min(n0 + row, a.N - 1)) * a.row_bytes + off;
-        const int mis = int(reinterpret_cast<uintptr_t>(rp) & 15);
-        const int nbytes = int(min(size_t(C::WSEG), a.row_bytes - off));
-        const int pc = min(piece, (mis + nbytes + 15) / 16 - 1);
-        dst = row * C::WS + 16 * pc;
-        return rp - mis + 16 * pc;
-    };
-    auto a_src = [&](int ch, int idx, int &dst) __attribute__((always_inline)) -> const int8_t * {
-        const int tok = min(idx / C::ACR, C::TM - 1), piece = idx - tok * C::ACR;
-        const int off = ch * C::ASEG;
-        const int pc = min(piece, min(C::ASEG, K - off) / 16 - 1);
-        dst = tok * C::AS + 16 * pc;
-        return x.qs + size_t(min(tok, a.M - 1)) * K + off + 16 * pc;
-    };
-    auto load_chunk = [&](int ch) __attribute__((always_inline)) {
-        int dummy;
-#pragma unroll
-        for (int i = 0; i < C::NW; ++i) rw[i] = ld16_nt(w_src(ch, min(t + 256 * i, 16 * C::WCR - 1), dummy));
-#pragma unroll
-        for (int i = 0; i < C::NA; ++i) ra[i] = ld16(a_src(ch, min(t + 256 * i, C::TM * C::ACR - 1), dummy));
-#pragma unroll
-        for (int i = 0; i < C::ND; ++i) {
-            const int idx = min(t + 256 * i, C::TM * C::KCB - 1);
-            const int tok = idx / C::KCB, j = idx - tok * C::KCB;
-            rd[i] = x.d[size_t(min(tok, a.M - 1)) * nb + min(ch * C::KCB + j, nb - 1)];
-        }
-    };
-    auto store_chunk = [&](int ch) __attribute__((always_inline)) {
-        int dst;
-#pragma unroll
-        for (int i = 0; i < C::NW; ++i) {
-            const int idx = t + 256 * i;
-            (void)w_src(ch, min(idx, 16 * C::WCR - 1), dst);
-            if (idx < 16 * C::WCR) *reinterpret_cast<uint4 *>(lw + dst) = rw[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::NA; ++i) {
-            const int idx = t + 256 * i;
-            (void)a_src(ch, min(idx, C::TM * C::ACR - 1), dst);
-            if (idx < C::TM * C::ACR) *reinterpret_cast<uint4 *>(la + dst) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::ND; ++i) {
-            const int idx = t + 256 * i;
-            if (idx < C::TM * C::KCB) ld[idx] = rd[i];
-        }
-    };
-
-    float acc[TT];
-#pragma unroll
-    for (int i = 0; i < TT; ++i) acc[i] = 0.0f;
-
-    load_chunk(0);
-    for (int ch = 0; ch < nchunks; ++ch) {
-        store_chunk(ch);
-        lds_barrier();
-        if (ch + 1 < nchunks) load_chunk(ch + 1);
-        // the lane's weight row in LDS for this chunk (its 16-B misalignment)
-        const size_t off = size_t(ch) * C::KCB * F::BB;
-        const int mis = int(reinterpret_cast<uintptr_t>(a.w + size_t(min(n0 + nl, a.N - 1)) * a.row_bytes + off) & 15);
-        const uint8_t *wrow = lw + nl * C::WS + mis;
-        for (int it = wid; it < C::KCB * TT; it += 4) {
-            const int j = it / TT, tt = it - j * TT;
-            if (ch * C::KCB + j >= nb) continue;
-            const typename F::W wv = F::load_lds(wrow + j * F::BB, cl);
-            Scales<F> s;
-            decode_scales<F>(wv, s);
-            const int8_t *arow = la + (16 * tt + nl) * C::AS + j * F::QK;
-            int S[4] = {0, 0, 0, 0};
-            int4v Mb = {0, 0, 0, 0};
-#pragma unroll
-            for (int u = 0; u < F::NU; ++u) {
-                const uint2 av = ld8(arow + F::koff(u, cl));
-                const int4v D = mfma16x16x32(av, F::bop(wv, u, cl));
-                if constexpr (F::kMin) {
-                    const uint32_t mb = uint32_t(s.m[u]) * 0x01010101u;
-                    Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) S[r] += __mul24(s.sc[u], D[r]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = 16 * tt + 4 * cl + r;
-                const float dx = ld[tok * C::KCB + j];
-                float v;
-                if constexpr (F::kMin) v = dx * (s.d * (float)S[r] - s.dmin * (float)Mb[r]);  // E:11026
-                else v = (s.d * dx) * (float)S[r];                                            // E:11101 / E:3405
-                part[(j * C::TM + tok) * 16 + nl] = v;
-            }
-        }
-        lds_barrier();
-        // this chunk's blocks, in order
-#pragma unroll
-        for (int i = 0; i < TT; ++i) {
-            const int o = t + 256 * i;  // token o / 16, row o % 16
-            for (int j = 0; j < C::KCB && ch * C::KCB + j < nb; ++j) acc[i] += part[j * C::TM * 16 + o];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < TT; ++i) {
-        const int o = t + 256 * i;
-        const int tok = o >> 4, n = n0 + (o & 15);
-        if (tok < a.M && n < a.N) {
-            float v = acc[i];
-            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
-            a.y[size_t(tok) * a.ldy + n] = v;
-        }
-    }
-}
-
-template <class F, int TT>
-static hipError_t launch_small_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    using C = SmallM<F, TT>;
-    hipLaunchKernelGGL((mfma_small_kernel<F, TT>), dim3(unsigned((a.N + 15) / 16)), dim3(256),
-                       size_t(C::LDS), s, a, x);
+template <class C, class F>
+static hipError_t launch_tile_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    const dim3 grid(unsigned((a.N + C::ROWS - 1) / C::ROWS), unsigned((a.M + C::TOK - 1) / C::TOK));
+    hipLaunchKernelGGL((tile_kernel<C, F>), grid, dim3(256), size_t(C::LDS), s, a, x);
     return hipGetLastError();
 }
 
 template <class F>
-static hipError_t launch_small(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    switch ((a.M + 15) / 16) {
-        case 1: return launch_small_t<F, 1>(a, x, s);
-        case 2: return launch_small_t<F, 2>(a, x, s);
-        case 3: return launch_small_t<F, 3>(a, x, s);
-        default: return launch_small_t<F, 4>(a, x, s);
-    }
-}
-
-template <class F, int TT, int PF, int PA>
-static hipError_t launch_mfma_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    const dim3 grid(unsigned((a.N + 15) / 16), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
-    hipLaunchKernelGGL((mfma_kernel<F, TT, PF, PA>), grid, dim3(256), 0, s, a, x);
-    return hipGetLastError();
+static hipError_t launch_tile(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+    // buffer offsets are 32-bit with kFar past every range
+    if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
+    //                      WR WT PR PT KS TR PD  LDS budget
+    if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(a, x, s);
+    if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(a, x, s);
+    if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(a, x, s);
+    // Q6_K's 16 units per block: one row tile per wave (two would spill)
+    if constexpr (F::NU > 8) return launch_tile_t<TileCfg<F, 1, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(a, x, s);
+    else return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(a, x, s);
 }
 
 template <class F>
 static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    // large M: 4 token tiles per wave (2 for Q6_K, whose 16 units would spill)
-    constexpr int kTT = F::NU > 8 ? 2 : 4;
-    if (a.M <= 64) return launch_small<F>(a, x, s);
-    return launch_mfma_t<F, kTT, 1, 1>(a, x, s);
+    return launch_tile<F>(a, x, s);
 }
 
 hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
