@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <type_traits>
 
 namespace qmm {
 
@@ -231,5 +232,68 @@ __device__ inline void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2
 }
 
 #endif  // device compile
+
+// ------------------------------------------------ direct buffer -> LDS transfers
+// Operands reach LDS by buffer_load ... lds (16 or 4 B per lane, lane l's
+// bytes land at the LDS base + l * size): no registers, no address
+// clamps, since every transfer goes through a buffer descriptor whose
+// range ends exactly at the data (a lane past it reads zeros and touches
+// no memory). Transfers retire in order, so a kernel releases a chunk with
+// one static vmcnt wait.
+//
+// The transfers are written as inline assembly: the compiler tracks the
+// builtin form as an LDS store and answers every later LDS read with a
+// full vmcnt(0) wait (it cannot tell the slots apart), which would wait for
+// the chunk still in flight. The kernel orders them itself with explicit
+// vmcnt waits and barriers; inside the asm, M0 (the LDS destination) is set
+// and given its one wait state.
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+// buffer descriptor: base, stride 0, num_records bytes, raw 32-bit dwords
+__device__ inline v4i32 buf_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    v4i32 r;
+    r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(b)));
+    r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane(int(bytes));
+    r.w = 0x00020000;
+    return r;
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane(
+        uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p)));
+}
+// M0 is reserved to the compiler, which uses it in these kernels for nothing
+// else (no LDS transfers of its own, no message or interpolation ops).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// lane l's 16 B at byte offset voff of the buffer land at LDS byte address lds + 16 l
+__device__ inline void dma16(const v4i32 &r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
+}
+// lane l's 4 B land at lds + 4 l
+__device__ inline void dma4(const v4i32 &r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt vmcnt(N) (lgkmcnt and expcnt not waited on)
+template <int N> __device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0) only
+
+constexpr uint32_t kFar = 0x80000000u;  // a byte offset past every descriptor's range
+
+// fn(integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
+template <int B, int E, class Fn>
+__device__ inline __attribute__((always_inline)) void static_for(Fn &&fn) {
+    if constexpr (B < E) {
+        fn(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(fn);
+    }
+}
 
 }  // namespace qmm

@@ -208,51 +208,6 @@ __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
 // is computed, and an explicit vmcnt wait (transfers retire in order)
 // releases chunk ch. Every wave issues the same number of transfers per
 // chunk (surplus ones target a dump line), so the wait counts are static.
-// The transfers are written as inline assembly: the compiler tracks the
-// builtin form as an LDS store and answers every later LDS read with a
-// full vmcnt(0) wait (it cannot tell the slots apart), which would wait for
-// the chunk still in flight. The kernel orders them itself with explicit
-// vmcnt waits and barriers; inside the asm, M0 (the LDS destination) is set
-// and given its one wait state.
-typedef int v4i32 __attribute__((ext_vector_type(4)));
-
-// buffer descriptor: base, stride 0, num_records bytes, raw 32-bit dwords
-__device__ inline v4i32 buf_rsrc(const void *p, uint32_t bytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(p);
-    v4i32 r;
-    r.x = __builtin_amdgcn_readfirstlane(int(uint32_t(b)));
-    r.y = __builtin_amdgcn_readfirstlane(int(uint32_t(b >> 32) & 0xFFFFu));
-    r.z = __builtin_amdgcn_readfirstlane(int(bytes));
-    r.w = 0x00020000;
-    return r;
-}
-__device__ inline uint32_t lds_addr(const void *p) {
-    return __builtin_amdgcn_readfirstlane(
-        uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p)));
-}
-// M0 is reserved to the compiler, which uses it in these kernels for nothing
-// else (no LDS transfers of its own, no message or interpolation ops).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// lane l's 16 B at byte offset voff of the buffer land at LDS byte address lds + 16 l
-__device__ inline void dma16(const v4i32 &r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds"
-                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
-}
-// lane l's 4 B land at lds + 4 l
-__device__ inline void dma4(const v4i32 &r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds"
-                 : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// s_waitcnt vmcnt(N) (lgkmcnt and expcnt not waited on)
-template <int N> __device__ inline void wait_vmcnt() {
-    static_assert(N >= 0 && N <= 63, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0) only
-
-constexpr uint32_t kFar = 0x80000000u;  // a byte offset past every descriptor's range
 
 template <class F, int WR_, int WT_, int PR_, int PT_, int KS_, int TR_, int PD_, int BUDGET>
 struct TileCfg {
@@ -304,8 +259,10 @@ __global__ __launch_bounds__(256) void tile_kernel(MatArgs a, typename ActOf<F>:
     const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
     const uint32_t bl = uint32_t(wstart & 15);
     const int rows_valid = min(C::ROWS, a.N - n0);
+    // (the range is rounded up to whole 16-B granules: the range check is per
+    // dword, and a 2-B aligned format's last bytes may share one with the end)
     const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
-                              bl + uint32_t(rows_valid) * uint32_t(a.row_bytes));
+                              (bl + uint32_t(rows_valid) * uint32_t(a.row_bytes) + 15u) & ~15u);
     const v4i32 ra = buf_rsrc(x.qs, uint32_t(a.M) * uint32_t(K));
     const v4i32 rd = buf_rsrc(x.d, uint32_t(a.M) * uint32_t(nb) * 4u);
     const uint32_t lds0 = lds_addr(lds);

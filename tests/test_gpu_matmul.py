@@ -61,6 +61,14 @@ def test_mfma_small_shapes(ctx, oracle, type_id, M):
     _run(ctx, oracle, type_id, 77, 512, M, seed=M * 13 + type_id)
 
 
+@pytest.mark.parametrize("type_id,K", [(TYPE_Q6_K, 256), (TYPE_Q6_K, 768), (TYPE_Q8_0, 96), (TYPE_Q8_0, 160)])
+@pytest.mark.parametrize("M", [1, 3, 12, 30, 70])
+def test_unaligned_tensor_end(ctx, oracle, type_id, K, M):
+    """2-B aligned formats whose tensor (and a workgroup's last row) ends
+    inside a dword: the last bytes (Q6_K's d) must still be read."""
+    _run(ctx, oracle, type_id, 45, K, M, seed=500 + K + M)
+
+
 @pytest.mark.parametrize("M", [8, 16, 32, 64])
 def test_tree_verify_q4k(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
