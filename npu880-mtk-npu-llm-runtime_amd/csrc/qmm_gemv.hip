@@ -86,6 +86,56 @@ struct FmtQ4K {
     }
 };
 
+// Q4_K, 4 lanes per block (the form the library launches): lane k owns
+// the 64 values of chunk k — code bytes [16 + 32k, +32): low nibbles =
+// sub-block 2k, high nibbles = sub-block 2k+1. The wave's span is staged
+// through LDS with coalesced 16-B loads (16 blocks per wave step).
+// Scales / mins of sub-blocks 2k, 2k+1 (get_scale_min_k4, E:743-749) in the
+// two low bytes of SC / MM.
+__device__ inline void scale_pair_k4(int k, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &SC, uint32_t &MM) {
+    const uint32_t sh = 16u * uint32_t(k & 1);
+    const uint32_t A = s0 >> sh, B = s1 >> sh, C = s2 >> sh;
+    const uint32_t sc_lo = A & 0x3F3Fu, m_lo = B & 0x3F3Fu;                  // j < 4
+    const uint32_t sc_hi = (C & 0x0F0Fu) | ((A >> 2) & 0x3030u);             // j >= 4
+    const uint32_t m_hi = ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u);
+    SC = (k >= 2) ? sc_hi : sc_lo;
+    MM = (k >= 2) ? m_hi : m_lo;
+}
+struct FmtQ4K4 {
+    static constexpr int G = 4, BB = 144, QK = 256;
+    static constexpr bool kStaged = true;
+    struct Raw { uint4 h, c0, c1; };
+    struct Act { uint4 x0, x1, x2, x3; uint2 bs; float dx; };
+    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into the LDS stage
+        return {ld16(blk), ld16(blk + 16 + 32 * k), ld16(blk + 32 + 32 * k)};
+    }
+    __device__ static Act load_act(const LdsAct &x, int b, int k) {
+        const int8_t *xb = x.qs + b * 272 + 64 * k;
+        return {ld16(xb), ld16(xb + 16), ld16(xb + 32), ld16(xb + 48), ld8(x.bs + b * 8 + 2 * k), x.d[b]};
+    }
+    __device__ static float compute(const Raw &r, const Act &a, int k) {
+        uint32_t SC, MM;
+        scale_pair_k4(k, r.h.y, r.h.z, r.h.w, SC, MM);
+        const uint32_t M4 = 0x0F0F0F0Fu;
+        const uint32_t c[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+        const uint32_t xl[8] = {a.x0.x, a.x0.y, a.x0.z, a.x0.w, a.x1.x, a.x1.y, a.x1.z, a.x1.w};
+        const uint32_t xh[8] = {a.x2.x, a.x2.y, a.x2.z, a.x2.w, a.x3.x, a.x3.y, a.x3.z, a.x3.w};
+        int dot1 = 0, dot2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            dot1 = sdot4(int(c[i] & M4), int(xl[i]), dot1);
+            dot2 = sdot4(int((c[i] >> 4) & M4), int(xh[i]), dot2);
+        }
+        int S = __mul24(int(SC & 0xFF), dot1) + __mul24(int(SC >> 8), dot2);
+        int Mb = __mul24(int(MM & 0xFF), int(a.bs.x)) + __mul24(int(MM >> 8), int(a.bs.y));
+        S = group4_sum(S);
+        Mb = group4_sum(Mb);
+        const float d = fp16_bits_to_f32(r.h.x & 0xFFFFu);
+        const float dmin = fp16_bits_to_f32(r.h.x >> 16);
+        return a.dx * (d * (float)S - dmin * (float)Mb);  // E:11026
+    }
+};
+
 // ----------------------------------------------------------------- Q5_K
 // Block (176 B): d @0, dmin @2, scales[12] @4, qh[32] @16, ql[128] @48.
 // Lane k: chunk j = k/2, half lh = k%2 -> ql bytes [48 + 32j + 16lh, +16),
@@ -460,7 +510,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, const float *__res
 
 size_t gemv_lds_bytes(uint32_t type, int K) {
     switch (type) {
-        case kQ4_K: return gemv_lds_bytes_t<FmtQ4K, kGemvR, kGemvU>(K);
+        case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K);
         case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, kGemvR, kGemvU>(K);
         case kQ6_K: return gemv_lds_bytes_t<FmtQ6K, kGemvR, kGemvU>(K);
         case kQ8_0: return gemv_lds_bytes_t<FmtQ80, kGemvR, kGemvU>(K);
@@ -484,7 +534,7 @@ static hipError_t launch_gemv_t(const MatArgs &a, const float *x32, const Q8KVie
 hipError_t launch_gemv(uint32_t type, const MatArgs &a, const float *x32, const Q8KView &xk,
                        const Q80View &x0, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_gemv_t<FmtQ4K, kGemvR, kGemvU>(a, x32, xk, x0, s);
+        case kQ4_K: return launch_gemv_t<FmtQ4K4, kGemvR, 3>(a, x32, xk, x0, s);
         case kQ5_K: return launch_gemv_t<FmtQ5K, kGemvR, kGemvU>(a, x32, xk, x0, s);
         case kQ6_K: return launch_gemv_t<FmtQ6K, kGemvR, kGemvU>(a, x32, xk, x0, s);
         case kQ8_0: return launch_gemv_t<FmtQ80, kGemvR, kGemvU>(a, x32, xk, x0, s);
