@@ -210,6 +210,28 @@ def bench_prefill(ctx, steps):
             "prefill_tokens_per_s": round(M / (36 * per_layer), 1), "replicas": R}
 
 
+def bench_rmsnorm_gemv(ctx, steps):
+    """The decode projection with its producer fused: RMSNorm -> Q8_K
+    (qmm_rmsnorm_q8k) then the Q4_K 9728 x 2560 GEMV on the prequantized
+    row, against the RMSNorm alone (M = 1, K = 2560)."""
+    N, K = synth.GEMV_Q4K["N"], synth.GEMV_Q4K["K"]
+    w = Replicated(ctx, synth.TYPE_Q4_K, N, K, max(1, math.ceil(ROTATE_BYTES / (N * 1440))), 0)
+    x = ctx.upload(synth.activations(1, K, seed=1))
+    gm = ctx.upload(np.random.default_rng(2).uniform(0.5, 1.5, K).astype(np.float32))
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, K))
+    y = ctx.malloc(N * 4)
+    ms_norm = timed(ctx, lambda i: ctx.rmsnorm_q8k(x, gm, 1, K, None, q), steps, 10)
+
+    def step(i):
+        ctx.rmsnorm_q8k(x, gm, 1, K, None, q)
+        ctx.gemm_multi_dispatch_prequantized(q, None, 1, K, [w.task(i, y, N)])
+
+    ms = timed(ctx, step, steps, 10)
+    for b in (w.buf, x, gm, q, y):
+        ctx.free(b)
+    return {"us_rmsnorm_q8k": round(ms_norm * 1e3, 3), "us_rmsnorm_then_gemv": round(ms * 1e3, 3)}
+
+
 def launch_floor(ctx, steps):
     """µs per launch of the smallest kernel the library has (Q8_K quantizer
     of one 256-value block), graph-captured: the per-launch floor."""
@@ -362,6 +384,8 @@ def main():
         log(f"FFN block: {extra['ffn_block_q4k_q6k']}")
         extra["prefill_layer_m512"] = bench_prefill(ctx, max(5, args.steps // 200))
         log(f"prefill layer M=512: {extra['prefill_layer_m512']}")
+        extra["rmsnorm_q8k_then_gemv_q4k_9728x2560"] = bench_rmsnorm_gemv(ctx, max(200, args.steps // 4))
+        log(f"RMSNorm->Q8_K + GEMV: {extra['rmsnorm_q8k_then_gemv_q4k_9728x2560']}")
         extra["launch_floor_us"] = launch_floor(ctx, max(200, args.steps // 4))
         log(f"launch floor: {extra['launch_floor_us']} us")
         lm = Workload(ctx, synth.TYPE_Q6_K, 151936, 2560, 1, 2, seed=20)

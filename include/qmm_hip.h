@@ -122,6 +122,13 @@ int qmm_quantize_q8_0(qmm_context *ctx, const float *x, int M, int K, void *q80_
  * Q8_K quantizer per 256 values; gate/up/h are [M][N]. h_out may be NULL. */
 int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, int N,
                    float *h_out, void *q8k_out);
+/* rmsnorm_fp16_rows_fast (E:4264-4314) with its Q8_K output (E:4303-4305,
+ * the producer that sets the prequantized flag, E:4312): per row of x
+ * [M][K], y = fp16(x * inv_rms * gamma), inv_rms = 1 / sqrt(mean(x^2) +
+ * 1e-6), then the Q8_K quantizer of y; x and gamma are rounded to fp16
+ * first. y_out [M][K] may be NULL. K % 256 == 0, K <= 16384. */
+int qmm_rmsnorm_q8k(qmm_context *ctx, const float *x, const float *gamma, int M, int K,
+                    float *y_out, void *q8k_out);
 
 /* -------------------------------------------------------------- dequant */
 /* dequant_contiguous_fast (E:3856-3902): rows x cols packed blocks -> fp16

@@ -360,6 +360,20 @@ int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, 
     return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "swiglu launch");
 }
 
+int qmm_rmsnorm_q8k(qmm_context *ctx, const float *x, const float *gamma, int M, int K, float *y_out,
+                    void *q8k_out) {
+    if (!ctx) return QMM_EINVAL;
+    if (!x || !gamma || !q8k_out || M <= 0 || K <= 0) return fail(ctx, QMM_EINVAL, "bad rmsnorm arguments");
+    if (K % 256) return fail(ctx, QMM_ESHAPE, "K must be a multiple of 256");
+    if (K > 16384) return fail(ctx, QMM_ESHAPE, "K above 16384");
+    if (!aligned(x, 16) || !aligned(gamma, 16) || !aligned(q8k_out, 16) || (y_out && !aligned(y_out, 16)))
+        return fail(ctx, QMM_EALIGN, "rmsnorm buffers must be 16-B aligned");
+    int rc = use_device(ctx);
+    if (rc) return rc;
+    hipError_t e = qmm::launch_rmsnorm_q8k(x, gamma, M, K, y_out, q8k_out, ctx->stream);
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "rmsnorm launch");
+}
+
 int qmm_dequantize_f16(qmm_context *ctx, const void *w_blocks, uint32_t type, int64_t rows,
                        int64_t cols, uint16_t *dst) {
     if (!ctx) return QMM_EINVAL;

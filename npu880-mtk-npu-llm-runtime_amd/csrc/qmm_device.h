@@ -75,6 +75,8 @@ hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStrea
 hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStream_t s);
 hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                              void *out, hipStream_t s);
+hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, float *y,
+                              void *out, hipStream_t s);
 hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
                               uint16_t *dst, hipStream_t s);
 // M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;

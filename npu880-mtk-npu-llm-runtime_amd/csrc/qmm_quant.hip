@@ -81,6 +81,59 @@ __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict
                     round_to_fp16(r.w), lane, blk, qs, d, bs);
 }
 
+// rmsnorm_fp16_rows_fast (E:4264-4314) + its Q8_K (E:4303-4305): one
+// workgroup per row. Thread t owns the float4s t + 256 j (values 4t + 1024 j
+// .. +3), so wave w holds the 256-value block 4j + w of the row for the
+// quantizer. The sum of squares is a tree over threads (not the reference's
+// row order: the last bits of inv_rms may differ, so y is compared with a
+// tolerance and the codes by composition); inv_rms = 1 / sqrtf(sum * (1/K)
+// + 1e-6f) and y = fp16((x * inv_rms) * gamma) as in E:4295-4302.
+template <int NJ>
+__global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ gamma, int K,
+                                                          float *__restrict__ y, int8_t *__restrict__ qs,
+                                                          float *__restrict__ d,
+                                                          int32_t *__restrict__ bs) {
+    __shared__ float part[4];
+    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    const size_t m = blockIdx.x;
+    const float *xr = x + m * size_t(K);
+    const int nq = K >> 2;  // float4s in the row
+    float4 h[NJ];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int q = t + 256 * j;
+        const float4 v = q < nq ? reinterpret_cast<const float4 *>(xr)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        h[j] = make_float4(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z), round_to_fp16(v.w));
+        s += h[j].x * h[j].x;
+        s += h[j].y * h[j].y;
+        s += h[j].z * h[j].z;
+        s += h[j].w * h[j].w;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) part[wid] = s;
+    __syncthreads();
+    const float sum_sq = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv_k = 1.0f / (float)K;
+    const float inv_rms = 1.0f / sqrtf(sum_sq * inv_k + 1.0e-6f);  // E:4295
+    const size_t nbk = size_t(K) >> 8;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int q = t + 256 * j;
+        if (4 * (256 * j + 64 * wid) >= K) break;  // whole waves past the row's end
+        const float4 g = reinterpret_cast<const float4 *>(gamma)[q];
+        float4 r;
+        r.x = round_to_fp16(h[j].x * inv_rms * round_to_fp16(g.x));  // E:4301
+        r.y = round_to_fp16(h[j].y * inv_rms * round_to_fp16(g.y));
+        r.z = round_to_fp16(h[j].z * inv_rms * round_to_fp16(g.z));
+        r.w = round_to_fp16(h[j].w * inv_rms * round_to_fp16(g.w));
+        if (y) reinterpret_cast<float4 *>(y + m * size_t(K))[q] = r;
+        store_q8k_block(r.x, r.y, r.z, r.w, lane, m * nbk + size_t(4 * j + wid), qs, d, bs);
+    }
+}
+
 // ---------------------------------------------------------------- dequant
 // One thread per 32-value group (a K-quant sub-block or a Q8_0 block);
 // formulas of dequant_block_q4_k/q5_k/q6_k/q8_0 scalar branches
@@ -177,6 +230,25 @@ hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, f
     hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(grid), dim3(256), 0, s, gate, up, nblk, h,
                        reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
                        reinterpret_cast<int32_t *>(base + L.bs_off));
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, float *y,
+                              void *out, hipStream_t s) {
+    const Q8KLayout L(M, K);
+    uint8_t *base = static_cast<uint8_t *>(out);
+    int8_t *qs = reinterpret_cast<int8_t *>(base);
+    float *d = reinterpret_cast<float *>(base + L.d_off);
+    int32_t *bs = reinterpret_cast<int32_t *>(base + L.bs_off);
+    const int nj = (K / 4 + 255) / 256;  // float4s per thread
+#define QMM_RMS(NJ) \
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel<NJ>, dim3(unsigned(M)), dim3(256), 0, s, x, gamma, K, y, qs, d, bs)
+    if (nj <= 3) QMM_RMS(3);
+    else if (nj <= 4) QMM_RMS(4);
+    else if (nj <= 10) QMM_RMS(10);
+    else if (nj <= 16) QMM_RMS(16);
+    else return hipErrorInvalidValue;
+#undef QMM_RMS
     return hipGetLastError();
 }
 

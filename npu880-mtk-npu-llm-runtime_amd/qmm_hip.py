@@ -77,6 +77,7 @@ _SIGNATURES = [
     ("qmm_quantize_q8k", C.c_int, [_p, _p, C.c_int, C.c_int, _p]),
     ("qmm_quantize_q8_0", C.c_int, [_p, _p, C.c_int, C.c_int, _p]),
     ("qmm_swiglu_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
+    ("qmm_rmsnorm_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_dequantize_f16", C.c_int, [_p, _p, C.c_uint32, C.c_int64, C.c_int64, _p]),
     ("qmm_gemm_multi_dispatch", C.c_int, [_p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_gemm_multi_dispatch_prequantized", C.c_int,
@@ -265,6 +266,10 @@ class Context:
 
     def quantize_q8_0(self, x, M: int, K: int, out):
         self._call("qmm_quantize_q8_0", self._h, _p(_addr(x)), M, K, _p(_addr(out)))
+
+    def rmsnorm_q8k(self, x, gamma, M: int, K: int, y_out, out):
+        self._call("qmm_rmsnorm_q8k", self._h, _p(_addr(x)), _p(_addr(gamma)), M, K,
+                   _p(_addr(y_out)), _p(_addr(out)))
 
     def swiglu_q8k(self, gate, up, M: int, N: int, h_out, out):
         self._call("qmm_swiglu_q8k", self._h, _p(_addr(gate)), _p(_addr(up)), M, N,

@@ -85,6 +85,7 @@ class Oracle:
         L.qo_gemm_multi_prequantized.argtypes = [_p, _p, _p, _p, _p, C.c_int, C.c_int,
                                                  C.POINTER(_MatrixTask), C.c_int]
         L.qo_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
+        L.qo_rmsnorm_q8k_f16.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
 
     # fp16 ----------------------------------------------------------------
     def f32_to_fp16(self, x) -> np.ndarray:
@@ -231,6 +232,26 @@ class Oracle:
         self.lib.qo_swiglu_q8k(_ptr(gate), _ptr(up), M, N, _ptr(h), _ptr(d), _ptr(qs), _ptr(bs))
         return h, (d, qs, bs)
 
+    def rmsnorm_q8k_f16(self, x16: np.ndarray, gamma16: np.ndarray):
+        """rmsnorm_fp16_rows_fast on fp16 bits: (y16 [M][K], (d, qs, bsum32))."""
+        x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+        gamma16 = np.ascontiguousarray(gamma16, dtype=np.uint16)
+        if x16.ndim == 1:
+            x16 = x16[None, :]
+        M, K = x16.shape
+        y = np.empty((M, K), np.uint16)
+        d = np.empty((M, K // 256), np.float32)
+        qs = np.empty((M, K), np.int8)
+        bs = np.empty((M, K // 32), np.int32)
+        self.lib.qo_rmsnorm_q8k_f16(_ptr(x16), _ptr(gamma16), M, K, _ptr(y), _ptr(d), _ptr(qs), _ptr(bs))
+        return y, (d, qs, bs)
+
+    def rmsnorm_q8k(self, x: np.ndarray, gamma: np.ndarray):
+        """The fp32 contract: x and gamma rounded to fp16 first; y as fp32."""
+        y16, q = self.rmsnorm_q8k_f16(self.f32_to_fp16(np.asarray(x, np.float32)),
+                                      self.f32_to_fp16(np.asarray(gamma, np.float32)))
+        return self.fp16_to_f32(y16), q
+
 
 class Reference:
     """The reference's own scalar code compiled in place (oracle/_ref/libref.so)."""
@@ -254,6 +275,8 @@ class Reference:
         L.ref_dot_rows.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p]
         L.ref_swiglu_q8k.restype = C.c_int
         L.ref_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p]
+        L.ref_rmsnorm_q8k.restype = C.c_int
+        L.ref_rmsnorm_q8k.argtypes = [_p, _p, _p, C.c_int, C.c_int, _p, _p, _p]
         L.ref_bench_gemv.restype = C.c_double
         L.ref_bench_gemv.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, C.c_int, C.c_int]
         self.max_k = L.ref_capacity_k()
@@ -329,6 +352,21 @@ class Reference:
         if rc != 0:
             raise ValueError("outside the reference's static capacity")
         return g, (d, qs, bs)
+
+    def rmsnorm_q8k(self, x16: np.ndarray, gamma16: np.ndarray):
+        x = np.ascontiguousarray(x16, dtype=np.uint16)
+        gm = np.ascontiguousarray(gamma16, dtype=np.uint16)
+        if x.ndim == 1:
+            x = x[None, :]
+        M, K = x.shape
+        y = np.empty((M, K), np.uint16)
+        d = np.empty((M, K // 256), np.float32)
+        qs = np.empty((M, K), np.int8)
+        bs = np.empty((M, K // 32), np.int32)
+        rc = self.lib.ref_rmsnorm_q8k(_ptr(x), _ptr(gm), _ptr(y), M, K, _ptr(d), _ptr(qs), _ptr(bs))
+        if rc != 0:
+            raise ValueError("outside the reference's static capacity")
+        return y, (d, qs, bs)
 
     def bench_gemv(self, type_id: int, w: np.ndarray, N: int, K: int, x16: np.ndarray,
                    threads: int, iters: int):

@@ -28,6 +28,10 @@
  *   qo_swiglu_q8k                    composition: h vs numpy fp64 SiLU*up
  *                                    (tolerance; expf differs between libms),
  *                                    codes vs qo_quantize_q8k_f32(h).
+ *   qo_rmsnorm_q8k_f16               bit-exact vs the compiled reference's
+ *                                    rmsnorm_fp16_rows_fast (y and Q8_K);
+ *                                    closed forms (constant rows, unit gamma)
+ *                                    and fp64 RMS within fp16 rounding.
  */
 #include "qmm_oracle.h"
 
@@ -620,5 +624,30 @@ void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
             qo_quantize_q8k_f32(hb, 1, 256, d + (size_t)m * nb + b, qs + off,
                                 bsum32 + ((size_t)m * nb + b) * 8);
         }
+    }
+}
+
+/* ------------------------------------------------------------ rmsnorm -- */
+
+/* rmsnorm_fp16_rows_fast scalar branch (E:4292-4302): sum of squares in row
+ * order, inv_rms = 1 / sqrtf(sum * (1/K) + 1e-6f), y = fp16(x * inv_rms *
+ * gamma), then the row's Q8_K (E:4303-4305). x, gamma, y are fp16 bits. */
+void qo_rmsnorm_q8k_f16(const uint16_t *x, const uint16_t *gamma, int M, int K, uint16_t *y,
+                        float *d, int8_t *qs, int32_t *bsum32) {
+    const float inv_k = 1.0f / (float)K;
+    const int nb = K / 256;
+    for (int m = 0; m < M; ++m) {
+        const uint16_t *xr = x + (size_t)m * K;
+        uint16_t *yr = y + (size_t)m * K;
+        float sum_sq = 0.0f;
+        for (int i = 0; i < K; ++i) {
+            const float v = qo_fp16_to_f32(xr[i]);
+            sum_sq += v * v;
+        }
+        const float inv_rms = 1.0f / sqrtf(sum_sq * inv_k + 1.0e-6f);
+        for (int i = 0; i < K; ++i)
+            yr[i] = qo_f32_to_fp16(qo_fp16_to_f32(xr[i]) * inv_rms * qo_fp16_to_f32(gamma[i]));
+        qo_quantize_row_q8k_f16(yr, K, d + (size_t)m * nb, qs + (size_t)m * K,
+                                bsum32 + (size_t)m * nb * 8);
     }
 }

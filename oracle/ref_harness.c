@@ -156,6 +156,22 @@ int ref_swiglu_q8k(uint16_t *gate_inout, const uint16_t *up, int M, int N, float
     return 0;
 }
 
+/* rmsnorm_fp16_rows_fast (E:4264-4314), scalar branch under this build:
+ * y rows out, and the Q8_K rows it leaves in g_sdot_input.q8k copied out. */
+int ref_rmsnorm_q8k(const uint16_t *x, const uint16_t *gamma, uint16_t *y, int M, int K,
+                    float *d, int8_t *qs, int32_t *bsum32) {
+    if (M < 1 || M > SDOT_MAX_BATCH || K % 256 || K > SDOT_MAX_K) return -1;
+    const int nb = K / 256;
+    rmsnorm_fp16_rows_fast((const __fp16 *)x, (const __fp16 *)gamma, (__fp16 *)y, M, K);
+    for (int m = 0; m < M; ++m)
+        for (int b = 0; b < nb; ++b) {
+            d[(size_t)m * nb + b] = g_sdot_input.q8k[m][b].d;
+            memcpy(qs + (size_t)m * K + (size_t)b * 256, g_sdot_input.q8k[m][b].qs, 256);
+            memcpy(bsum32 + ((size_t)m * nb + b) * 8, g_sdot_input.q8k[m][b].bsum32, 32);
+        }
+    return 0;
+}
+
 /* ---------------------------------------------------------------------------
  * CPU baseline: the reference's portable batch-1 path for one projection —
  * quantize_row_fp16_to_q8_k of x once, then eval_single_lm_row_dot per

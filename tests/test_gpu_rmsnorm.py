@@ -1,0 +1,58 @@
+"""RMSNorm -> Q8_K on the HIP path. The sum of squares is a tree on the GPU
+and row order in the reference, so y is compared with a tolerance; the
+codes are checked by composition (the oracle's quantizer on the GPU's y,
+bit-exact), and against the oracle's own codes wherever y agrees."""
+import numpy as np
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (1, 2560), (4, 4096), (3, 9728), (2, 16384)])
+def test_rmsnorm_q8k(ctx, oracle, M, K):
+    say(f"rmsnorm_q8k M={M} K={K}")
+    g = np.random.default_rng(M * 7 + K)
+    x = (g.standard_normal((M, K)) * 3).astype(np.float32)
+    if M > 1:
+        x[1] *= 1e-3  # mean square near the epsilon
+    gamma = g.uniform(0.5, 1.5, K).astype(np.float32)
+    xb, gb = ctx.upload(x), ctx.upload(gamma)
+    yb = ctx.malloc(M * K * 4)
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.rmsnorm_q8k(xb, gb, M, K, yb, q)
+    ctx.sync()
+    y = ctx.d2h(yb, np.float32, (M, K))
+    d, qs, bs = ctx.read_q8k(q, M, K)
+    ry, (rd, rqs, rbs) = oracle.rmsnorm_q8k(x, gamma)
+    # y: fp16 values; the summation order only moves inv_rms by a few ulps
+    assert np.array_equal(y, oracle.fp16_to_f32(oracle.f32_to_fp16(y))), "y must be fp16 values"
+    rel = np.abs(y - ry) / np.maximum(np.abs(ry), 6.1e-5)
+    assert rel.max() <= 1e-3, rel.max()
+    assert np.mean(y != ry) < 0.01
+    # codes by composition: bit-exact
+    ed, eqs, ebs = oracle.quantize_q8k(y)
+    assert np.array_equal(d.view(np.uint32), ed.view(np.uint32))
+    assert np.array_equal(qs, eqs) and np.array_equal(bs, ebs)
+    # and equal to the oracle's own codes in every block where y agrees
+    same = (y == ry).reshape(M, K // 256, 256).all(axis=2)
+    assert np.array_equal(qs.reshape(M, -1, 256)[same], rqs.reshape(M, -1, 256)[same])
+    for b in (xb, gb, yb, q):
+        ctx.free(b)
+
+
+def test_rmsnorm_without_y(ctx, oracle):
+    M, K = 2, 2560
+    x = np.random.default_rng(1).standard_normal((M, K)).astype(np.float32)
+    gamma = np.ones(K, np.float32)
+    xb, gb = ctx.upload(x), ctx.upload(gamma)
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.rmsnorm_q8k(xb, gb, M, K, None, q)
+    ctx.sync()
+    d, qs, bs = ctx.read_q8k(q, M, K)
+    ry, _ = oracle.rmsnorm_q8k(x, gamma)
+    ed, eqs, ebs = oracle.quantize_q8k(ry)
+    assert np.mean(qs != eqs) < 0.01
+    for b in (xb, gb, q):
+        ctx.free(b)
