@@ -232,6 +232,39 @@ def bench_rmsnorm_gemv(ctx, steps):
     return {"us_rmsnorm_q8k": round(ms_norm * 1e3, 3), "us_rmsnorm_then_gemv": round(ms * 1e3, 3)}
 
 
+def bench_lm_head_argmax(ctx, steps):
+    """The LM head with its argmax epilogue (Q6_K 151936 x 2560, M = 1,
+    prequantized row): one call over all rows, and the reference's chunking
+    (24832-row chunks chained through the running best)."""
+    N, K = synth.GEMV_Q6K_LMHEAD["N"], synth.GEMV_Q6K_LMHEAD["K"]
+    w = Replicated(ctx, synth.TYPE_Q6_K, N, K, 2, 20)
+    rb = synth.row_bytes(synth.TYPE_Q6_K, K)
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, K))
+    ctx.quantize_q8k(ctx.upload(synth.activations(1, K, seed=21)), 1, K, q)
+    bv, bi = ctx.upload(np.full(1, -1e30, np.float32)), ctx.upload(np.zeros(1, np.uint32))
+
+    def one(i):
+        base = w.buf.ptr + (i % w.R) * w.stride
+        ctx.lm_head_argmax(q, None, 1, K, base, synth.TYPE_Q6_K, N, 0, None, bv, bi)
+
+    def chunked(i):
+        base = w.buf.ptr + (i % w.R) * w.stride
+        for r0 in range(0, N, 24832):
+            rows = min(24832, N - r0)
+            ctx.lm_head_argmax(q, None, 1, K, base + r0 * rb, synth.TYPE_Q6_K, rows, r0, None, bv, bi)
+
+    one(0)
+    chunked(0)
+    ctx.sync()
+    ms1 = timed(ctx, one, steps, 3)
+    ms7 = timed(ctx, chunked, steps, 3)
+    for b in (w.buf, q, bv, bi):
+        ctx.free(b)
+    byts = N * rb
+    return {"us_one_call": round(ms1 * 1e3, 2), "us_7_chunks": round(ms7 * 1e3, 2),
+            "gbs_one_call": round(byts / (ms1 * 1e-3) / 1e9, 1)}
+
+
 def launch_floor(ctx, steps):
     """µs per launch of the smallest kernel the library has (Q8_K quantizer
     of one 256-value block), graph-captured: the per-launch floor."""
@@ -386,6 +419,8 @@ def main():
         log(f"prefill layer M=512: {extra['prefill_layer_m512']}")
         extra["rmsnorm_q8k_then_gemv_q4k_9728x2560"] = bench_rmsnorm_gemv(ctx, max(200, args.steps // 4))
         log(f"RMSNorm->Q8_K + GEMV: {extra['rmsnorm_q8k_then_gemv_q4k_9728x2560']}")
+        extra["lm_head_argmax_q6k_151936x2560"] = bench_lm_head_argmax(ctx, max(20, args.steps // 20))
+        log(f"LM head + argmax: {extra['lm_head_argmax_q6k_151936x2560']}")
         extra["launch_floor_us"] = launch_floor(ctx, max(200, args.steps // 4))
         log(f"launch floor: {extra['launch_floor_us']} us")
         lm = Workload(ctx, synth.TYPE_Q6_K, 151936, 2560, 1, 2, seed=20)

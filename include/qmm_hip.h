@@ -130,6 +130,27 @@ int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, 
 int qmm_rmsnorm_q8k(qmm_context *ctx, const float *x, const float *gamma, int M, int K,
                     float *y_out, void *q8k_out);
 
+/* -------------------------------------------------------- LM-head epilogue */
+/* One vocabulary chunk of the LM head (run_final_norm_and_lm_head_batch_sdot,
+ * E:11150-11184): logits of rows [row_base, row_base + rows) of the tensor
+ * (w_rows points at row row_base) for the M prequantized activation rows,
+ * then, per token m, the reference's running argmax over the chunk's logits
+ * rounded to fp16, in row order with a strictly greater test:
+ * (best_val[m], best_id[m]) are read and updated in place (the caller seeds
+ * them, e.g. -1e30 / 0, and chains chunks). logits_out [M][rows] receives the
+ * fp32 sums, or may be NULL (library scratch). q80 is needed only for Q8_0. */
+int qmm_lm_head_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
+                       const void *w_rows, uint32_t type, int rows, uint32_t row_base,
+                       float *logits_out, float *best_val, uint32_t *best_id);
+/* Indexed rows (the pre-evaluated candidate / end-of-text rows, E:11141-11148,
+ * and the extended-script row lists, exec_cyrillic_lm_work_item E:9473-9579):
+ * the fp32 dots of rows row_ids[0..n_ids) (device array) of the tensor at
+ * w_tensor, and the running argmax over them in list order, fp32 values,
+ * strictly greater; best_id receives row ids. vals_out [M][n_ids] may be NULL. */
+int qmm_eval_rows_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
+                         const void *w_tensor, uint32_t type, const uint32_t *row_ids, int n_ids,
+                         float *vals_out, float *best_val, uint32_t *best_id);
+
 /* -------------------------------------------------------------- dequant */
 /* dequant_contiguous_fast (E:3856-3902): rows x cols packed blocks -> fp16
  * bits [rows][cols] (for validation; not on the matmul path). */

@@ -24,6 +24,8 @@ struct qmm_context {
     hipStream_t stream = nullptr;
     void *act = nullptr;  // Q8_K + Q8_0 activation buffers of the dispatcher
     size_t act_cap = 0;
+    void *lm = nullptr;   // LM-head epilogue scratch: logits | argmax slices | gathered rows
+    size_t lm_cap = 0;
     bool capturing = false;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::string err;
@@ -78,6 +80,73 @@ int ensure_act(qmm_context *ctx, size_t bytes) {
     }
     ctx->act_cap = bytes;
     return QMM_OK;
+}
+
+int ensure_lm(qmm_context *ctx, size_t bytes) {
+    if (bytes <= ctx->lm_cap) return QMM_OK;
+    if (ctx->capturing)
+        return fail(ctx, QMM_ENOMEM, "LM-head scratch too small during graph capture: run once before capturing");
+    if (ctx->lm) {
+        (void)hipStreamSynchronize(ctx->stream);
+        hipError_t e = hipFree(ctx->lm);
+        ctx->lm = nullptr;
+        ctx->lm_cap = 0;
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
+    }
+    hipError_t e = hipMalloc(&ctx->lm, bytes);
+    if (e != hipSuccess) {
+        ctx->lm = nullptr;
+        (void)hipGetLastError();
+        return fail(ctx, QMM_ENOMEM, "hipMalloc of LM-head scratch failed");
+    }
+    ctx->lm_cap = bytes;
+    return QMM_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// the LM-head epilogue: rows of one tensor (contiguous, or gathered by id)
+// on prequantized activations, then the running argmax update
+int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w, uint32_t type,
+              int rows, uint32_t row_base, const uint32_t *ids, float *logits_out, float *best_val,
+              uint32_t *best_id) {
+    if (!ctx) return QMM_EINVAL;
+    if (!w || !best_val || !best_id || M <= 0 || K <= 0 || rows <= 0)
+        return fail(ctx, QMM_EINVAL, "bad LM-head arguments");
+    if (!supported(type)) return fail(ctx, QMM_ETYPE, "unsupported ggml type");
+    if (!aligned(best_val, 4) || !aligned(best_id, 4)) return fail(ctx, QMM_EALIGN, "best_val/best_id must be 4-B aligned");
+    const size_t rb = qmm_row_bytes(type, K);
+    const size_t logit_b = logits_out ? 0 : align256(size_t(M) * rows * 4);
+    const size_t part_b = align256(qmm::argmax_scratch_bytes(M, rows));
+    const size_t gather_b = ids ? align256(size_t(rows) * rb) : 0;
+    int rc = use_device(ctx);
+    if (rc) return rc;
+    if ((rc = ensure_lm(ctx, logit_b + part_b + gather_b))) return rc;
+    uint8_t *scr = static_cast<uint8_t *>(ctx->lm);
+    float *logits = logits_out ? logits_out : reinterpret_cast<float *>(scr);
+    void *part = scr + logit_b;
+    const void *wrows = w;
+    if (ids) {
+        uint8_t *g = scr + logit_b + part_b;
+        hipError_t e = qmm::launch_gather_rows(static_cast<const uint8_t *>(w), rb, ids, rows, g, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "row gather launch");
+        wrows = g;
+    }
+    qmm_matrix_task t{};
+    t.w_base = wrows;
+    t.type = type;
+    t.row_bytes = rb;
+    t.dst = logits;
+    t.dst_stride = size_t(rows);
+    t.residual = nullptr;
+    t.res_stride = 0;
+    t.rows = rows;
+    t.cols = K;
+    rc = qmm_gemm_multi_dispatch_prequantized(ctx, q8k, q80, M, K, &t, 1);
+    if (rc) return rc;
+    hipError_t e = qmm::launch_argmax(logits, M, rows, size_t(rows), /*round16=*/ids == nullptr, ids, row_base,
+                                      best_val, best_id, part, ctx->stream);
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "argmax launch");
 }
 
 // Validate the task list against (M, K) and assign start_row.
@@ -213,6 +282,7 @@ int qmm_destroy(qmm_context *ctx) {
     (void)use_device(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->act) (void)hipFree(ctx->act);
+    if (ctx->lm) (void)hipFree(ctx->lm);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -424,6 +494,19 @@ int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, cons
     if ((rc = use_device(ctx))) return rc;
     return run_tasks(ctx, nullptr, need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, M, K, tasks,
                      n_tasks);
+}
+
+int qmm_lm_head_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_rows,
+                       uint32_t type, int rows, uint32_t row_base, float *logits_out, float *best_val,
+                       uint32_t *best_id) {
+    return lm_argmax(ctx, q8k, q80, M, K, w_rows, type, rows, row_base, nullptr, logits_out, best_val, best_id);
+}
+
+int qmm_eval_rows_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_tensor,
+                         uint32_t type, const uint32_t *row_ids, int n_ids, float *vals_out, float *best_val,
+                         uint32_t *best_id) {
+    if (ctx && !row_ids) return fail(ctx, QMM_EINVAL, "row_ids is NULL");
+    return lm_argmax(ctx, q8k, q80, M, K, w_tensor, type, n_ids, 0, row_ids, vals_out, best_val, best_id);
 }
 
 int qmm_graph_begin(qmm_context *ctx) {

@@ -77,6 +77,13 @@ hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, f
                              void *out, hipStream_t s);
 hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, float *y,
                               void *out, hipStream_t s);
+// LM-head epilogue (qmm_lmhead.hip)
+size_t argmax_scratch_bytes(int M, int rows);
+hipError_t launch_argmax(const float *logits, int M, int rows, size_t ldl, bool round16,
+                         const uint32_t *ids, uint32_t row_base, float *best_val, uint32_t *best_id,
+                         void *scratch, hipStream_t s);
+hipError_t launch_gather_rows(const uint8_t *w, size_t row_bytes, const uint32_t *ids, int n, uint8_t *dst,
+                              hipStream_t s);
 hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
                               uint16_t *dst, hipStream_t s);
 // M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;

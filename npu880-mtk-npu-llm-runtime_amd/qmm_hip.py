@@ -78,6 +78,10 @@ _SIGNATURES = [
     ("qmm_quantize_q8_0", C.c_int, [_p, _p, C.c_int, C.c_int, _p]),
     ("qmm_swiglu_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_rmsnorm_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
+    ("qmm_lm_head_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int, C.c_uint32,
+                                     _p, _p, _p]),
+    ("qmm_eval_rows_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, _p, C.c_int,
+                                       _p, _p, _p]),
     ("qmm_dequantize_f16", C.c_int, [_p, _p, C.c_uint32, C.c_int64, C.c_int64, _p]),
     ("qmm_gemm_multi_dispatch", C.c_int, [_p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_gemm_multi_dispatch_prequantized", C.c_int,
@@ -270,6 +274,17 @@ class Context:
     def rmsnorm_q8k(self, x, gamma, M: int, K: int, y_out, out):
         self._call("qmm_rmsnorm_q8k", self._h, _p(_addr(x)), _p(_addr(gamma)), M, K,
                    _p(_addr(y_out)), _p(_addr(out)))
+
+    def lm_head_argmax(self, q8k, q80, M: int, K: int, w_rows, type_id: int, rows: int, row_base: int,
+                       logits_out, best_val, best_id):
+        self._call("qmm_lm_head_argmax", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_rows)),
+                   type_id, rows, row_base, _p(_addr(logits_out)), _p(_addr(best_val)), _p(_addr(best_id)))
+
+    def eval_rows_argmax(self, q8k, q80, M: int, K: int, w_tensor, type_id: int, row_ids, n_ids: int,
+                         vals_out, best_val, best_id):
+        self._call("qmm_eval_rows_argmax", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_tensor)),
+                   type_id, _p(_addr(row_ids)), n_ids, _p(_addr(vals_out)), _p(_addr(best_val)),
+                   _p(_addr(best_id)))
 
     def swiglu_q8k(self, gate, up, M: int, N: int, h_out, out):
         self._call("qmm_swiglu_q8k", self._h, _p(_addr(gate)), _p(_addr(up)), M, N,

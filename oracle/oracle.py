@@ -86,6 +86,7 @@ class Oracle:
                                                  C.POINTER(_MatrixTask), C.c_int]
         L.qo_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
         L.qo_rmsnorm_q8k_f16.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
+        L.qo_chunk_argmax.argtypes = [_p, C.c_int, C.c_int, C.c_size_t, C.c_int, _p, C.c_uint32, _p, _p]
 
     # fp16 ----------------------------------------------------------------
     def f32_to_fp16(self, x) -> np.ndarray:
@@ -231,6 +232,42 @@ class Oracle:
         bs = np.empty((M, N // 32), np.int32)
         self.lib.qo_swiglu_q8k(_ptr(gate), _ptr(up), M, N, _ptr(h), _ptr(d), _ptr(qs), _ptr(bs))
         return h, (d, qs, bs)
+
+    def chunk_argmax(self, logits: np.ndarray, best_val, best_id, round16=True, ids=None, row_base=0):
+        """The running argmax update over logits [M][rows]; returns new (best_val, best_id)."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        if lg.ndim == 1:
+            lg = lg[None, :]
+        M, rows = lg.shape
+        bv = np.array(best_val, dtype=np.float32).reshape(M).copy()
+        bi = np.array(best_id, dtype=np.uint32).reshape(M).copy()
+        idp = None
+        if ids is not None:
+            ids = np.ascontiguousarray(ids, dtype=np.uint32)
+            idp = _ptr(ids)
+        self.lib.qo_chunk_argmax(_ptr(lg), M, rows, rows, 1 if round16 else 0, idp, row_base, _ptr(bv), _ptr(bi))
+        return bv, bi
+
+    def lm_head_argmax(self, prequantized, w_rows, type_id: int, rows: int, row_base: int, best_val, best_id):
+        """One LM-head chunk on prequantized Q8_K rows: (logits, best_val, best_id)."""
+        M = prequantized[0].shape[0]
+        K = prequantized[1].shape[1]
+        lg = self.gemm_multi(np.zeros((M, K), np.float32), [dict(w=w_rows, type=type_id, rows=rows)],
+                             prequantized=(prequantized, None))[0]
+        bv, bi = self.chunk_argmax(lg, best_val, best_id, True, None, row_base)
+        return lg, bv, bi
+
+    def eval_rows_argmax(self, prequantized, w_tensor, type_id: int, K: int, row_ids, best_val, best_id):
+        """Indexed rows: (vals [M][n], best_val, best_id) in list order, fp32 values."""
+        rb = row_bytes(type_id, K)
+        ids = np.asarray(row_ids, dtype=np.uint32)
+        w = np.asarray(w_tensor, np.uint8).reshape(-1)
+        rows = np.concatenate([w[int(i) * rb:(int(i) + 1) * rb] for i in ids])
+        M = prequantized[0].shape[0]
+        vals = self.gemm_multi(np.zeros((M, K), np.float32), [dict(w=rows, type=type_id, rows=len(ids))],
+                               prequantized=(prequantized, None))[0]
+        bv, bi = self.chunk_argmax(vals, best_val, best_id, False, ids, 0)
+        return vals, bv, bi
 
     def rmsnorm_q8k_f16(self, x16: np.ndarray, gamma16: np.ndarray):
         """rmsnorm_fp16_rows_fast on fp16 bits: (y16 [M][K], (d, qs, bsum32))."""

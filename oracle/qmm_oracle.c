@@ -28,6 +28,9 @@
  *   qo_swiglu_q8k                    composition: h vs numpy fp64 SiLU*up
  *                                    (tolerance; expf differs between libms),
  *                                    codes vs qo_quantize_q8k_f32(h).
+ *   qo_chunk_argmax                  vs a first-maximum / strict-update
+ *                                    restatement in numpy on planted ties,
+ *                                    NaNs and values equal to the seed.
  *   qo_rmsnorm_q8k_f16               bit-exact vs the compiled reference's
  *                                    rmsnorm_fp16_rows_fast (y and Q8_K);
  *                                    closed forms (constant rows, unit gamma)
@@ -649,5 +652,30 @@ void qo_rmsnorm_q8k_f16(const uint16_t *x, const uint16_t *gamma, int M, int K, 
             yr[i] = qo_f32_to_fp16(qo_fp16_to_f32(xr[i]) * inv_rms * qo_fp16_to_f32(gamma[i]));
         qo_quantize_row_q8k_f16(yr, K, d + (size_t)m * nb, qs + (size_t)m * K,
                                 bsum32 + (size_t)m * nb * 8);
+    }
+}
+
+/* ------------------------------------------------------------- LM head -- */
+
+/* The running argmax of run_final_norm_and_lm_head_batch_sdot over one
+ * chunk's logits (E:11172-11183): row order, v = (float)(fp16)logit, replace
+ * on v > best only. With round16 = 0, the fp32 form of the indexed-row scans
+ * (E:9568-9569). ids (may be NULL) name the rows; else row_base + r. */
+void qo_chunk_argmax(const float *logits, int M, int rows, size_t ldl, int round16, const uint32_t *ids,
+                     uint32_t row_base, float *best_val, uint32_t *best_id) {
+    for (int m = 0; m < M; ++m) {
+        float bv = best_val[m];
+        uint32_t bi = best_id[m];
+        const float *lr = logits + (size_t)m * ldl;
+        for (int r = 0; r < rows; ++r) {
+            float v = lr[r];
+            if (round16) v = qo_fp16_to_f32(qo_f32_to_fp16(v));
+            if (v > bv) {
+                bv = v;
+                bi = ids ? ids[r] : row_base + (uint32_t)r;
+            }
+        }
+        best_val[m] = bv;
+        best_id[m] = bi;
     }
 }

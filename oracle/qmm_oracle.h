@@ -123,6 +123,11 @@ int qo_gemm_multi_prequantized(const float *q8k_d, const int8_t *q8k_qs,
 void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                    float *d, int8_t *qs, int32_t *bsum32);
 
+/* Running argmax over one chunk of logits [M][ldl] (E:11172-11183): row
+ * order, fp16-rounded values when round16, strict >; best_* updated in place. */
+void qo_chunk_argmax(const float *logits, int M, int rows, size_t ldl, int round16, const uint32_t *ids,
+                     uint32_t row_base, float *best_val, uint32_t *best_id);
+
 /* rmsnorm_fp16_rows_fast (E:4264-4314), scalar branch, on fp16 bits:
  * y [M][K] fp16 bits, then the Q8_K of each y row. K % 256 == 0. */
 void qo_rmsnorm_q8k_f16(const uint16_t *x, const uint16_t *gamma, int M, int K, uint16_t *y,
