@@ -48,7 +48,7 @@ __device__ inline Best block_best(Best b, Best *sh) {
 }
 
 // slice s of token m: rows [s * SLICE, (s + 1) * SLICE) of logits[m][.]
-constexpr int kSlice = 4096;
+constexpr int kSlice = 1024;
 
 template <bool ROUND16>
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *__restrict__ logits, int rows,
