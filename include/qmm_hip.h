@@ -40,6 +40,7 @@ extern "C" {
 #define QMM_EHIP 4    /* HIP runtime error (message in qmm_last_error) */
 #define QMM_ENOMEM 5  /* device allocation failed */
 #define QMM_EALIGN 6  /* device pointer misaligned for its format */
+#define QMM_ENOTFOUND 7  /* no GGUF tensor of that name */
 
 /* ggml type ids (E:115-120) */
 #define QMM_TYPE_Q8_0 8
@@ -180,6 +181,39 @@ int qmm_graph_destroy(void *graph_exec);
  * returning the elapsed milliseconds. */
 int qmm_timer_begin(qmm_context *ctx);
 int qmm_timer_end(qmm_context *ctx, float *ms);
+
+/* ---------------------------------------------------------------- GGUF */
+/* GGUF v2/v3 container, memory-mapped read-only (parse_gguf_file E:376-413,
+ * GgufTensorInfo E:168-177, find_tensor E:415-420). Host code: needs no GPU.
+ * Differences from the reference: tensor bytes outside the file are an
+ * error (QMM_ESHAPE), and up to 65536 tensors are accepted (not 512). */
+typedef struct qmm_gguf qmm_gguf;
+typedef struct {
+    char name[128];       /* truncated to 127 bytes, as the reference */
+    uint32_t n_dims;      /* 1..4 */
+    uint64_t dims[4];     /* dims[0] innermost (= cols of a matrix); unused dims 1 */
+    uint32_t type;        /* ggml type id */
+    uint64_t rel_offset;  /* from the data section */
+    uint64_t abs_offset;  /* from the file start: data_offset + rel_offset */
+    uint64_t n_elems;
+    uint64_t byte_size;   /* compute_ggml_bytes (E:364-374); 0 for other types */
+} qmm_gguf_tensor;
+
+int qmm_gguf_open(const char *path, qmm_gguf **out);
+int qmm_gguf_close(qmm_gguf *g);
+/* version, alignment (general.alignment or 32), data section offset, tensor count */
+int qmm_gguf_header(const qmm_gguf *g, uint32_t *version, uint64_t *alignment, uint64_t *data_offset,
+                    int *n_tensors);
+int qmm_gguf_tensor_at(const qmm_gguf *g, int i, qmm_gguf_tensor *out);
+/* QMM_ENOTFOUND if absent */
+int qmm_gguf_find_tensor(const qmm_gguf *g, const char *name, qmm_gguf_tensor *out);
+/* host pointer to a tensor's bytes inside the mapping (valid until close) */
+const void *qmm_gguf_data(const qmm_gguf *g, const qmm_gguf_tensor *t);
+/* residency of one quantized matrix: qmm_weight_upload of its rows
+ * (n_elems / dims[0]) x cols (dims[0]); the reference uses the mapped bytes
+ * in place (w_base = ctx->base + t->abs_offset, E:4174) */
+int qmm_gguf_upload(qmm_context *ctx, const qmm_gguf *g, const char *name, void **dev_blocks,
+                    qmm_gguf_tensor *info);
 
 #ifdef __cplusplus
 }

@@ -230,6 +230,7 @@ const char *qmm_status_string(int status) {
         case QMM_EHIP: return "HIP runtime error";
         case QMM_ENOMEM: return "device allocation failed";
         case QMM_EALIGN: return "misaligned device pointer";
+        case QMM_ENOTFOUND: return "tensor not found";
         default: return "unknown status";
     }
 }

@@ -78,6 +78,13 @@ _SIGNATURES = [
     ("qmm_quantize_q8_0", C.c_int, [_p, _p, C.c_int, C.c_int, _p]),
     ("qmm_swiglu_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_rmsnorm_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
+    ("qmm_gguf_open", C.c_int, [C.c_char_p, _p]),
+    ("qmm_gguf_close", C.c_int, [_p]),
+    ("qmm_gguf_header", C.c_int, [_p, _p, _p, _p, _p]),
+    ("qmm_gguf_tensor_at", C.c_int, [_p, C.c_int, _p]),
+    ("qmm_gguf_find_tensor", C.c_int, [_p, C.c_char_p, _p]),
+    ("qmm_gguf_data", _p, [_p, _p]),
+    ("qmm_gguf_upload", C.c_int, [_p, _p, C.c_char_p, _p, _p]),
     ("qmm_lm_head_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int, C.c_uint32,
                                      _p, _p, _p]),
     ("qmm_eval_rows_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, _p, C.c_int,
@@ -162,6 +169,73 @@ def _addr(x) -> int:
     if x is None:
         return 0
     return int(x)
+
+
+class GgufTensor(C.Structure):
+    """qmm_gguf_tensor (GgufTensorInfo, E:168-177)."""
+    _fields_ = [("name", C.c_char * 128), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("type", C.c_uint32), ("rel_offset", C.c_uint64), ("abs_offset", C.c_uint64),
+                ("n_elems", C.c_uint64), ("byte_size", C.c_uint64)]
+
+    def as_dict(self):
+        return dict(name=self.name.decode("utf-8", "replace"), n_dims=self.n_dims, dims=list(self.dims),
+                    type=self.type, rel_offset=self.rel_offset, abs_offset=self.abs_offset,
+                    n_elems=self.n_elems, byte_size=self.byte_size)
+
+
+class Gguf:
+    """A GGUF file, memory-mapped by the library (host only; no GPU needed)."""
+
+    def __init__(self, path: str):
+        self.lib = load_library()
+        h = _p()
+        rc = self.lib.qmm_gguf_open(os.fsencode(path), C.byref(h))
+        if rc != 0:
+            raise QmmError(rc, f"qmm_gguf_open({path}): {self.lib.qmm_status_string(rc).decode()}")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            self.lib.qmm_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def header(self):
+        v, al, do, n = C.c_uint32(), C.c_uint64(), C.c_uint64(), C.c_int()
+        self.lib.qmm_gguf_header(self._h, C.byref(v), C.byref(al), C.byref(do), C.byref(n))
+        return dict(version=v.value, alignment=al.value, data_offset=do.value, n_tensors=n.value)
+
+    def tensors(self):
+        out = []
+        for i in range(self.header()["n_tensors"]):
+            t = GgufTensor()
+            self.lib.qmm_gguf_tensor_at(self._h, i, C.byref(t))
+            out.append(t.as_dict())
+        return out
+
+    def find(self, name: str):
+        t = GgufTensor()
+        rc = self.lib.qmm_gguf_find_tensor(self._h, name.encode(), C.byref(t))
+        return t.as_dict() if rc == 0 else None
+
+    def data(self, name: str) -> np.ndarray:
+        t = GgufTensor()
+        rc = self.lib.qmm_gguf_find_tensor(self._h, name.encode(), C.byref(t))
+        if rc != 0:
+            raise QmmError(rc, f"no tensor {name}")
+        p = self.lib.qmm_gguf_data(self._h, C.byref(t))
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint8)), shape=(t.byte_size,)).copy()
+
+    def upload(self, ctx: "Context", name: str):
+        p = _p()
+        t = GgufTensor()
+        ctx._call("qmm_gguf_upload", ctx._h, self._h, name.encode(), C.byref(p), C.byref(t))
+        return p.value, t.as_dict()
 
 
 class Context:

@@ -312,6 +312,8 @@ class Reference:
         L.ref_dot_rows.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p]
         L.ref_swiglu_q8k.restype = C.c_int
         L.ref_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p]
+        L.ref_gguf_parse.restype = C.c_int
+        L.ref_gguf_parse.argtypes = [_p, C.c_size_t, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, C.c_int]
         L.ref_rmsnorm_q8k.restype = C.c_int
         L.ref_rmsnorm_q8k.argtypes = [_p, _p, _p, C.c_int, C.c_int, _p, _p, _p]
         L.ref_bench_gemv.restype = C.c_double
@@ -389,6 +391,26 @@ class Reference:
         if rc != 0:
             raise ValueError("outside the reference's static capacity")
         return g, (d, qs, bs)
+
+    def gguf_parse(self, data: bytes, cap: int = 512):
+        """parse_gguf_file on the bytes: None if rejected, else (alignment,
+        data_offset, [tensor dicts])."""
+        buf = np.frombuffer(data, dtype=np.uint8).copy()
+        al, do = np.zeros(1, np.uint64), np.zeros(1, np.uint64)
+        names = np.zeros((cap, 128), np.uint8)
+        nd, ty = np.zeros(cap, np.uint32), np.zeros(cap, np.uint32)
+        dims = np.zeros((cap, 4), np.uint64)
+        rel, ab, ne, bs = (np.zeros(cap, np.uint64) for _ in range(4))
+        n = self.lib.ref_gguf_parse(_ptr(buf), buf.size, _ptr(al), _ptr(do), _ptr(names), _ptr(nd), _ptr(dims),
+                                    _ptr(ty), _ptr(rel), _ptr(ab), _ptr(ne), _ptr(bs), cap)
+        if n < 0:
+            return None
+        ts = []
+        for i in range(min(n, cap)):
+            ts.append(dict(name=bytes(names[i]).split(b"\0")[0].decode("utf-8", "replace"), n_dims=int(nd[i]),
+                           dims=[int(v) for v in dims[i]], type=int(ty[i]), rel_offset=int(rel[i]),
+                           abs_offset=int(ab[i]), n_elems=int(ne[i]), byte_size=int(bs[i])))
+        return int(al[0]), int(do[0]), ts
 
     def rmsnorm_q8k(self, x16: np.ndarray, gamma16: np.ndarray):
         x = np.ascontiguousarray(x16, dtype=np.uint16)

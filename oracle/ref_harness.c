@@ -172,6 +172,37 @@ int ref_rmsnorm_q8k(const uint16_t *x, const uint16_t *gamma, uint16_t *y, int M
     return 0;
 }
 
+/* parse_gguf_file (E:376-413) on an in-memory file: the header values and
+ * the tensor table (up to cap entries) copied out. Returns the tensor count,
+ * or -1 where the reference rejects the file. */
+int ref_gguf_parse(const uint8_t *buf, size_t size, uint64_t *alignment, uint64_t *data_offset,
+                   char *names, uint32_t *n_dims, uint64_t *dims, uint32_t *types, uint64_t *rel,
+                   uint64_t *abs_off, uint64_t *n_elems, uint64_t *byte_size, int cap) {
+    static GgufContext g;
+    memset(&g, 0, sizeof(g));
+    g.base = buf;
+    g.file_size = size;
+    g.pos = 0;
+    const int ok = parse_gguf_file(&g);
+    free(g.vocab_ptrs);
+    free(g.vocab_lens);
+    if (!ok) return -1;
+    *alignment = g.alignment;
+    *data_offset = g.data_offset;
+    for (int i = 0; i < (int)g.n_tensors && i < cap; ++i) {
+        const GgufTensorInfo *t = &g.tensors[i];
+        memcpy(names + (size_t)i * 128, t->name, 128);
+        n_dims[i] = t->n_dims;
+        for (int d = 0; d < 4; ++d) dims[(size_t)i * 4 + d] = t->dims[d];
+        types[i] = t->type;
+        rel[i] = t->rel_offset;
+        abs_off[i] = t->abs_offset;
+        n_elems[i] = t->n_elems;
+        byte_size[i] = t->byte_size;
+    }
+    return (int)g.n_tensors;
+}
+
 /* ---------------------------------------------------------------------------
  * CPU baseline: the reference's portable batch-1 path for one projection —
  * quantize_row_fp16_to_q8_k of x once, then eval_single_lm_row_dot per
