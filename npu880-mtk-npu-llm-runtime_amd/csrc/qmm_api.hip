@@ -154,6 +154,7 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
                 bool *need_q8k, bool *need_q80) {
     if (M <= 0 || K <= 0) return fail(ctx, QMM_EINVAL, "M and K must be positive");
     if (!tasks || n_tasks <= 0) return fail(ctx, QMM_EINVAL, "empty task list");
+    if (n_tasks > 256) return fail(ctx, QMM_EINVAL, "more than 256 tasks in one dispatch");
     *need_q8k = *need_q80 = false;
     int total = 0;
     for (int t = 0; t < n_tasks; ++t) {
@@ -197,21 +198,32 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
         const uint8_t *b = static_cast<const uint8_t *>(q80);
         x0 = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off)};
     }
-    for (int t = 0; t < n_tasks; ++t) {
-        const qmm_matrix_task &T = tasks[t];
-        if (T.rows == 0) continue;
-        qmm::MatArgs a;
-        a.w = static_cast<const uint8_t *>(T.w_base);
-        a.row_bytes = T.row_bytes;
-        a.N = T.rows;
-        a.K = K;
-        a.M = M;
-        a.y = T.dst;
-        a.ldy = M > 1 ? T.dst_stride : size_t(T.rows);
-        a.res = T.residual;
-        a.ldr = M > 1 ? T.res_stride : size_t(T.rows);
-        const hipError_t e = (M == 1) ? qmm::launch_gemv(T.type, a, x32, xk, x0, ctx->stream)
-                                      : qmm::launch_mfma(T.type, a, xk, x0, ctx->stream);
+    // tasks of one type run as one launch (up to kMaxGroup per launch), in
+    // order of first appearance; outputs are disjoint, so grouping changes
+    // no result
+    bool done[256] = {};
+    for (int t0 = 0; t0 < n_tasks; ++t0) {
+        if (done[t0] || tasks[t0].rows == 0) continue;
+        qmm::MatArgs group[qmm::kMaxGroup];
+        int n = 0;
+        for (int t = t0; t < n_tasks; ++t) {
+            const qmm_matrix_task &T = tasks[t];
+            if (done[t] || T.rows == 0 || T.type != tasks[t0].type) continue;
+            done[t] = true;
+            qmm::MatArgs &a = group[n++];
+            a.w = static_cast<const uint8_t *>(T.w_base);
+            a.row_bytes = T.row_bytes;
+            a.N = T.rows;
+            a.K = K;
+            a.M = M;
+            a.y = T.dst;
+            a.ldy = M > 1 ? T.dst_stride : size_t(T.rows);
+            a.res = T.residual;
+            a.ldr = M > 1 ? T.res_stride : size_t(T.rows);
+            if (n == qmm::kMaxGroup) break;
+        }
+        const hipError_t e = (M == 1) ? qmm::launch_gemv(tasks[t0].type, group, n, x32, xk, x0, ctx->stream)
+                                      : qmm::launch_mfma(tasks[t0].type, group, n, xk, x0, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
     return QMM_OK;

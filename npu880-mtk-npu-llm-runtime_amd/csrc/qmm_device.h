@@ -70,6 +70,23 @@ struct MatArgs {
     size_t ldr;
 };
 
+// Several tasks of one type in one launch (the dispatcher's task groups,
+// E:7954-7959, E:8110-8114): task i owns workgroups [wg0[i], wg0[i+1]) of
+// the grid's x dimension; all tasks share K, M and the activations.
+constexpr int kMaxGroup = 8;
+struct MatGroup {
+    MatArgs t[kMaxGroup];
+    int wg0[kMaxGroup + 1];
+    int n;
+};
+// the task of workgroup bx (uniform), and bx relative to that task
+__device__ inline int group_task(const MatGroup &g, int bx, int &local) {
+    int i = 0;
+    while (i + 1 < g.n && bx >= g.wg0[i + 1]) ++i;
+    local = bx - g.wg0[i];
+    return i;
+}
+
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStream_t s);
@@ -88,11 +105,11 @@ hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int
                               uint16_t *dst, hipStream_t s);
 // M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;
 // otherwise xk / x0 hold the prequantized row.
-hipError_t launch_gemv(uint32_t type, const MatArgs &a, const float *x32, const Q8KView &xk,
+hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                        const Q80View &x0, hipStream_t s);
 // dynamic LDS bytes the GEMV needs for K (must stay <= 64 KiB)
 size_t gemv_lds_bytes(uint32_t type, int K);
-hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
+hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s);
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)

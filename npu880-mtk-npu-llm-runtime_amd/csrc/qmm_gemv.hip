@@ -401,17 +401,24 @@ __host__ __device__ inline size_t gemv_lds_bytes_t(int K) {
 // R rows per wave, U wave steps of SLOTS blocks per batch.
 // FUSED: x32 is quantized in the kernel; otherwise prek / pre0 hold the
 // prequantized activation row.
-template <class F, int R, int U, bool FUSED>
-__global__ __launch_bounds__(256) void gemv_kernel(MatArgs a, const float *__restrict__ x32,
+// GRP: several tasks of the type in one launch (a MatGroup argument);
+// otherwise one task, passed alone (a smaller argument block)
+template <class F, int R, int U, bool FUSED, bool GRP>
+__global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGroup, MatArgs> grp,
+                                                   const float *__restrict__ x32,
                                                    Q8KView prek, Q80View pre0) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
     constexpr bool q80 = IsQ80<F>::v;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / G, k = lane % G;
+    int bx = int(blockIdx.x);
+    MatArgs a;
+    if constexpr (GRP) a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    else a = grp;
     const int K = a.K;
     const int nb = K / F::QK;
-    const int row0 = (int(blockIdx.x) * 4 + wid) * R;
+    const int row0 = (bx * 4 + wid) * R;
     const int nrows = max(0, min(R, a.N - row0));
     const int nblk = nrows * nb;
     // waves past the last row still issue (discarded) loads of row 0 so the
@@ -519,25 +526,35 @@ size_t gemv_lds_bytes(uint32_t type, int K) {
 }
 
 template <class F, int R, int U>
-static hipError_t launch_gemv_t(const MatArgs &a, const float *x32, const Q8KView &xk,
+static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                                 const Q80View &x0, hipStream_t s) {
-    const int waves = (a.N + R - 1) / R;
-    const unsigned grid = unsigned((waves + 3) / 4);
-    const size_t lds = gemv_lds_bytes_t<F, R, U>(a.K);
-    if (x32)
-        hipLaunchKernelGGL((gemv_kernel<F, R, U, true>), dim3(grid), dim3(256), lds, s, a, x32, xk, x0);
-    else
-        hipLaunchKernelGGL((gemv_kernel<F, R, U, false>), dim3(grid), dim3(256), lds, s, a, x32, xk, x0);
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + ((tasks[i].N + R - 1) / R + 3) / 4;  // 4 waves of R rows
+    }
+    const size_t lds = gemv_lds_bytes_t<F, R, U>(tasks[0].K);
+    const dim3 grid(unsigned(g.wg0[n]));
+    if (n == 1) {
+        if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
+        else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
+    } else {
+        if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, true>), grid, dim3(256), lds, s, g, x32, xk, x0);
+        else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, true>), grid, dim3(256), lds, s, g, x32, xk, x0);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(uint32_t type, const MatArgs &a, const float *x32, const Q8KView &xk,
+hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                        const Q80View &x0, hipStream_t s) {
+    if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
     switch (type) {
-        case kQ4_K: return launch_gemv_t<FmtQ4K4, kGemvR, 3>(a, x32, xk, x0, s);
-        case kQ5_K: return launch_gemv_t<FmtQ5K, kGemvR, kGemvU>(a, x32, xk, x0, s);
-        case kQ6_K: return launch_gemv_t<FmtQ6K, kGemvR, kGemvU>(a, x32, xk, x0, s);
-        case kQ8_0: return launch_gemv_t<FmtQ80, kGemvR, kGemvU>(a, x32, xk, x0, s);
+        case kQ4_K: return launch_gemv_t<FmtQ4K4, kGemvR, 3>(tasks, n, x32, xk, x0, s);
+        case kQ5_K: return launch_gemv_t<FmtQ5K, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ6_K: return launch_gemv_t<FmtQ6K, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ8_0: return launch_gemv_t<FmtQ80, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -243,14 +243,16 @@ struct TileCfg {
 };
 
 template <class C, class F>
-__global__ __launch_bounds__(256) void tile_kernel(MatArgs a, typename ActOf<F>::T x) {
+__global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<F>::T x) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int WR = C::WR, WT = C::WT, KS = C::KS, TR = C::TR, KCB = C::KCB;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, cl = lane >> 4;
     const int kp = wid % KS, pt = (wid / KS) % C::PT, pr = wid / (KS * C::PT);
-    const int n0 = int(blockIdx.x) * C::ROWS, m0 = int(blockIdx.y) * C::TOK;
+    int bx;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    const int n0 = bx * C::ROWS, m0 = int(blockIdx.y) * C::TOK;
     const int K = a.K, nb = K / F::QK;
     const int nchunks = (nb + KCB - 1) / KCB;
 
@@ -446,37 +448,46 @@ __global__ __launch_bounds__(256) void tile_kernel(MatArgs a, typename ActOf<F>:
 }
 
 template <class C, class F>
-static hipError_t launch_tile_t(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    const dim3 grid(unsigned((a.N + C::ROWS - 1) / C::ROWS), unsigned((a.M + C::TOK - 1) / C::TOK));
-    hipLaunchKernelGGL((tile_kernel<C, F>), grid, dim3(256), size_t(C::LDS), s, a, x);
+static hipError_t launch_tile_t(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + C::ROWS - 1) / C::ROWS;
+    }
+    const dim3 grid(unsigned(g.wg0[n]), unsigned((tasks[0].M + C::TOK - 1) / C::TOK));
+    hipLaunchKernelGGL((tile_kernel<C, F>), grid, dim3(256), size_t(C::LDS), s, g, x);
     return hipGetLastError();
 }
 
 template <class F>
-static hipError_t launch_tile(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
+static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    const MatArgs &a = tasks[0];
     // buffer offsets are 32-bit with kFar past every range
     if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
     //                      WR WT PR PT KS TR PD  LDS budget
-    if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(a, x, s);
-    if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(a, x, s);
-    if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(a, x, s);
+    if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(tasks, n, x, s);
+    if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(tasks, n, x, s);
+    if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
     // Q6_K's 16 units per block: one row tile per wave (two would spill)
-    if constexpr (F::NU > 8) return launch_tile_t<TileCfg<F, 1, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(a, x, s);
-    else return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(a, x, s);
+    if constexpr (F::NU > 8) return launch_tile_t<TileCfg<F, 1, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
+    else return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
 }
 
 template <class F>
-static hipError_t launch_mfma_f(const MatArgs &a, const typename ActOf<F>::T &x, hipStream_t s) {
-    return launch_tile<F>(a, x, s);
+static hipError_t launch_mfma_f(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    return launch_tile<F>(tasks, n, x, s);
 }
 
-hipError_t launch_mfma(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0,
+hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s) {
+    if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
     switch (type) {
-        case kQ4_K: return launch_mfma_f<MQ4K>(a, xk, s);
-        case kQ5_K: return launch_mfma_f<MQ5K>(a, xk, s);
-        case kQ6_K: return launch_mfma_f<MQ6K>(a, xk, s);
-        case kQ8_0: return launch_mfma_f<MQ80>(a, x0, s);
+        case kQ4_K: return launch_mfma_f<MQ4K>(tasks, n, xk, s);
+        case kQ5_K: return launch_mfma_f<MQ5K>(tasks, n, xk, s);
+        case kQ6_K: return launch_mfma_f<MQ6K>(tasks, n, xk, s);
+        case kQ8_0: return launch_mfma_f<MQ80>(tasks, n, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -150,3 +150,32 @@ def test_prequantized_dispatch_and_strides(ctx, oracle):
     assert np.all(y[:, N:] == 7.0)  # nothing written past the task's rows
     for b in (qb, wb, yb):
         ctx.free(b)
+
+
+@pytest.mark.parametrize("M", [1, 6, 70])
+def test_task_groups_one_launch(ctx, oracle, M):
+    """Many tasks of one type (more than one launch's group of 8), tiny-N tasks
+    and residuals interleaved with another type: the E:7954-7959 /
+    E:8110-8114 task groups run as one launch per type group."""
+    K = 2560
+    say(f"task groups M={M}")
+    specs = [(TYPE_Q4_K, 96), (TYPE_Q6_K, 40), (TYPE_Q4_K, 32), (TYPE_Q4_K, 1), (TYPE_Q4_K, 300),
+             (TYPE_Q4_K, 33), (TYPE_Q6_K, 16), (TYPE_Q4_K, 64), (TYPE_Q4_K, 7), (TYPE_Q4_K, 128),
+             (TYPE_Q4_K, 48), (TYPE_Q4_K, 17)]
+    x = synth.activations(M, K, seed=19)
+    ws = [synth.weights(t, n, K, seed=60 + i) for i, (t, n) in enumerate(specs)]
+    ress = [synth.activations(M, n, seed=80 + i) if i % 3 == 1 else None for i, (_, n) in enumerate(specs)]
+    xb = ctx.upload(x)
+    wbs = [ctx.weight_upload(w, t, n, K) for w, (t, n) in zip(ws, specs)]
+    ybs = [ctx.malloc(M * n * 4) for _, n in specs]
+    rbs = [ctx.upload(r) if r is not None else None for r in ress]
+    tasks = [qmm_hip.MatrixTask(wb, t, n, K, yb, n, rb, n if rb is not None else 0)
+             for wb, yb, rb, (t, n) in zip(wbs, ybs, rbs, specs)]
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=t, rows=n, **({"residual": r} if r is not None else {}))
+                                 for w, r, (t, n) in zip(ws, ress, specs)])
+    for i, ((t, n), yb) in enumerate(zip(specs, ybs)):
+        check_outputs(ctx.d2h(yb, np.float32, (M, n)), refs[i], f"task {i}")
+    for b in [xb] + wbs + ybs + [r for r in rbs if r is not None]:
+        ctx.free(b)
