@@ -43,7 +43,7 @@ __device__ inline int4v mfma16x16x32(uint2 a, uint2 b) {
 // Q4_K: unit u = sub-block 2j + h; lane c holds values 64j + 32h + 8c + t.
 struct MQ4K {
     static constexpr int NU = 8, QK = 256, BB = 144;
-    static constexpr bool kMin = true;
+    static constexpr bool kMin = true, kSplit = false;
     struct W { uint4 h; uint2 q[4]; };
     __device__ static W load(const uint8_t *blk, int c) {
         W w;
@@ -65,7 +65,7 @@ struct MQ4K {
 // Q5_K: as Q4_K with the high bit u of qh[8c + t].
 struct MQ5K {
     static constexpr int NU = 8, QK = 256, BB = 176;
-    static constexpr bool kMin = true;
+    static constexpr bool kMin = true, kSplit = false;
     struct W { uint4 h; uint2 qh; uint2 q[4]; };
     __device__ static W load(const uint8_t *blk, int c) {
         W w;
@@ -91,7 +91,7 @@ struct MQ5K {
 // 8 values l = 8c + t; lanes c = 2, 3 supply zero weights.
 struct MQ6K {
     static constexpr int NU = 16, QK = 256, BB = 210;
-    static constexpr bool kMin = false;
+    static constexpr bool kMin = false, kSplit = false;
     struct W { uint2 a[4], b[4], qh[4]; uint2 s0, s1; uint32_t d; };
     __device__ static W load(const uint8_t *blk, int c) {
         W w;
@@ -151,7 +151,7 @@ struct MQ6K {
 // Q8_0: one unit per 32-value block; lane c holds values 8c + t.
 struct MQ80 {
     static constexpr int NU = 1, QK = 32, BB = 34;
-    static constexpr bool kMin = false;
+    static constexpr bool kMin = false, kSplit = false;
     struct W { uint2 q; uint32_t d; };
     __device__ static W load(const uint8_t *blk, int c) { return {ld8_a2(blk + 2 + 8 * c), ld16b_a2(blk)}; }
     __device__ static W load_lds(const uint8_t *blk, int c) { return {lds8_a2(blk + 2 + 8 * c), lds16b_a2(blk)}; }
@@ -159,15 +159,170 @@ struct MQ80 {
     __device__ static uint2 bop(const W &w, int u, int c) { (void)u; (void)c; return w.q; }
 };
 
+// Q4_K with the unit scales folded into the B operand (token tiles >= 2 per
+// wave): sc = 8 sh + sl with sh, sl in 0..7, so q * sh and q * sl (q <= 15)
+// are int8 (<= 105) and, byte by byte, one packed 16-bit multiply each (no
+// byte product reaches 256). Over one 64-value chunk h (units 2h, 2h+1) a
+// v_mfma_i32_16x16x64_i8 chain accumulates sum a*q*sh (D1), sum a*q*sl (D2)
+// and sum a*m (Dm, broadcast mins) across the block's 4 chunks, all exact:
+// S = 8 D1 + D2, Mb = Dm. A lane's 16 bytes per chunk are values
+// 64h + 8c + t (low nibbles, unit 2h) and 64h + 32 + 8c + t (high nibbles,
+// unit 2h + 1), t < 8, in both operands.
+struct MQ4KS : MQ4K {
+    static constexpr bool kSplit = true;
+    static constexpr int kShift = 3;  // S = (D1 << 3) + D2
+};
+
+// Q5_K with the unit scales folded into the B operand: w = q * sc <= 1953;
+// in 16-bit lanes P = w + 128 and w = 256 hi + lo, hi = P's high byte,
+// lo = P's low byte xor 0x80 (as for Q6_K below): S = 256 D1 + D2, plus the
+// mins chain of Q4_K. Same value placement as Q4_K (the high bit of value
+// 64h + 32k + 8c + t is bit 2h + k of qh[8c + t]).
+struct MQ5KS : MQ5K {
+    static constexpr bool kSplit = true;
+    static constexpr int kShift = 8;  // S = (D1 << 8) + D2
+};
+
+// Q6_K with the scales folded into the B operand (token tiles >= 2 per
+// wave): w = (q - 32) * sc lies in [-4064, 4096]; in 16-bit lanes
+// P = w + 128 = q * sc + (128 - 32 sc) (one packed multiply-add), and
+// w = 256 hi + lo with hi = the high byte of P (|hi| <= 16) and
+// lo = (P mod 256) - 128, i.e. P's low byte xor 0x80: two int8 operands,
+// S = 256 D1 + D2 over two K=64 chains, exact.
+// Lane group c holds, per half hf, values 32 i + 8 c + t (t < 8) of every
+// i = 0..3; chunk h = 2 hf + ip takes i = 2 ip (ql[64 hf + l], nibble 4 ip,
+// qh[32 hf + l] bits 4 ip) and i = 2 ip + 1 (ql[64 hf + 32 + l], nibble 4 ip,
+// qh bits 4 ip + 2), so the chunk's values are 64 h + 8 c + t and
+// 64 h + 32 + 8 c + t as for Q4_K; value 32 i + l of half hf has scale
+// sc[8 hf + 2 i + l / 16] with l / 16 = c / 2 (block layout: E:673-700).
+struct MQ6KS : MQ6K {
+    static constexpr bool kSplit = true;
+    static constexpr int kShift = 8;  // S = (D1 << 8) + D2
+    struct W { uint2 a[2], b[2], qh[2]; uint2 s0, s1; uint32_t d; };
+    __device__ static W load_lds(const uint8_t *blk, int c) {
+        W w;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            w.a[hf] = lds8_a2(blk + 64 * hf + 8 * c);
+            w.b[hf] = lds8_a2(blk + 64 * hf + 32 + 8 * c);
+            w.qh[hf] = lds8_a2(blk + 128 + 32 * hf + 8 * c);
+        }
+        w.s0 = lds8_a2(blk + 192);
+        w.s1 = lds8_a2(blk + 200);
+        w.d = lds16b_a2(blk + 208);
+        return w;
+    }
+};
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {  // per byte, q_b * f < 256
+    const u16x2 v = __builtin_bit_cast(u16x2, q) * u16x2{uint16_t(f), uint16_t(f)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ inline int4v mfma16x16x64(const uint4 &a, const uint4 &b, int4v c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, a), __builtin_bit_cast(int4v, b), c,
+                                                 0, 0, 0);
+}
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+// B operands of one row tile's block: [chunk][high part | low part | mins]
+struct SplitB { uint4 b1[4], b2[4], bm[4]; };
+__device__ inline void split_b(const MQ4K::W &w, const int (&sc)[8], const int (&m)[8], SplitB &o) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const uint2 q = w.q[h];
+        const uint32_t lo0 = q.x & 0x0F0F0F0Fu, lo1 = q.y & 0x0F0F0F0Fu;
+        const uint32_t hi0 = (q.x >> 4) & 0x0F0F0F0Fu, hi1 = (q.y >> 4) & 0x0F0F0F0Fu;
+        const uint32_t sh0 = uint32_t(sc[2 * h]) >> 3, sl0 = uint32_t(sc[2 * h]) & 7u;
+        const uint32_t sh1 = uint32_t(sc[2 * h + 1]) >> 3, sl1 = uint32_t(sc[2 * h + 1]) & 7u;
+        o.b1[h] = make_uint4(bytes_times(lo0, sh0), bytes_times(lo1, sh0), bytes_times(hi0, sh1), bytes_times(hi1, sh1));
+        o.b2[h] = make_uint4(bytes_times(lo0, sl0), bytes_times(lo1, sl0), bytes_times(hi0, sl1), bytes_times(hi1, sl1));
+        const uint32_t m0 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h]), 0u);
+        const uint32_t m1 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h + 1]), 0u);
+        o.bm[h] = make_uint4(m0, m0, m1, m1);
+    }
+}
+
+// Four unsigned bytes q (< 64) times one scale: P = q * s + c in 16-bit
+// lanes (sp = (s, s), cp = (c, c)); lo gets P's low bytes xor 0x80, hi its
+// high bytes, in the order of q's bytes.
+__device__ inline void fold4(uint32_t q, u16x2 sp, u16x2 cp, uint32_t &lo, uint32_t &hi) {
+    const u16x2 ev = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, q, 0x0C020C00u));  // bytes 0, 2
+    const u16x2 od = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, q, 0x0C030C01u));  // bytes 1, 3
+    const uint32_t pe = __builtin_bit_cast(uint32_t, ev * sp + cp);
+    const uint32_t po = __builtin_bit_cast(uint32_t, od * sp + cp);
+    lo = __builtin_amdgcn_perm(po, pe, 0x06020400u) ^ 0x80808080u;
+    hi = __builtin_amdgcn_perm(po, pe, 0x07030501u);
+}
+
+__device__ inline void split_b(const MQ5K::W &w, const int (&sc)[8], const int (&m)[8], SplitB &o) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int u = 2 * h + k;
+            const u16x2 sp = {uint16_t(sc[u]), uint16_t(sc[u])};
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t v = e ? w.q[h].y : w.q[h].x, qv = e ? w.qh.y : w.qh.x;
+                const uint32_t q5 = ((v >> (4 * k)) & 0x0F0F0F0Fu) | (((qv >> u) & 0x01010101u) << 4);
+                fold4(q5, sp, u16x2{128u, 128u}, lo[2 * k + e], hi[2 * k + e]);
+            }
+        }
+        o.b1[h] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        o.b2[h] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        const uint32_t m0 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h]), 0u);
+        const uint32_t m1 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h + 1]), 0u);
+        o.bm[h] = make_uint4(m0, m0, m1, m1);
+    }
+}
+
+__device__ inline void split_b(const MQ6KS::W &w, int c, SplitB &o) {
+    const int cb = 8 * (c >> 1);  // bit offset of the lane's scale within a byte pair
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const int hf = h >> 1, ip = h & 1;
+        const uint2 sw = hf ? w.s1 : w.s0;
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = 2 * ip + k;
+            // sc[8 hf + 2 i + c / 2], sign-extended, in both 16-bit lanes
+            const int sc = __builtin_amdgcn_sbfe(int((i & 2) ? sw.y : sw.x), 16 * (i & 1) + cb, 8);
+            const u16x2 sp = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, uint32_t(sc), 0x01000100u));
+            const u16x2 cp = sp * u16x2{0xFFE0u, 0xFFE0u} + u16x2{128u, 128u};  // 128 - 32 sc
+            const uint2 src = k ? w.b[hf] : w.a[hf];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t v = e ? src.y : src.x, qv = e ? w.qh[hf].y : w.qh[hf].x;
+                const int hs = 4 * ip + 2 * k;  // qh bits of this i
+                const uint32_t q6 = ((v >> (4 * ip)) & 0x0F0F0F0Fu) | (((qv >> hs) & 0x03030303u) << 4);
+                fold4(q6, sp, cp, lo[2 * k + e], hi[2 * k + e]);
+            }
+        }
+        o.b1[h] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        o.b2[h] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+}
+
 template <class F> struct ActOf { using T = Q8KView; };
 template <> struct ActOf<MQ80> { using T = Q80View; };
+// the format with the scales folded into the B operand, used from two
+// token tiles per wave (M > 16)
+template <class F> struct Folded { using T = F; };
+template <> struct Folded<MQ4K> { using T = MQ4KS; };
+template <> struct Folded<MQ5K> { using T = MQ5KS; };
+template <> struct Folded<MQ6K> { using T = MQ6KS; };
 
 // Scales / mins of the lane's row for the current block.
 template <class F> struct Scales { int sc[F::NU]; int m[F::NU]; float d, dmin; };
 
 template <class F>
 __device__ inline void decode_scales(const typename F::W &w, Scales<F> &s) {
-    if constexpr (F::NU == 8) {
+    if constexpr (std::is_same_v<F, MQ6KS>) {  // the scales are folded into the B operand
+        s.d = fp16_bits_to_f32(w.d);
+        s.dmin = 0.0f;
+    } else if constexpr (F::NU == 8) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) scale_min_k4(u, w.h.y, w.h.z, w.h.w, s.sc[u], s.m[u]);
         s.d = fp16_bits_to_f32(w.h.x & 0xFFFFu);
@@ -350,22 +505,41 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
                 // dx are zeroed, its term is a signed zero, the sums are
                 // unchanged (a sum starting at +0 is never -0)
                 const float d = valid ? sc.d : 0.0f, dmin = valid ? sc.dmin : 0.0f;
+                [[maybe_unused]] SplitB sb;
+                if constexpr (F::kSplit) {
+                    if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+                    else split_b(wv, cl, sb);
+                }
 #pragma unroll
                 for (int wt = 0; wt < WT; ++wt) {
                     const int tl = (pt * WT + wt) * TR + (nl & (TR - 1));  // lane's A token
                     const int8_t *arow = as + tl * (C::ACR * 16) + j * F::QK;
                     int S[4] = {0, 0, 0, 0};
                     int4v Mb = {0, 0, 0, 0};
+                    if constexpr (F::kSplit) {
+                        int4v D1 = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
 #pragma unroll
-                    for (int u = 0; u < F::NU; ++u) {
-                        const uint2 av = ld8(arow + F::koff(u, cl));
-                        const int4v D = mfma16x16x32(av, F::bop(wv, u, cl));
-                        if constexpr (F::kMin) {
-                            const uint32_t mb = __builtin_amdgcn_perm(0u, uint32_t(sc.m[u]), 0u);  // byte broadcast
-                            Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
+                        for (int h = 0; h < 4; ++h) {
+                            const uint2 a0 = ld8(arow + 64 * h + 8 * cl), a1 = ld8(arow + 64 * h + 32 + 8 * cl);
+                            const uint4 av = make_uint4(a0.x, a0.y, a1.x, a1.y);
+                            D1 = mfma16x16x64(av, sb.b1[h], D1);
+                            D2 = mfma16x16x64(av, sb.b2[h], D2);
+                            if constexpr (F::kMin) Mb = mfma16x16x64(av, sb.bm[h], Mb);
                         }
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) S[r] += __mul24(sc.sc[u], D[r]);
+                        for (int r = 0; r < 4; ++r) S[r] = (D1[r] << F::kShift) + D2[r];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < F::NU; ++u) {
+                            const uint2 av = ld8(arow + F::koff(u, cl));
+                            const int4v D = mfma16x16x32(av, F::bop(wv, u, cl));
+                            if constexpr (F::kMin) {
+                                const uint32_t mb = __builtin_amdgcn_perm(0u, uint32_t(sc.m[u]), 0u);  // byte broadcast
+                                Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
+                            }
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) S[r] += __mul24(sc.sc[u], D[r]);
+                        }
                     }
                     // dx of output tokens 4 cl + r of this token tile (tokens
                     // past TR read neighbouring scales; their outputs are not kept)
@@ -466,28 +640,35 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     const MatArgs &a = tasks[0];
     // buffer offsets are 32-bit with kFar past every range
     if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
-    //                      WR WT PR PT KS TR PD  LDS budget
-    if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(tasks, n, x, s);
-    if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(tasks, n, x, s);
-    if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
-    // Q6_K's 16 units per block: one row tile per wave (two would spill)
-    if constexpr (F::NU > 8) return launch_tile_t<TileCfg<F, 1, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
-    else return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
-}
-
-template <class F>
-static hipError_t launch_mfma_f(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
-    return launch_tile<F>(tasks, n, x, s);
+    using G = typename Folded<F>::T;
+    //                          WR WT PR PT KS TR PD  LDS budget
+    if constexpr (!F::kSplit) {
+        if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(tasks, n, x, s);
+        if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(tasks, n, x, s);
+    }
+    if constexpr (!std::is_same_v<G, F>) {
+        return launch_tile<G>(tasks, n, x, s);
+    } else {
+        if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
+        // folded formats: one row tile decoded per wave, shared by 4 (Q6_K: 3)
+        // token tiles
+        if constexpr (F::kSplit && F::NU > 8)
+            return launch_tile_t<TileCfg<F, 1, 3, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
+        else if constexpr (F::kSplit)
+            return launch_tile_t<TileCfg<F, 1, 4, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
+        else
+            return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
+    }
 }
 
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
     switch (type) {
-        case kQ4_K: return launch_mfma_f<MQ4K>(tasks, n, xk, s);
-        case kQ5_K: return launch_mfma_f<MQ5K>(tasks, n, xk, s);
-        case kQ6_K: return launch_mfma_f<MQ6K>(tasks, n, xk, s);
-        case kQ8_0: return launch_mfma_f<MQ80>(tasks, n, x0, s);
+        case kQ4_K: return launch_tile<MQ4K>(tasks, n, xk, s);
+        case kQ5_K: return launch_tile<MQ5K>(tasks, n, xk, s);
+        case kQ6_K: return launch_tile<MQ6K>(tasks, n, xk, s);
+        case kQ8_0: return launch_tile<MQ80>(tasks, n, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -78,6 +78,42 @@ def test_tree_verify_q5k_qkv(ctx, oracle):
     _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, 64, seed=2100)
 
 
+def _extreme_weights(type_id, N, K, seed):
+    """Random blocks pushed to the ends of the integer ranges: all 6-bit
+    scales and mins 63 (Q4_K / Q5_K) or int8 scales cycling through -128,
+    127, -1, 0 (Q6_K), and every third row with all-max or all-zero quants,
+    so every weight * scale product reaches its largest magnitude."""
+    w = synth.weights(type_id, N, K, seed=seed)
+    bb = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}[type_id]
+    blk = w.reshape(N, -1, bb)
+    if type_id == TYPE_Q6_K:
+        blk[:, :, 192:208] = np.resize(np.array([-128, 127, -1, 0], np.int8), 16).view(np.uint8)
+        blk[0::3, :, 0:192] = 0x00   # q = 0: q - 32 = -32
+        blk[1::3, :, 0:192] = 0xFF   # q = 63: q - 32 = 31
+    else:
+        blk[:, :, 4:16] = 0xFF       # every scale and min 63
+        blk[0::3, :, 16:] = 0xFF     # q = 15 (Q4_K) / 31 (Q5_K)
+        blk[1::3, :, 16:] = 0x00
+    return w
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
+@pytest.mark.parametrize("M", [5, 40, 512])
+def test_mfma_extreme_scales(ctx, oracle, type_id, M):
+    """Extreme scales and quants through the MFMA paths (scales folded into
+    the weight operand from M > 16): the integer sums stay exact."""
+    N, K = 96, 1024
+    say(f"extreme scales {NAMES[type_id]} N={N} K={K} M={M}")
+    w = _extreme_weights(type_id, N, K, seed=700 + M)
+    x = synth.activations(M, K, seed=701)
+    x[:, ::7] *= 50.0   # large entries: many codes at +-127
+    wb = ctx.weight_upload(w, type_id, N, K)
+    y = ctx.gemm(type_id, wb, N, K, x)
+    ctx.free(wb)
+    ref = oracle.gemm_multi(x, [dict(w=w, type=type_id, rows=N)])[0]
+    check_outputs(y, ref, f"extreme {NAMES[type_id]} M={M}")
+
+
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K])
 def test_mfma_residual(ctx, oracle, type_id):
     _run(ctx, oracle, type_id, 200, 2560, 9, seed=7, residual=True)
