@@ -656,8 +656,8 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
             return launch_tile_t<TileCfg<F, 1, 3, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
         else if constexpr (F::kSplit)
             return launch_tile_t<TileCfg<F, 1, 4, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
-        else
-            return launch_tile_t<TileCfg<F, 2, 2, 2, 2, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
+        else  // Q8_0: a fp32 term per 32 values; smaller tiles, 3 workgroups per CU
+            return launch_tile_t<TileCfg<F, 1, 2, 4, 1, 1, 16, 2, 52 * 1024>, F>(tasks, n, x, s);
     }
 }
 
