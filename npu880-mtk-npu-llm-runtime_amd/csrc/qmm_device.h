@@ -202,16 +202,14 @@ __device__ inline uint32_t lds16b_a2(const uint8_t *p) {
 }
 
 // ------------------------------------------------------ Q8 quantization
-// Quantize the 4 fp16-rounded values a lane owns given the block's max |x|
-// (quantize_row_fp16_to_q8_k E:947-988): id = 127 / amax (correctly rounded),
+// Q8_K / Q8_0 codes of fp16-rounded values (quantize_row_fp16_to_q8_k
+// E:947-988): id = 127 / amax, correctly rounded, computed once per block;
 // q = rint(x * id) (round to nearest even, as lrintf in the default mode),
-// clamp to [-127, 127]. Returns the packed int8 codes and their sum.
-__device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
-    if (amax == 0.0f) {  // E:947-952
-        sum = 0;
-        return 0u;
-    }
-    const float id = 127.0f / amax;  // E:954
+// clamped to [-127, 127]. An all-zero block (E:947-952) takes id = 0, which
+// gives the same all-zero codes.
+__device__ inline float q8_inv_scale(float amax) { return amax == 0.0f ? 0.0f : 127.0f / amax; }
+// 4 values at a given id: the packed int8 codes and their sum
+__device__ inline uint32_t quant4_id(float h0, float h1, float h2, float h3, float id, int &sum) {
     int q[4];
     const float h[4] = {h0, h1, h2, h3};
 #pragma unroll
@@ -222,8 +220,12 @@ __device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float 
         q[i] = v;
     }
     sum = q[0] + q[1] + q[2] + q[3];
-    return (uint32_t(q[0]) & 0xFFu) | ((uint32_t(q[1]) & 0xFFu) << 8) |
-           ((uint32_t(q[2]) & 0xFFu) << 16) | ((uint32_t(q[3]) & 0xFFu) << 24);
+    const uint32_t lo = __builtin_amdgcn_perm(uint32_t(q[1]), uint32_t(q[0]), 0x0C0C0400u);  // q0, q1 low bytes
+    const uint32_t hi = __builtin_amdgcn_perm(uint32_t(q[3]), uint32_t(q[2]), 0x04000C0Cu);  // q2, q3 low bytes
+    return lo | hi;
+}
+__device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
+    return quant4_id(h0, h1, h2, h3, q8_inv_scale(amax), sum);
 }
 // d = amax / 127 (E:953), 0 for an all-zero block
 __device__ inline float q8_scale(float amax) { return amax == 0.0f ? 0.0f : amax / 127.0f; }

@@ -304,10 +304,11 @@ __device__ inline void x_quant(const XPre &p, int c, int K, bool store, const Ld
     const float amax = Q80 ? fmaxf(m, dppf<0xB1>(m)) : row16_max(m);
     int s0, s1, s2, s3;
     uint4 q;
-    q.x = quant4(h[0], h[1], h[2], h[3], amax, s0);
-    q.y = quant4(h[4], h[5], h[6], h[7], amax, s1);
-    q.z = quant4(h[8], h[9], h[10], h[11], amax, s2);
-    q.w = quant4(h[12], h[13], h[14], h[15], amax, s3);
+    const float id = q8_inv_scale(amax);
+    q.x = quant4_id(h[0], h[1], h[2], h[3], id, s0);
+    q.y = quant4_id(h[4], h[5], h[6], h[7], id, s1);
+    q.z = quant4_id(h[8], h[9], h[10], h[11], id, s2);
+    q.w = quant4_id(h[12], h[13], h[14], h[15], id, s3);
     int sum = s0 + s1 + s2 + s3;
     sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);  // the 32-value pair
     const int v0 = c * 256 + 16 * sub;
@@ -381,7 +382,7 @@ __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d
 constexpr int kGemvR = 4, kGemvU = 5;
 
 // LDS carve-up: padded codes | d | bsum32 (Q8_K only) | per-wave block
-// terms | per-wave weight stage (staged formats)
+// terms and a 64-float dump | per-wave weight stage (staged formats)
 __host__ __device__ inline size_t gemv_act_lds_bytes(bool q80, int K) {
     const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
     const size_t nd = q80 ? size_t(K / 32) : size_t(K / 256);
@@ -394,7 +395,7 @@ __host__ __device__ constexpr int stage_chunks() {  // 16-B loads per lane per b
 }
 template <class F, int R, int U>
 __host__ __device__ inline size_t gemv_lds_bytes_t(int K) {
-    const size_t terms = (size_t(4) * R * (K / F::QK) * sizeof(float) + 15) & ~size_t(15);
+    const size_t terms = (size_t(4) * (R * (K / F::QK) + 64) * sizeof(float) + 15) & ~size_t(15);
     return gemv_act_lds_bytes(IsQ80<F>::v, K) + terms + size_t(4) * stage_chunks<F, U>() * 1024;
 }
 
@@ -432,8 +433,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     act.d = reinterpret_cast<const float *>(lds + codes);
     act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
     const size_t act_bytes = gemv_act_lds_bytes(q80, K);
-    const size_t terms_bytes = (size_t(4) * R * nb * sizeof(float) + 15) & ~size_t(15);
-    float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * R * nb;
+    const size_t terms_bytes = (size_t(4) * (R * nb + 64) * sizeof(float) + 15) & ~size_t(15);
+    float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * (R * nb + 64);
+    float *dump = contrib + R * nb;  // stores of lanes that own no term
     uint8_t *stage = lds + act_bytes + terms_bytes + size_t(wid) * NST * 1024;
 
     const int8_t *pq = q80 ? pre0.qs : prek.qs;
@@ -477,7 +479,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     else cpre_fill<q80>(cp, pq, pd, pb, K, act);
     if constexpr (F::kStaged) stage_store();
     lds_barrier();
-    // 4. block terms
+    // 4. block terms. b = f mod nb advances by SLOTS mod nb per wave step;
+    // every lane stores (lanes that own no term into the dump), so the steps
+    // are straight-line code the scheduler can overlap.
+    const int adv = SLOTS % nb;
     for (int t0 = 0; t0 < nblk; t0 += SLOTS * U) {
         if (t0 > 0) {
             if constexpr (F::kStaged) {
@@ -492,15 +497,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
                     raw[u] = F::load(span + size_t(min(t0 + u * SLOTS + g, flast)) * F::BB, k);
             }
         }
+        int b = (t0 + g) % nb;
+        if constexpr (U <= 3) {
+            // all steps' operands first (one LDS round trip), then the math
+            typename F::Raw rs[U];
+            typename F::Act as[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int f = t0 + u * SLOTS + g;
-            const int b = f - (f / nb) * nb;
-            typename F::Raw r;
-            if constexpr (F::kStaged) r = F::load(stage + span_mis + (u * SLOTS + g) * F::BB, k);
-            else r = raw[u];
-            const float c = F::compute(r, F::load_act(act, f < nblk ? b : 0, k), k);
-            if (k == 0 && f < nblk) contrib[f] = c;
+            for (int u = 0; u < U; ++u) {
+                const bool own = t0 + u * SLOTS + g < nblk;
+                if constexpr (F::kStaged) rs[u] = F::load(stage + span_mis + (u * SLOTS + g) * F::BB, k);
+                else rs[u] = raw[u];
+                as[u] = F::load_act(act, own ? b : 0, k);
+                b += adv;
+                b = b >= nb ? b - nb : b;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int f = t0 + u * SLOTS + g;
+                const float c = F::compute(rs[u], as[u], k);
+                *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int f = t0 + u * SLOTS + g;
+                const bool own = f < nblk;
+                typename F::Raw r;
+                if constexpr (F::kStaged) r = F::load(stage + span_mis + (u * SLOTS + g) * F::BB, k);
+                else r = raw[u];
+                const float c = F::compute(r, F::load_act(act, own ? b : 0, k), k);
+                *((k == 0 && own) ? contrib + f : dump + lane) = c;
+                b += adv;
+                b = b >= nb ? b - nb : b;
+            }
         }
     }
     lds_barrier();
@@ -508,7 +537,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     if (lane < nrows) {
         float acc = 0.0f;
         const float *cr = contrib + lane * nb;
-        for (int b = 0; b < nb; ++b) acc += cr[b];
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {  // 8 reads in flight, then the adds in order
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = cr[b + i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc += v[i];
+        }
+        for (; b < nb; ++b) acc += cr[b];
         const int row = row0 + lane;
         if (a.res) acc = acc + a.res[row];
         a.y[row] = acc;
