@@ -224,6 +224,22 @@ __device__ inline uint32_t quant4_id(float h0, float h1, float h2, float h3, flo
     const uint32_t hi = __builtin_amdgcn_perm(uint32_t(q[3]), uint32_t(q[2]), 0x04000C0Cu);  // q2, q3 low bytes
     return lo | hi;
 }
+// The same codes with the rounding done by an fp32 add: for |p| < 2^22,
+// p + 1.5 * 2^23 lies where the fp32 spacing is 1, so the add rounds p to an
+// integer, to nearest even (the default mode), and the code is the low byte
+// of the sum's bits. With |x| <= amax, |x * id| <= 127 (1 + 2^-24)^2 < 127.5:
+// the clamp never binds, and x * id is NaN (code 0, as the conversion of NaN
+// gives) only for a block holding an infinity or a NaN.
+__device__ inline uint32_t quant4_rne(float h0, float h1, float h2, float h3, float id, int &sum) {
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+    const uint32_t y0 = __builtin_bit_cast(uint32_t, h0 * id + kMagic);  // E:979 (separate mul and add)
+    const uint32_t y1 = __builtin_bit_cast(uint32_t, h1 * id + kMagic);
+    const uint32_t y2 = __builtin_bit_cast(uint32_t, h2 * id + kMagic);
+    const uint32_t y3 = __builtin_bit_cast(uint32_t, h3 * id + kMagic);
+    const uint32_t q = __builtin_amdgcn_perm(y1, y0, 0x0C0C0400u) | __builtin_amdgcn_perm(y3, y2, 0x04000C0Cu);
+    sum = __builtin_amdgcn_sdot4(int(q), 0x01010101, 0, false);
+    return q;
+}
 __device__ inline uint32_t quant4(float h0, float h1, float h2, float h3, float amax, int &sum) {
     return quant4_id(h0, h1, h2, h3, q8_inv_scale(amax), sum);
 }

@@ -305,10 +305,10 @@ __device__ inline void x_quant(const XPre &p, int c, int K, bool store, const Ld
     int s0, s1, s2, s3;
     uint4 q;
     const float id = q8_inv_scale(amax);
-    q.x = quant4_id(h[0], h[1], h[2], h[3], id, s0);
-    q.y = quant4_id(h[4], h[5], h[6], h[7], id, s1);
-    q.z = quant4_id(h[8], h[9], h[10], h[11], id, s2);
-    q.w = quant4_id(h[12], h[13], h[14], h[15], id, s3);
+    q.x = quant4_rne(h[0], h[1], h[2], h[3], id, s0);
+    q.y = quant4_rne(h[4], h[5], h[6], h[7], id, s1);
+    q.z = quant4_rne(h[8], h[9], h[10], h[11], id, s2);
+    q.w = quant4_rne(h[12], h[13], h[14], h[15], id, s3);
     int sum = s0 + s1 + s2 + s3;
     sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);  // the 32-value pair
     const int v0 = c * 256 + 16 * sub;
