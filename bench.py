@@ -168,12 +168,12 @@ def bench_ffn(ctx, steps):
         ctx.gemm_multi_dispatch_prequantized(q, None, 1, F, [wd.task(i, y, H)])
 
     ms = timed(ctx, step, steps, 10)
-    alg = block + H * 4 + H * 4  # weights + fp32 x in + fp32 y out (SURVEY-style fused minimum)
+    alg = block + H * 4 + H * 4  # weights + fp32 x in + fp32 y out (the fused minimum)
     for b in (wg.buf, wu.buf, wd.buf, x, g, u, h, y, q):
         ctx.free(b)
     return {"us_per_block": round(ms * 1e3, 3), "algorithmic_bytes": alg,
             "gbs": round(alg / (ms * 1e-3) / 1e9, 1), "replicas": R,
-            "launches": "gemv(gate), gemv(up), swiglu+Q8_K, gemv(down)"}
+            "launches": "gemv(gate+up, one launch), swiglu+Q8_K, gemv(down)"}
 
 
 def bench_prefill(ctx, steps):

@@ -584,14 +584,27 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     return hipGetLastError();
 }
 
+// Rows per wave by the launch's total rows: 4 from 8192 rows, else 2 from
+// 4096, else 1, so that a short tensor (the 2560-row down projection) still
+// spreads over enough waves to stream at full rate.
+template <class F, int U>
+static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
+                                   const Q80View &x0, hipStream_t s) {
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) rows += tasks[i].N;
+    if (rows >= 8192) return launch_gemv_t<F, kGemvR, U>(tasks, n, x32, xk, x0, s);
+    if (rows >= 4096) return launch_gemv_t<F, 2, U>(tasks, n, x32, xk, x0, s);
+    return launch_gemv_t<F, 1, U>(tasks, n, x32, xk, x0, s);
+}
+
 hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                        const Q80View &x0, hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
     switch (type) {
-        case kQ4_K: return launch_gemv_t<FmtQ4K4, kGemvR, 3>(tasks, n, x32, xk, x0, s);
-        case kQ5_K: return launch_gemv_t<FmtQ5K, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
-        case kQ6_K: return launch_gemv_t<FmtQ6K, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
-        case kQ8_0: return launch_gemv_t<FmtQ80, kGemvR, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ4_K: return launch_gemv_rows<FmtQ4K4, 3>(tasks, n, x32, xk, x0, s);
+        case kQ5_K: return launch_gemv_rows<FmtQ5K, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ6_K: return launch_gemv_rows<FmtQ6K, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ8_0: return launch_gemv_rows<FmtQ80, kGemvU>(tasks, n, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -1,7 +1,7 @@
 /*
  * qmm_oracle.c — CPU restatement of the reference engine's quantized-matmul
  * path.  TEST INFRASTRUCTURE ONLY: the parity tests, the smoke check and the
- * CPU-baseline leg of the benchmark use it as the checker; the HIP library
+ * CPU-baseline leg of the benchmark use it to check results; the HIP library
  * never links or calls it.
  *
  * Source followed: src/v182_r22_breakthrough_engine.c (E:<line>), scalar

@@ -1,7 +1,7 @@
 /*
  * qmm_oracle.h — CPU restatement of the reference engine's quantized-matmul
- * path, used ONLY as test infrastructure (the checker for the HIP library and
- * the CPU side of the parity tests).  Nothing in the product links or calls
+ * path, used ONLY as test infrastructure (it checks the HIP library's results
+ * in the parity tests).  Nothing in the product links or calls
  * this code.
  *
  * Every function follows the scalar (non-NEON) branch of

@@ -1,7 +1,7 @@
 """Helpers for the GPU parity tests."""
 import numpy as np
 
-# north-star tolerance for fp32 dot / GEMM outputs: max|y - ref| / max|ref|
+# stated tolerance for fp32 dot / GEMM outputs: max|y - ref| / max|ref|
 TOL = 1e-3
 
 
