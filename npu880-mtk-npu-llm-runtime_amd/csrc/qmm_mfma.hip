@@ -363,10 +363,15 @@ __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
 // is computed, and an explicit vmcnt wait (transfers retire in order)
 // releases chunk ch. Every wave issues the same number of transfers per
 // chunk (surplus ones target a dump line), so the wait counts are static.
+// With KMAX > 0 (small M) the tokens' codes and scales for the whole of
+// K <= KMAX are transferred once, ahead of the first chunk, and stay in LDS;
+// the slots then carry weights only, so more chunks fit in flight.
 
-template <class F, int WR_, int WT_, int PR_, int PT_, int KS_, int TR_, int PD_, int BUDGET>
+template <class F, int WR_, int WT_, int PR_, int PT_, int KS_, int TR_, int PD_, int BUDGET, int KMAX_ = 0>
 struct TileCfg {
     static constexpr int WR = WR_, WT = WT_, PR = PR_, PT = PT_, KS = KS_, TR = TR_, PD = PD_;
+    static constexpr int KMAX = KMAX_;
+    static constexpr bool AR = KMAX > 0;  // codes and scales resident
     static_assert(PR * PT * KS == 4, "4 waves");
     static_assert(TR == 16 || (TR == 8 && WT == 1 && PT == 1), "8 resident tokens: one token tile");
     static constexpr int ROWS = 16 * WR * PR;
@@ -374,12 +379,15 @@ struct TileCfg {
     static constexpr int wcr(int k) { return ((k * F::BB + 30) / 16) | 1; }  // odd: rows 4 banks apart
     static constexpr int acr(int k) { return k * F::QK / 16 + 1; }
     static constexpr int nwi(int k) { return (ROWS * wcr(k) + 63) / 64; }
-    static constexpr int nai(int k) { return (TOK * acr(k) + 63) / 64; }
-    static constexpr int ndi(int k) { return (k * TOK + 63) / 64; }
+    static constexpr int nai(int k) { return AR ? 0 : (TOK * acr(k) + 63) / 64; }
+    static constexpr int ndi(int k) { return AR ? 0 : (k * TOK + 63) / 64; }
+    // resident codes (rows of K / 16 + 1 units of 16 B) and scales ([block][token])
+    static constexpr int AR_BYTES = AR ? (TOK * (KMAX / 16 + 1) + 63) / 64 * 1024 : 0;
+    static constexpr int DR_BYTES = AR ? (KMAX / F::QK * TOK + 63) / 64 * 256 : 0;
     static constexpr int slot(int k) { return nwi(k) * 1024 + nai(k) * 1024 + ndi(k) * 256; }
     static constexpr int per_wave(int k) { return (nwi(k) + 3) / 4 + (nai(k) + 3) / 4 + (ndi(k) + 3) / 4; }
     static constexpr int part(int k) { return KS > 1 ? k * TOK * ROWS * 4 : 0; }
-    static constexpr int total(int k) { return PD * slot(k) + part(k) + 1024; }
+    static constexpr int total(int k) { return PD * slot(k) + AR_BYTES + DR_BYTES + part(k) + 1024; }
     static constexpr bool fits(int k) { return total(k) <= BUDGET && (PD - 1) * per_wave(k) <= 63; }
     static constexpr int pick() {
         int k = KS;
@@ -392,7 +400,8 @@ struct TileCfg {
     static constexpr int NWW = (NWI + 3) / 4, NAW = (NAI + 3) / 4, NDW = (NDI + 3) / 4;
     static constexpr int L = NWW + NAW + NDW;  // transfers per wave per chunk
     static constexpr int OFF_A = NWI * 1024, OFF_D = OFF_A + NAI * 1024, SLOT = slot(KCB);
-    static constexpr int OFF_P = PD * SLOT, OFF_DUMP = OFF_P + part(KCB), LDS = total(KCB);
+    static constexpr int OFF_AR = PD * SLOT, OFF_DR = OFF_AR + AR_BYTES;
+    static constexpr int OFF_P = OFF_DR + DR_BYTES, OFF_DUMP = OFF_P + part(KCB), LDS = total(KCB);
     static_assert(fits(KCB), "tile does not fit the LDS budget");
     static_assert(KS == 1 || TOK * ROWS <= 4 * 256, "K-split tiles: at most 4 outputs per thread");
 };
@@ -410,6 +419,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     const int n0 = bx * C::ROWS, m0 = int(blockIdx.y) * C::TOK;
     const int K = a.K, nb = K / F::QK;
     const int nchunks = (nb + KCB - 1) / KCB;
+    const int acr_rt = C::AR ? K / 16 + 1 : C::ACR;  // codes row stride, 16-B units
 
     // descriptors: this workgroup's rows (from the 16-B boundary at or below
     // the first), the M tokens' codes, their block scales
@@ -425,7 +435,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     const uint32_t lds0 = lds_addr(lds);
 
     // per-lane transfer offsets (chunk 0); lanes past a region's pieces get kFar
-    uint32_t wo[C::NWW], wp[C::NWW], ao[C::NAW], dof[C::NDW];
+    uint32_t wo[C::NWW], wp[C::NWW], ao[C::NAW > 0 ? C::NAW : 1], dof[C::NDW > 0 ? C::NDW : 1];
 #pragma unroll
     for (int s = 0; s < C::NWW; ++s) {
         const int p = (s * 4 + wid) * 64 + lane;
@@ -487,13 +497,16 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t *ws = lds + sl * C::SLOT;
-        const int8_t *as = reinterpret_cast<const int8_t *>(ws + C::OFF_A);
-        const float *ds = reinterpret_cast<const float *>(ws + C::OFF_D);
+        const int8_t *as = reinterpret_cast<const int8_t *>(C::AR ? lds + C::OFF_AR : ws + C::OFF_A);
+        const float *ds = reinterpret_cast<const float *>(C::AR ? lds + C::OFF_DR : ws + C::OFF_D);
         const uint32_t cw = uint32_t(ch) * uint32_t(KCB * F::BB);
 #pragma unroll
         for (int jj = 0; jj < KCB / KS; ++jj) {
             const int j = jj * KS + kp;
             const bool valid = ch * KCB + j < nb;
+            // block index into the codes and scales: of the chunk's slot, or of
+            // the resident arrays (block 0 stands in for blocks past K)
+            const int jr = C::AR ? (valid ? ch * KCB + j : 0) : j;
 #pragma unroll
             for (int wr = 0; wr < WR; ++wr) {
                 const int rl = (pr * WR + wr) * 16 + nl;  // lane's weight row in the tile
@@ -513,7 +526,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
 #pragma unroll
                 for (int wt = 0; wt < WT; ++wt) {
                     const int tl = (pt * WT + wt) * TR + (nl & (TR - 1));  // lane's A token
-                    const int8_t *arow = as + tl * (C::ACR * 16) + j * F::QK;
+                    const int8_t *arow = as + tl * (acr_rt * 16) + jr * F::QK;
                     int S[4] = {0, 0, 0, 0};
                     int4v Mb = {0, 0, 0, 0};
                     if constexpr (F::kSplit) {
@@ -543,7 +556,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
                     }
                     // dx of output tokens 4 cl + r of this token tile (tokens
                     // past TR read neighbouring scales; their outputs are not kept)
-                    const float4 dx4 = *reinterpret_cast<const float4 *>(ds + j * C::TOK + (pt * WT + wt) * TR + 4 * cl);
+                    const float4 dx4 = *reinterpret_cast<const float4 *>(ds + jr * C::TOK + (pt * WT + wt) * TR + 4 * cl);
                     const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -582,6 +595,24 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
         __builtin_amdgcn_s_barrier();  // every wave is done with slot sl
     };
 
+    // resident codes (row stride K / 16 + 1 units) and scales, once, ahead of
+    // every chunk: the first chunk's wait covers them
+    if constexpr (C::AR) {
+        const int nar = (C::TOK * acr_rt + 63) / 64;
+        for (int i = wid; i < nar; i += 4) {
+            const int p = i * 64 + lane;
+            const int tok = p / acr_rt, pc = p - tok * acr_rt;
+            dma16(ra, tok < C::TOK ? uint32_t(m0 + tok) * uint32_t(K) + 16u * uint32_t(pc) : kFar,
+                  lds0 + uint32_t(C::OFF_AR + i * 1024));
+        }
+        const int ndr = (nb * C::TOK + 63) / 64;
+        for (int i = wid; i < ndr; i += 4) {
+            const int e = i * 64 + lane;
+            const int j = e / C::TOK, tok = e - j * C::TOK;
+            dma4(rd, j < nb ? (uint32_t(m0 + tok) * uint32_t(nb) + uint32_t(j)) * 4u : kFar,
+                 lds0 + uint32_t(C::OFF_DR + i * 256));
+        }
+    }
 #pragma unroll
     for (int p = 0; p + 1 < C::PD; ++p) issue(p, p);
     int ch = 0;
@@ -643,7 +674,12 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     using G = typename Folded<F>::T;
     //                          WR WT PR PT KS TR PD  LDS budget
     if constexpr (!F::kSplit) {
+        // codes resident for K <= 2560 (the hidden size of the workload)
+        if (a.M <= 8 && a.K <= 2560)
+            return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 53 * 1024, 2560>, F>(tasks, n, x, s);
         if (a.M <= 8) return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 52 * 1024>, F>(tasks, n, x, s);
+        if (a.M <= 16 && a.K <= 2560)
+            return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 80 * 1024, 2560>, F>(tasks, n, x, s);
         if (a.M <= 16) return launch_tile_t<TileCfg<F, 1, 1, 2, 1, 2, 16, 2, 56 * 1024>, F>(tasks, n, x, s);
     }
     if constexpr (!std::is_same_v<G, F>) {

@@ -69,6 +69,14 @@ def test_unaligned_tensor_end(ctx, oracle, type_id, K, M):
     _run(ctx, oracle, type_id, 45, K, M, seed=500 + K + M)
 
 
+@pytest.mark.parametrize("type_id,K,M", [(TYPE_Q4_K, 4096, 8), (TYPE_Q6_K, 9728, 12), (TYPE_Q8_0, 3072, 5),
+                                         (TYPE_Q5_K, 2816, 16)])
+def test_mfma_small_m_long_k(ctx, oracle, type_id, K, M):
+    """M <= 16 with K past the resident-codes limit (2560): codes stream with
+    the weights, chunk by chunk."""
+    _run(ctx, oracle, type_id, 70, K, M, seed=900 + K + M)
+
+
 @pytest.mark.parametrize("M", [8, 16, 32, 64])
 def test_tree_verify_q4k(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
