@@ -86,66 +86,12 @@ struct MQ5K {
     }
 };
 
-// Q6_K: unit u = (hf, i, is) = (u >> 3, (u >> 1) & 3, u & 1), 16 values
-// 128hf + 32i + 16is + l, scale sc[8hf + 2i + is]. Lanes c = 0, 1 hold the
-// 8 values l = 8c + t; lanes c = 2, 3 supply zero weights.
+// Q6_K block constants; the kernels use the folded form MQ6KS below at
+// every M (sixteen 16-value scale groups would leave half of each
+// 16x16x32 MFMA's k-slices empty).
 struct MQ6K {
     static constexpr int NU = 16, QK = 256, BB = 210;
     static constexpr bool kMin = false, kSplit = false;
-    struct W { uint2 a[4], b[4], qh[4]; uint2 s0, s1; uint32_t d; };
-    __device__ static W load(const uint8_t *blk, int c) {
-        W w;
-        const int c2 = c & 1;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int is = 0; is < 2; ++is) {
-                const int p = 2 * hf + is, l = 16 * is + 8 * c2;
-                w.a[p] = ld8_a2(blk + 64 * hf + l);
-                w.b[p] = ld8_a2(blk + 64 * hf + 32 + l);
-                w.qh[p] = ld8_a2(blk + 128 + 32 * hf + l);
-            }
-        w.s0 = ld8_a2(blk + 192);
-        w.s1 = ld8_a2(blk + 200);
-        w.d = ld16b_a2(blk + 208);
-        return w;
-    }
-    __device__ static W load_lds(const uint8_t *blk, int c) {
-        W w;
-        const int c2 = c & 1;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int is = 0; is < 2; ++is) {
-                const int p = 2 * hf + is, l = 16 * is + 8 * c2;
-                w.a[p] = lds8_a2(blk + 64 * hf + l);
-                w.b[p] = lds8_a2(blk + 64 * hf + 32 + l);
-                w.qh[p] = lds8_a2(blk + 128 + 32 * hf + l);
-            }
-        w.s0 = lds8_a2(blk + 192);
-        w.s1 = lds8_a2(blk + 200);
-        w.d = lds16b_a2(blk + 208);
-        return w;
-    }
-    __device__ static int koff(int u, int c) {
-        return 128 * (u >> 3) + 32 * ((u >> 1) & 3) + 16 * (u & 1) + 8 * (c & 1);
-    }
-    __device__ static uint2 bop(const W &w, int u, int c) {
-        if (c >= 2) return make_uint2(0u, 0u);
-        const int hf = u >> 3, i = (u >> 1) & 3, is = u & 1, p = 2 * hf + is;
-        const uint2 src = (i & 1) ? w.b[p] : w.a[p];
-        const int nsh = (i >> 1) * 4;
-        const int hsh = 2 * i;
-        const uint32_t x = ((src.x >> nsh) & 0x0F0F0F0Fu) | (((w.qh[p].x >> hsh) & 0x03030303u) << 4);
-        const uint32_t y = ((src.y >> nsh) & 0x0F0F0F0Fu) | (((w.qh[p].y >> hsh) & 0x03030303u) << 4);
-        return make_uint2(sub32_bytes(x), sub32_bytes(y));
-    }
-    __device__ static int scale(const W &w, int u) {
-        const int idx = 8 * (u >> 3) + 2 * ((u >> 1) & 3) + (u & 1);
-        const uint2 s = (idx < 8) ? w.s0 : w.s1;
-        const uint64_t s64 = (uint64_t(s.y) << 32) | s.x;
-        return int(int8_t(uint8_t(s64 >> (8 * (idx & 7)))));
-    }
 };
 
 // Q8_0: one unit per 32-value block; lane c holds values 8c + t.
@@ -183,8 +129,8 @@ struct MQ5KS : MQ5K {
     static constexpr int kShift = 8;  // S = (D1 << 8) + D2
 };
 
-// Q6_K with the scales folded into the B operand (token tiles >= 2 per
-// wave): w = (q - 32) * sc lies in [-4064, 4096]; in 16-bit lanes
+// Q6_K with the scales folded into the B operand (at every M): w = (q - 32)
+// * sc lies in [-4064, 4096]; in 16-bit lanes
 // P = w + 128 = q * sc + (128 - 32 sc) (one packed multiply-add), and
 // w = 256 hi + lo with hi = the high byte of P (|hi| <= 16) and
 // lo = (P mod 256) - 128, i.e. P's low byte xor 0x80: two int8 operands,
@@ -312,7 +258,9 @@ template <> struct ActOf<MQ80> { using T = Q80View; };
 template <class F> struct Folded { using T = F; };
 template <> struct Folded<MQ4K> { using T = MQ4KS; };
 template <> struct Folded<MQ5K> { using T = MQ5KS; };
-template <> struct Folded<MQ6K> { using T = MQ6KS; };
+// formats run with one token tile per wave (M <= 16): the unfolded ones, and
+// Q6_K folded
+template <class F> constexpr bool kSmallM = !F::kSplit || std::is_same_v<F, MQ6KS>;
 
 // Scales / mins of the lane's row for the current block.
 template <class F> struct Scales { int sc[F::NU]; int m[F::NU]; float d, dmin; };
@@ -327,14 +275,6 @@ __device__ inline void decode_scales(const typename F::W &w, Scales<F> &s) {
         for (int u = 0; u < 8; ++u) scale_min_k4(u, w.h.y, w.h.z, w.h.w, s.sc[u], s.m[u]);
         s.d = fp16_bits_to_f32(w.h.x & 0xFFFFu);
         s.dmin = fp16_bits_to_f32(w.h.x >> 16);
-    } else if constexpr (F::NU == 16) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            s.sc[u] = F::scale(w, u);
-            s.m[u] = 0;
-        }
-        s.d = fp16_bits_to_f32(w.d);
-        s.dmin = 0.0f;
     } else {
         s.sc[0] = 1;
         s.m[0] = 0;
@@ -673,7 +613,7 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
     using G = typename Folded<F>::T;
     //                          WR WT PR PT KS TR PD  LDS budget
-    if constexpr (!F::kSplit) {
+    if constexpr (kSmallM<F>) {
         // codes resident for K <= 2560 (the hidden size of the workload)
         if (a.M <= 8 && a.K <= 2560)
             return launch_tile_t<TileCfg<F, 1, 1, 1, 1, 4, 8, 2, 53 * 1024, 2560>, F>(tasks, n, x, s);
@@ -703,7 +643,7 @@ hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView
     switch (type) {
         case kQ4_K: return launch_tile<MQ4K>(tasks, n, xk, s);
         case kQ5_K: return launch_tile<MQ5K>(tasks, n, xk, s);
-        case kQ6_K: return launch_tile<MQ6K>(tasks, n, xk, s);
+        case kQ6_K: return launch_tile<MQ6KS>(tasks, n, xk, s);
         case kQ8_0: return launch_tile<MQ80>(tasks, n, x0, s);
         default: return hipErrorInvalidValue;
     }
