@@ -552,6 +552,120 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     }
 }
 
+// --------------------------------------------- persistent batch-1 kernel
+// For one task with many more row groups than workgroups fit at once (the
+// LM head). A fixed grid: wave w of workgroup i takes the R-row groups
+// (i + j G) * 4 + w, j = 0, 1, ...; the activation row is filled once per
+// workgroup, and a wave loads its next group's bytes into registers while it
+// computes the current one (one batch per group: R nb <= SLOTS U). After the
+// fill the waves never synchronize with each other.
+template <class F, int R, int U, bool FUSED>
+__global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const float *__restrict__ x32,
+                                                           Q8KView prek, Q80View pre0) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
+    constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
+    constexpr bool q80 = IsQ80<F>::v;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int g = lane / G, k = lane % G;
+    const int K = a.K, nb = K / F::QK;
+    const int ngroups = (a.N + R - 1) / R;
+
+    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
+    LdsAct act;
+    act.qs = reinterpret_cast<const int8_t *>(lds);
+    act.d = reinterpret_cast<const float *>(lds + codes);
+    act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
+    const size_t act_bytes = gemv_act_lds_bytes(q80, K);
+    const size_t terms_bytes = (size_t(4) * (R * nb + 64) * sizeof(float) + 15) & ~size_t(15);
+    float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * (R * nb + 64);
+    float *dump = contrib + R * nb;
+    uint8_t *stage = lds + act_bytes + terms_bytes + size_t(wid) * NST * 1024;
+
+    const int8_t *pq = q80 ? pre0.qs : prek.qs;
+    const float *pd = q80 ? pre0.d : prek.d;
+    const int32_t *pb = prek.bs;
+
+    // a group's bytes from the 16-B boundary at or below its first byte;
+    // chunk indices clamped so every lane issues its loads
+    uint4 st[NST];
+    auto stage_load = [&](int gr) __attribute__((always_inline)) {
+        const int rows = max(0, min(R, a.N - gr * R));
+        const uint8_t *span = a.w + size_t(rows > 0 ? gr * R : 0) * a.row_bytes;
+        const int mis = int(reinterpret_cast<uintptr_t>(span) & 15);
+        const int nchunks = (mis + max(rows * nb, 1) * F::BB + 15) >> 4;
+#pragma unroll
+        for (int j = 0; j < NST; ++j) st[j] = ld16_nt(span - mis + 16 * min(64 * j + lane, nchunks - 1));
+    };
+
+    int gw = int(blockIdx.x) * 4 + wid;
+    const int stride = int(gridDim.x) * 4;
+    // 1. the activation row, then the first group's bytes
+    XPre xp;
+    CPre cp;
+    if constexpr (FUSED) x_load(x32, K, x_chunk(0, K), xp);
+    else cpre_load<q80>(pq, pd, pb, K, cp);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_load(min(gw, ngroups - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. the activations into LDS, once
+    if constexpr (FUSED) x_fill<q80>(xp, x32, K, act);
+    else cpre_fill<q80>(cp, pq, pd, pb, K, act);
+    lds_barrier();
+    // 3. groups
+    const int adv = SLOTS % nb;
+    for (; gw < ngroups; gw += stride) {
+        const int row0 = gw * R;
+        const int nrows = min(R, a.N - row0);
+        const int nblk = nrows * nb;
+        const int mis = int(reinterpret_cast<uintptr_t>(a.w + size_t(row0) * a.row_bytes) & 15);
+        // all lanes of this wave are done with the previous group's stage and terms
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        stage_load(min(gw + stride, ngroups - 1));  // the next group, in flight during the math
+        int b = g % nb;
+        typename F::Raw rs[U];
+        typename F::Act as[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool own = u * SLOTS + g < nblk;
+            rs[u] = F::load(stage + mis + (u * SLOTS + g) * F::BB, k);
+            as[u] = F::load_act(act, own ? b : 0, k);
+            b += adv;
+            b = b >= nb ? b - nb : b;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int f = u * SLOTS + g;
+            const float c = F::compute(rs[u], as[u], k);
+            *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        // per row, blocks in order (eval_single_lm_row_dot's accumulation)
+        if (lane < nrows) {
+            float acc = 0.0f;
+            const float *cr = contrib + lane * nb;
+            int bb = 0;
+            for (; bb + 8 <= nb; bb += 8) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = cr[bb + i];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc += v[i];
+            }
+            for (; bb < nb; ++bb) acc += cr[bb];
+            const int row = row0 + lane;
+            if (a.res) acc = acc + a.res[row];
+            a.y[row] = acc;
+        }
+    }
+}
+
 size_t gemv_lds_bytes(uint32_t type, int K) {
     switch (type) {
         case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K);
@@ -560,6 +674,27 @@ size_t gemv_lds_bytes(uint32_t type, int K) {
         case kQ8_0: return gemv_lds_bytes_t<FmtQ80, kGemvR, kGemvU>(K);
         default: return 0;
     }
+}
+
+// the persistent grid: 3 workgroups per CU of the current device
+static int persist_wgs() {
+    static int cus[64] = {};  // per device; concurrent first calls store the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return 3 * cus[dev];
+}
+template <class F, int R, int U>
+static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, const Q8KView &xk, const Q80View &x0,
+                                        size_t lds, int wgs, hipStream_t s) {
+    const dim3 grid{unsigned(wgs)};
+    if (x32) hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, true>), grid, dim3(256), lds, s, a, x32, xk, x0);
+    else hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, false>), grid, dim3(256), lds, s, a, x32, xk, x0);
+    return hipGetLastError();
 }
 
 template <class F, int R, int U>
@@ -574,6 +709,14 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     }
     const size_t lds = gemv_lds_bytes_t<F, R, U>(tasks[0].K);
     const dim3 grid(unsigned(g.wg0[n]));
+    // one task with many more row groups than fit at once: a persistent grid
+    if constexpr (F::kStaged) {
+        const int nb = tasks[0].K / F::QK;
+        if (n == 1 && R * nb <= (64 / F::G) * U && g.wg0[1] > 12 * 256) {
+            const int wgs = persist_wgs();
+            if (g.wg0[1] > 4 * wgs) return launch_gemv_persist_t<F, R, U>(tasks[0], x32, xk, x0, lds, wgs, s);
+        }
+    }
     if (n == 1) {
         if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
         else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);

@@ -43,6 +43,14 @@ def test_gemv_q6k_lm_head_shape(ctx, oracle):
     _run(ctx, oracle, TYPE_Q6_K, 151936, 2560, 1, seed=1001)
 
 
+@pytest.mark.parametrize("type_id,N,K,residual", [(TYPE_Q4_K, 60001, 256, True), (TYPE_Q8_0, 50003, 512, False),
+                                                  (TYPE_Q6_K, 49157, 768, True)])
+def test_gemv_tall_tensors(ctx, oracle, type_id, N, K, residual):
+    """Tensors tall enough for the persistent grid (several row groups per
+    wave, the next group prefetched), with ragged last groups."""
+    _run(ctx, oracle, type_id, N, K, 1, seed=1100 + type_id, residual=residual)
+
+
 @pytest.mark.parametrize("type_id,N,K", [(TYPE_Q6_K, 2560, 9728), (TYPE_Q5_K, 4096, 2560),
                                          (TYPE_Q8_0, 2560, 2560), (TYPE_Q4_K, 2560, 4096)])
 def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
