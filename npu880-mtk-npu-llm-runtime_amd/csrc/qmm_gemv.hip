@@ -676,17 +676,18 @@ size_t gemv_lds_bytes(uint32_t type, int K) {
     }
 }
 
-// the persistent grid: 3 workgroups per CU of the current device
-static int persist_wgs() {
-    static int cus[64] = {};  // per device; concurrent first calls store the same value
+// CUs of the current device (cached per device; concurrent first calls store
+// the same value)
+static int cu_count() {
+    static int cus[64] = {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
     if (cus[dev] == 0) {
         int n = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
         cus[dev] = n;
     }
-    return 3 * cus[dev];
+    return cus[dev];
 }
 template <class F, int R, int U>
 static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, const Q8KView &xk, const Q80View &x0,
@@ -709,12 +710,15 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     }
     const size_t lds = gemv_lds_bytes_t<F, R, U>(tasks[0].K);
     const dim3 grid(unsigned(g.wg0[n]));
-    // one task with many more row groups than fit at once: a persistent grid
+    // one task of at least two workgroups' rows per CU: a persistent grid of
+    // 5/8 of a workgroup per row group, at most 3 per CU (measured: 380
+    // workgroups for 608 groups, 768 for the 9496 of the LM head)
     if constexpr (F::kStaged) {
         const int nb = tasks[0].K / F::QK;
-        if (n == 1 && R * nb <= (64 / F::G) * U && g.wg0[1] > 12 * 256) {
-            const int wgs = persist_wgs();
-            if (g.wg0[1] > 4 * wgs) return launch_gemv_persist_t<F, R, U>(tasks[0], x32, xk, x0, lds, wgs, s);
+        const int cus = cu_count();
+        if (n == 1 && R * nb <= (64 / F::G) * U && g.wg0[1] >= 2 * cus) {
+            const int wgs = min(3 * cus, g.wg0[1] * 5 / 8);
+            return launch_gemv_persist_t<F, R, U>(tasks[0], x32, xk, x0, lds, wgs, s);
         }
     }
     if (n == 1) {
