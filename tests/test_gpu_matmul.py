@@ -204,6 +204,34 @@ def test_prequantized_dispatch_and_strides(ctx, oracle):
         ctx.free(b)
 
 
+@pytest.mark.parametrize("type_id,specs", [
+    (TYPE_Q4_K, [(9000, True), (7001, False), (4003, True)]),
+    (TYPE_Q6_K, [(5000, False), (3001, True), (6007, False)]),
+])
+def test_task_groups_large(ctx, oracle, type_id, specs):
+    """Batch-1 task groups of thousands of rows per task (one launch of
+    several workgroups per CU), ragged ends and residuals."""
+    K = 2560
+    say(f"large task group {NAMES[type_id]} {specs}")
+    x = synth.activations(1, K, seed=23)
+    ws = [synth.weights(type_id, n, K, seed=70 + i) for i, (n, _) in enumerate(specs)]
+    ress = [synth.activations(1, n, seed=90 + i) if r else None for i, (n, r) in enumerate(specs)]
+    xb = ctx.upload(x)
+    wbs = [ctx.weight_upload(w, type_id, n, K) for w, (n, _) in zip(ws, specs)]
+    ybs = [ctx.malloc(n * 4) for n, _ in specs]
+    rbs = [ctx.upload(r) if r is not None else None for r in ress]
+    tasks = [qmm_hip.MatrixTask(wb, type_id, n, K, yb, n, rb, n if rb is not None else 0)
+             for wb, yb, rb, (n, _) in zip(wbs, ybs, rbs, specs)]
+    ctx.gemm_multi_dispatch(xb, 1, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=type_id, rows=n, **({"residual": r} if r is not None else {}))
+                                 for w, r, (n, _) in zip(ws, ress, specs)])
+    for i, ((n, _), yb) in enumerate(zip(specs, ybs)):
+        check_outputs(ctx.d2h(yb, np.float32, (1, n)), refs[i], f"task {i}")
+    for b in [xb] + wbs + ybs + [r for r in rbs if r is not None]:
+        ctx.free(b)
+
+
 @pytest.mark.parametrize("M", [1, 6, 70])
 def test_task_groups_one_launch(ctx, oracle, M):
     """Many tasks of one type (more than one launch's group of 8), tiny-N tasks
