@@ -625,7 +625,9 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     if constexpr (!std::is_same_v<G, F>) {
         return launch_tile<G>(tasks, n, x, s);
     } else {
-        if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
+        if (a.M <= 32) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
+        // 64 rows x 32 tokens: half the activation re-reads of 32-row tiles
+        if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 4, 1, 1, 16, 2, 53 * 1024>, F>(tasks, n, x, s);
         // folded formats: one row tile decoded per wave, shared by 4 (Q6_K: 3)
         // token tiles
         if constexpr (F::kSplit && F::NU > 8)
