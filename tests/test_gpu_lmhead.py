@@ -75,3 +75,54 @@ def test_eval_rows(ctx, oracle, M):
     assert np.array_equal(ctx.d2h(bi, np.uint32, (M,)), ei)
     for b in (wb, idb, vb, bv, bi, qb):
         ctx.free(b)
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q6_K, TYPE_Q4_K])
+def test_lm_head_tall_chunks(ctx, oracle, type_id):
+    """One row, no logits requested, chunks tall enough for the persistent
+    GEMV grid. Ties planted inside a chunk and across chunks (the earlier row
+    must win)."""
+    N, K = 60000, 2560
+    say(f"tall lm head chunks type={type_id}")
+    w, q, qb = _setup(ctx, oracle, type_id, N, K, 1, seed=650 + type_id)
+    rb = synth.row_bytes(type_id, K)
+    lg_all, _, _ = oracle.lm_head_argmax(q, w, type_id, N, 0, np.full(1, -1e30, np.float32), np.zeros(1, np.uint32))
+    top = int(np.argmax(lg_all[0]))
+    for dst in (min(top + 9001, N - 1), (top + 30011) % N):
+        if dst != top:
+            w[dst * rb:(dst + 1) * rb] = w[top * rb:(top + 1) * rb]
+    wb = ctx.weight_upload(w, type_id, N, K)
+    bv = ctx.upload(np.full(1, -1e30, np.float32))
+    bi = ctx.upload(np.zeros(1, np.uint32))
+    ebv, ebi = np.full(1, -1e30, np.float32), np.zeros(1, np.uint32)
+    for r0, r1 in [(0, 25000), (25000, N)]:
+        ctx.lm_head_argmax(qb, None, 1, K, wb.ptr + r0 * rb, type_id, r1 - r0, r0, None, bv, bi)
+        _, ebv, ebi = oracle.lm_head_argmax(q, w[r0 * rb:r1 * rb], type_id, r1 - r0, r0, ebv, ebi)
+    ctx.sync()
+    got_v, got_i = ctx.d2h(bv, np.float32, (1,)), ctx.d2h(bi, np.uint32, (1,))
+    assert np.array_equal(got_v.view(np.uint32), ebv.view(np.uint32)), (got_v, ebv)
+    assert np.array_equal(got_i, ebi), (got_i, ebi)
+    for b in (wb, bv, bi, qb):
+        ctx.free(b)
+
+
+def test_eval_rows_many(ctx, oracle):
+    """9000 indexed rows at M = 1 without the values requested (list
+    positions mapped to row ids, no fp16 rounding)."""
+    N, K = 12000, 2560
+    say("many eval rows")
+    w, q, qb = _setup(ctx, oracle, TYPE_Q6_K, N, K, 1, seed=760)
+    ids = np.random.default_rng(9).integers(0, N, 9000).astype(np.uint32)
+    ids[7000] = ids[5]  # a duplicate: the earlier position keeps the tie
+    wb = ctx.weight_upload(w, TYPE_Q6_K, N, K)
+    idb = ctx.upload(ids)
+    bv = ctx.upload(np.full(1, -1e30, np.float32))
+    bi = ctx.upload(np.zeros(1, np.uint32))
+    ctx.eval_rows_argmax(qb, None, 1, K, wb, TYPE_Q6_K, idb, len(ids), None, bv, bi)
+    ctx.sync()
+    _, ev, ei = oracle.eval_rows_argmax(q, w, TYPE_Q6_K, K, ids, np.full(1, -1e30, np.float32),
+                                        np.zeros(1, np.uint32))
+    assert np.array_equal(ctx.d2h(bv, np.float32, (1,)).view(np.uint32), ev.view(np.uint32))
+    assert np.array_equal(ctx.d2h(bi, np.uint32, (1,)), ei)
+    for b in (wb, idb, bv, bi, qb):
+        ctx.free(b)
