@@ -155,6 +155,9 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
     if (M <= 0 || K <= 0) return fail(ctx, QMM_EINVAL, "M and K must be positive");
     if (!tasks || n_tasks <= 0) return fail(ctx, QMM_EINVAL, "empty task list");
     if (n_tasks > 256) return fail(ctx, QMM_EINVAL, "more than 256 tasks in one dispatch");
+    // the M >= 2 kernels address the activation codes with 32-bit offsets
+    if (M > 1 && int64_t(M) * int64_t(K) >= (int64_t(1) << 31))
+        return fail(ctx, QMM_ESHAPE, "M * K must stay below 2^31 for M >= 2");
     *need_q8k = *need_q80 = false;
     int total = 0;
     for (int t = 0; t < n_tasks; ++t) {

@@ -76,6 +76,8 @@ def test_bad_sizes(ctx, bufs):
     assert _dispatch(ctx, bufs["x"], 1, 300, _task(bufs, cols=300)) == qmm_hip.QMM_ESHAPE
     t = _task(bufs, dst_stride=1)
     assert _dispatch(ctx, bufs["x"], 4, bufs["K"], t) == qmm_hip.QMM_EINVAL
+    # M * K past 2^31 at M >= 2 (checked before any allocation or launch)
+    assert _dispatch(ctx, bufs["x"], (1 << 31) // bufs["K"], bufs["K"], _task(bufs)) == qmm_hip.QMM_ESHAPE
     arr = (qmm_hip._Task * 1)(_task(bufs))
     assert ctx.lib.qmm_gemm_multi_dispatch(ctx._h, C.c_void_p(int(bufs["x"])), 1, bufs["K"], arr, 0) == qmm_hip.QMM_EINVAL
     assert ctx.lib.qmm_gemm_multi_dispatch(ctx._h, None, 1, bufs["K"], arr, 1) == qmm_hip.QMM_EINVAL
