@@ -731,16 +731,18 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     return hipGetLastError();
 }
 
-// Rows per wave by the launch's total rows: 4 from 8192 rows, else 2 from
-// 4096, else 1, so that a short tensor (the 2560-row down projection) still
-// spreads over enough waves to stream at full rate.
+// Rows per wave by the launch's total rows and K (measured per shape): the
+// k-quants take 4 from 4096 rows, else 2 up to K = 4096, else 1 (the 2560-row
+// K = 9728 down projection: 12.4 -> 8.9 us with 1); Q8_0 (34-B blocks, 5
+// wave steps per batch) takes 4 from 8192 rows, 2 from 4096, else 1.
 template <class F, int U>
 static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                                    const Q80View &x0, hipStream_t s) {
     int64_t rows = 0;
     for (int i = 0; i < n; ++i) rows += tasks[i].N;
-    if (rows >= 8192) return launch_gemv_t<F, kGemvR, U>(tasks, n, x32, xk, x0, s);
-    if (rows >= 4096) return launch_gemv_t<F, 2, U>(tasks, n, x32, xk, x0, s);
+    const bool q80 = IsQ80<F>::v;
+    if (rows >= (q80 ? 8192 : 4096)) return launch_gemv_t<F, kGemvR, U>(tasks, n, x32, xk, x0, s);
+    if (q80 ? rows >= 4096 : tasks[0].K <= 4096) return launch_gemv_t<F, 2, U>(tasks, n, x32, xk, x0, s);
     return launch_gemv_t<F, 1, U>(tasks, n, x32, xk, x0, s);
 }
 
