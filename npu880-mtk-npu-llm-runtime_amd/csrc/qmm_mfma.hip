@@ -283,6 +283,18 @@ __device__ inline void decode_scales(const typename F::W &w, Scales<F> &s) {
     }
 }
 
+// Q4_K / Q5_K scales and mins of the 8 sub-blocks from the 12 scale bytes
+// (three little-endian dwords s0..s2), four to a dword: sub-block u is byte
+// u & 3 of sc[u >> 2] / m[u >> 2] — get_scale_min_k4 (E:743-749) done on
+// whole dwords (j < 4: low 6 bits of bytes j, j + 4; j >= 4: the nibbles of
+// byte j + 4 under the top 2 bits of bytes j - 4, j).
+__device__ inline void scales_k4_packed(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t (&sc)[2], uint32_t (&m)[2]) {
+    sc[0] = s0 & 0x3F3F3F3Fu;
+    m[0] = s1 & 0x3F3F3F3Fu;
+    sc[1] = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    m[1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+}
+
 __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
     const long av = (long)(((uint64_t)a.y << 32) | a.x);
     const long bv = (long)(((uint64_t)b.y << 32) | b.x);
@@ -592,6 +604,258 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     }
 }
 
+// ====================================================== resident-tile GEMM
+// Small M (up to 16 * TT tokens) of a k-quant over K <= NBK * 4 * 256: one
+// workgroup per CU owns RT <= RTM consecutive 16-row tiles (of the group's
+// concatenated row tiles) and every token, with one wave per (tile, K part):
+// wave (rt, kp) computes tile rt over the kp-th of 4 contiguous parts of the
+// K blocks. At start the waves move the M x K codes (rows padded by 16 B)
+// and the M x nb block scales into LDS (1-KB buffer -> LDS transfers, each
+// code fetched once per CU), then each wave its own part of its tile's 16
+// rows, so every byte is in flight at once and a wave starts computing as
+// soon as its own transfers land. A lane keeps one fp32 term per output and
+// block; a chain through LDS hands the running sum of part kp - 1 to part
+// kp, which adds its terms in block order, so every output is the
+// reference's block-ordered fp32 sum.
+struct ResArgs {
+    int tiles;                // row tiles of the group
+    int acr;                  // codes row stride in LDS, 16-B units (K / 16 + 1)
+    int off_a, off_d, lds;    // LDS offsets of the codes and the scales; LDS bytes
+};
+
+template <class F, int NBK>
+struct ResPart {
+    // row stride in 16-B units: a part's bytes from the 16-B boundary at or
+    // below its start; odd, so the 16 rows start 4 banks apart
+    static constexpr int RU = ((15 + NBK * F::BB + 15) / 16) | 1;
+    static constexpr int NI = (16 * RU + 63) / 64;  // transfers (KB) per wave
+};
+
+template <class F, int TT, int NBK, int RTM>
+__global__ __launch_bounds__(256 * RTM) void res_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
+    using P = ResPart<F, NBK>;
+    constexpr int W = 4 * RTM;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rt = wid % RTM, kp = wid / RTM;
+    const int nl = lane & 15, cl = lane >> 4;
+    const int G = int(gridDim.x);
+    const int t0 = int(blockIdx.x) * ra.tiles / G, nrt = (int(blockIdx.x) + 1) * ra.tiles / G - t0;
+    const int M = grp.t[0].M, K = grp.t[0].K, nb = K / 256;
+    const uint32_t lds0 = lds_addr(lds);
+
+    // codes and scales, dealt out to the waves in turn
+    const int ncode = (M * ra.acr + 63) / 64, nscale = (M * nb + 63) / 64;
+    const v4i32 ra_q = buf_rsrc(x.qs, uint32_t(M) * uint32_t(K));
+    const v4i32 ra_d = buf_rsrc(x.d, uint32_t(M) * uint32_t(nb) * 4u);
+    for (int q = wid; q < ncode + nscale; q += W) {
+        if (q < ncode) {
+            const int g = q * 64 + lane;
+            const int tok = g / ra.acr, u = g - tok * ra.acr;
+            dma16(ra_q, (tok < M && 16 * u < K) ? uint32_t(tok) * uint32_t(K) + 16u * uint32_t(u) : kFar,
+                  lds0 + uint32_t(ra.off_a + q * 1024));
+        } else {
+            const int e = (q - ncode) * 64 + lane;
+            dma4(ra_d, e < M * nb ? 4u * uint32_t(e) : kFar, lds0 + uint32_t(ra.off_d + (q - ncode) * 256));
+        }
+    }
+    // this wave's part of its tile's rows (P::NI transfers by every wave;
+    // rows past N, bytes past the tile and waves without a tile or blocks
+    // read zeros)
+    const int j0 = kp * nb / 4, nbk = (kp + 1) * nb / 4 - j0;
+    const bool live = rt < nrt;
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, t0 + (live ? rt : 0), bx)];
+    const int n0 = bx * 16;
+    const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
+    const uint32_t bl = uint32_t(wstart & 15);
+    const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
+                              (bl + uint32_t(min(16, a.N - n0)) * uint32_t(a.row_bytes) + 15u) & ~15u);
+    uint8_t *ws = lds + wid * (P::NI * 1024);
+    const uint32_t part0 = bl + uint32_t(j0) * uint32_t(F::BB);  // part start in row 0, from the 16-B base
+#pragma unroll
+    for (int i = 0; i < P::NI; ++i) {
+        const int p = i * 64 + lane;
+        const int row = p / P::RU, u = p - row * P::RU;
+        const uint32_t o = ((uint32_t(row) * uint32_t(a.row_bytes) + part0) & ~15u) + 16u * uint32_t(u);
+        dma16(rw, (live && nbk > 0 && row < 16) ? o : kFar, lds_addr(ws) + uint32_t(i * 1024));
+    }
+    wait_vmcnt<P::NI>();              // this wave's codes and scales
+    __builtin_amdgcn_s_barrier();     // everyone's
+    wait_vmcnt<0>();                  // this wave's rows
+    const uint8_t *wrow = ws + nl * (P::RU * 16) + int((uint32_t(nl) * uint32_t(a.row_bytes) + part0) & 15u);
+    const int8_t *acode = reinterpret_cast<const int8_t *>(lds + ra.off_a) + 8 * cl;
+    // scales of the lane's output tokens 16t + 4c + r at block j0
+    const float *dxp[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            dxp[t][r] = reinterpret_cast<const float *>(lds + ra.off_d) + min(16 * t + 4 * cl + r, M - 1) * nb + j0;
+
+    float term[NBK][TT][4];
+    static_for<0, NBK>([&](auto JB) __attribute__((always_inline)) {
+        constexpr int jb = decltype(JB)::value;
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) term[jb][t][r] = 0.0f;
+        if (!live || jb >= nbk) return;
+        const int j = j0 + jb;
+        const typename F::W wv = F::load_lds(wrow + jb * F::BB, cl);
+        Scales<F> sc;
+        decode_scales<F>(wv, sc);
+        [[maybe_unused]] SplitB sb;
+        [[maybe_unused]] uint32_t scw[2], mw[2];
+        if constexpr (F::kSplit) {
+            if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+            else split_b(wv, cl, sb);
+        } else {
+            scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scw, mw);
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            // the lane's A token (tokens past M repeat token M - 1; their
+            // outputs are not kept); chunk h: values 64h + 8c + t, 64h + 32 + 8c + t
+            const int8_t *arow = acode + min(16 * t + nl, M - 1) * (ra.acr * 16) + 256 * j;
+            uint4 av[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint2 lo = ld8(arow + 64 * h), hi = ld8(arow + 64 * h + 32);
+                av[h] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
+            int S[4] = {0, 0, 0, 0};
+            int4v Mb = {0, 0, 0, 0};
+            if constexpr (F::kSplit) {
+                int4v D1 = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    D1 = mfma16x16x64(av[h], sb.b1[h], D1);
+                    D2 = mfma16x16x64(av[h], sb.b2[h], D2);
+                    if constexpr (F::kMin) Mb = mfma16x16x64(av[h], sb.bm[h], Mb);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) S[r] = (D1[r] << F::kShift) + D2[r];
+            } else {
+                // Q4_K / Q5_K: one 16x16x32 MFMA per sub-block, its scale
+                // applied in int32; the mins of sub-blocks 2h, 2h + 1 as
+                // one 16x16x64 MFMA against broadcast bytes
+                int4v D[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint4 &q = av[u >> 1];
+                    const uint2 au = (u & 1) ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y);
+                    D[u] = mfma16x16x32(au, F::bop(wv, u, cl));
+                }
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t m0 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t(2 * h & 3));
+                    const uint32_t m1 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t((2 * h + 1) & 3));
+                    Mb = mfma16x16x64(av[h], make_uint4(m0, m0, m1, m1), Mb);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int su = int(__builtin_amdgcn_ubfe(scw[u >> 2], 8 * (u & 3), 8));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) S[r] += __mul24(su, D[u][r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float dx = dxp[t][r][jb];
+                if constexpr (F::kMin) term[jb][t][r] = dx * (sc.d * (float)S[r] - sc.dmin * (float)Mb[r]);  // E:11026
+                else term[jb][t][r] = (sc.d * dx) * (float)S[r];                                          // E:11101 / E:3405
+            }
+        }
+    });
+
+    // the terms go to this wave's own (spent) weight region as
+    // [block][token tile][r][lane]; after one barrier wave (rt, kp) sums
+    // output r = kp of each token tile of tile rt over the 4 parts' blocks,
+    // in block order
+    static_assert(NBK * TT <= P::NI, "terms fit the wave's region");
+    float *mine = reinterpret_cast<float *>(ws);
+    if (live) {
+#pragma unroll
+        for (int jb = 0; jb < NBK; ++jb)
+#pragma unroll
+            for (int t = 0; t < TT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (jb < nbk) mine[((jb * TT + t) * 4 + r) * 64 + lane] = term[jb][t][r];
+    }
+    lds_barrier();
+    if (live) {
+        const int n = n0 + nl;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            float x4[4][NBK];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float *src = reinterpret_cast<const float *>(lds + (p * RTM + rt) * (P::NI * 1024));
+#pragma unroll
+                for (int jb = 0; jb < NBK; ++jb) x4[p][jb] = src[((jb * TT + t) * 4 + kp) * 64 + lane];
+            }
+            float v = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int nbp = (p + 1) * nb / 4 - p * nb / 4;
+#pragma unroll
+                for (int jb = 0; jb < NBK; ++jb)
+                    if (jb < nbp) v = v + x4[p][jb];
+            }
+            const int tok = 16 * t + 4 * cl + kp;
+            if (tok < M && n < a.N) {
+                if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+                a.y[size_t(tok) * a.ldy + n] = v;
+            }
+        }
+    }
+}
+
+int mfma_cu_count();
+
+// Resident-tile launch if the tiles, codes and scales fit one CU's LDS;
+// returns hipErrorNotSupported (nothing launched) otherwise.
+template <class F, int TT, int NBK, int RTM>
+static hipError_t launch_res_r(const MatArgs *tasks, int n, const Q8KView &x, int tiles, hipStream_t s) {
+    using P = ResPart<F, NBK>;
+    const MatArgs &a = tasks[0];
+    const int nb = a.K / 256;
+    if (nb > 4 * NBK) return hipErrorNotSupported;
+    ResArgs ra{};
+    ra.tiles = tiles;
+    ra.acr = a.K / 16 + 1;
+    ra.off_a = 4 * RTM * P::NI * 1024;
+    ra.off_d = ra.off_a + (a.M * ra.acr + 63) / 64 * 1024;
+    ra.lds = ra.off_d + (a.M * nb + 63) / 64 * 256;
+    const size_t lds = size_t(ra.lds);
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
+    }
+    // at most RTM tiles per workgroup, and one workgroup per CU while the
+    // tiles last
+    const unsigned grid = unsigned(max((tiles + RTM - 1) / RTM, min(tiles, mfma_cu_count())));
+    hipLaunchKernelGGL((res_kernel<F, TT, NBK, RTM>), dim3(grid), dim3(256 * RTM), lds, s, g, x, ra);
+    return hipGetLastError();
+}
+
+template <class F, int TT>
+static hipError_t launch_res(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
+    const int cus = mfma_cu_count();
+    if (tiles <= cus) return launch_res_r<F, TT, 3, 1>(tasks, n, x, tiles, s);
+    if (tiles <= 2 * cus) return launch_res_r<F, TT, 3, 2>(tasks, n, x, tiles, s);
+    return launch_res_r<F, TT, 3, 3>(tasks, n, x, tiles, s);
+}
+
 template <class C, class F>
 static hipError_t launch_tile_t(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     MatGroup g{};
@@ -612,6 +876,13 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // buffer offsets are 32-bit with kFar past every range
     if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
     using G = typename Folded<F>::T;
+    // up to 32 tokens over K <= 3072: the resident-tile kernel
+    if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
+        hipError_t e = hipErrorNotSupported;
+        if (a.M <= 16 && a.K <= 3072) e = launch_res<F, 1>(tasks, n, x, s);
+        else if (a.M <= 32 && a.K <= 3072) e = launch_res<G, 2>(tasks, n, x, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     //                          WR WT PR PT KS TR PD  LDS budget
     if constexpr (kSmallM<F>) {
         // codes resident for K <= 2560 (the hidden size of the workload)
@@ -637,6 +908,17 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
         else  // Q8_0: a fp32 term per 32 values; smaller tiles, 3 workgroups per CU
             return launch_tile_t<TileCfg<F, 1, 2, 4, 1, 1, 16, 2, 52 * 1024>, F>(tasks, n, x, s);
     }
+}
+
+int mfma_cu_count() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        cus[dev] = (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0) ? c : 256;
+    }
+    return cus[dev];
 }
 
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,

@@ -85,6 +85,16 @@ def test_mfma_small_m_long_k(ctx, oracle, type_id, K, M):
     _run(ctx, oracle, type_id, 70, K, M, seed=900 + K + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 6144, 2560, 8), (TYPE_Q6_K, 13000, 1024, 3),
+                                           (TYPE_Q5_K, 300, 3072, 16), (TYPE_Q4_K, 4111, 768, 11),
+                                           (TYPE_Q6_K, 3000, 2560, 7)])
+def test_resident_tile_layouts(ctx, oracle, type_id, N, K, M):
+    """M <= 16, K <= 3072: one workgroup per CU with one, two or three
+    16-row tiles resident (and more workgroups than CUs past three tiles
+    per CU), 12 blocks per row, a partial last tile."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
+
+
 @pytest.mark.parametrize("M", [8, 16, 32, 64])
 def test_tree_verify_q4k(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
