@@ -91,10 +91,18 @@ int qmm_device_info(qmm_context *ctx, int *cu_count, size_t *hbm_bytes, char *ar
 size_t qmm_row_bytes(uint32_t type, int64_t cols);
 /* Bytes of a device Q8_K activation buffer for M rows of K values
  * (BlockQ8K E:868-872 as arrays): qs int8[M][K] at 0, d f32[M][K/256] at
- * qmm_q8k_d_offset, bsum32 i32[M][K/32] at qmm_q8k_bsum_offset. */
+ * qmm_q8k_d_offset, bsum32 i32[M][K/32] at qmm_q8k_bsum_offset, and at
+ * qmm_q8k_tile_offset the codes again in matrix-core operand order (no
+ * counterpart in the reference; read by the M >= 2 kernels): for token tile
+ * t (tokens 16t..16t+15), block j and 64-value chunk h, 1 KB at
+ * ((t * K/256 + j) * 4 + h) * 1024 whose 16-B slot 16c + n holds token
+ * 16t + n's codes at block offsets 64h + 8c..+7 then 64h + 32 + 8c..+7.
+ * Every producer (qmm_quantize_q8k, qmm_swiglu_q8k, qmm_rmsnorm_q8k)
+ * writes all four sections. */
 size_t qmm_q8k_bytes(int M, int K);
 size_t qmm_q8k_d_offset(int M, int K);
 size_t qmm_q8k_bsum_offset(int M, int K);
+size_t qmm_q8k_tile_offset(int M, int K);
 /* Q8_0 activations (BlockQ8_0_Fast E:874-877): qs int8[M][K] at 0,
  * d f32[M][K/32] at qmm_q8_0_d_offset. */
 size_t qmm_q8_0_bytes(int M, int K);

@@ -188,13 +188,13 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
 // x32 != nullptr (M = 1 only): the GEMV kernels quantize x themselves.
 int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q80, int M, int K,
               const qmm_matrix_task *tasks, int n_tasks) {
-    qmm::Q8KView xk{nullptr, nullptr, nullptr};
+    qmm::Q8KView xk{nullptr, nullptr, nullptr, nullptr};
     qmm::Q80View x0{nullptr, nullptr};
     if (q8k) {
         const qmm::Q8KLayout L(M, K);
         const uint8_t *b = static_cast<const uint8_t *>(q8k);
         xk = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off),
-              reinterpret_cast<const int32_t *>(b + L.bs_off)};
+              reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off)};
     }
     if (q80) {
         const qmm::Q80Layout L(M, K);
@@ -266,6 +266,7 @@ size_t qmm_row_bytes(uint32_t type, int64_t cols) {
 size_t qmm_q8k_bytes(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).total : 0; }
 size_t qmm_q8k_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).d_off : 0; }
 size_t qmm_q8k_bsum_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).bs_off : 0; }
+size_t qmm_q8k_tile_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).tile_off : 0; }
 size_t qmm_q8_0_bytes(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).total : 0; }
 size_t qmm_q8_0_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).d_off : 0; }
 

@@ -18,16 +18,29 @@ constexpr uint32_t kQ6_K = 14;
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Q8_K activation buffer layout (all sections 256-B aligned):
-//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32]
+//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32] | tiles
+// tiles: the codes again, in the order of an MFMA operand: for token tile t
+// (tokens 16t .. 16t + 15), 256-value block j and 64-value chunk h, 1 KB at
+// ((t * K/256 + j) * 4 + h) * 1024 whose 16-B slot 16c + n (c < 4, n < 16)
+// holds token 16t + n's codes at block offsets 64h + 8c .. +7, then
+// 64h + 32 + 8c .. +7 (slots of tokens past M are not written).
 struct Q8KLayout {
-    size_t d_off, bs_off, total;
+    size_t d_off, bs_off, tile_off, total;
     __host__ __device__ Q8KLayout(int M, int K) {
         const size_t mk = size_t(M) * size_t(K);
         d_off = align256(mk);
         bs_off = align256(d_off + 4 * size_t(M) * size_t(K / 256));
-        total = align256(bs_off + 4 * size_t(M) * size_t(K / 32));
+        tile_off = align256(bs_off + 4 * size_t(M) * size_t(K / 32));
+        total = align256(tile_off + size_t((M + 15) / 16) * 16 * size_t(K));
     }
 };
+// byte offset in the tiles section of the 4 codes of token m at values
+// 4i .. 4i + 3 of block j (nb blocks per row)
+__host__ __device__ inline size_t q8k_tile_pos(int m, int j, int i, int nb) {
+    const int h = i >> 4, kk = 4 * (i & 15);
+    const int c = (kk & 31) >> 3, byte = (kk & 7) + ((kk & 32) >> 2);
+    return ((size_t(m >> 4) * size_t(nb) + size_t(j)) * 4 + size_t(h)) * 1024 + size_t(16 * (16 * c + (m & 15)) + byte);
+}
 // Q8_0 activation buffer layout: qs int8[M][K] | d f32[M][K/32]
 struct Q80Layout {
     size_t d_off, total;
@@ -42,6 +55,7 @@ struct Q8KView {
     const int8_t *qs;   // [M][K]
     const float *d;     // [M][K/256]
     const int32_t *bs;  // [M][K/32]
+    const int8_t *qt;   // the tiles section
 };
 struct Q80View {
     const int8_t *qs;  // [M][K]

@@ -12,13 +12,16 @@ namespace qmm {
 
 // Quantize one fp16-rounded 256-value block held 4 values per lane and
 // store it as Q8_K block `blk` (flattened over [M][K/256]).
+// The codes also go to the tiles section qt (nb blocks per row).
 __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
-                                       size_t blk, int8_t *qs, float *d, int32_t *bs) {
+                                       size_t blk, int8_t *qs, float *d, int32_t *bs, int8_t *qt, int nb) {
     float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
     a = wave_max(a);  // E:941-946
     int sum;
     const uint32_t packed = quant4(h0, h1, h2, h3, a, sum);
     reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
+    const int m = int(blk / size_t(nb)), j = int(blk - size_t(m) * size_t(nb));
+    *reinterpret_cast<uint32_t *>(qt + q8k_tile_pos(m, j, lane, nb)) = packed;
     sum = group8_sum(sum);  // bsum32 over 32 values = 8 lanes
     if ((lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
     if (lane == 0) d[blk] = q8_scale(a);  // E:953
@@ -28,13 +31,14 @@ __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, i
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x,
                                                            size_t nblk, int8_t *__restrict__ qs,
                                                            float *__restrict__ d,
-                                                           int32_t *__restrict__ bs) {
+                                                           int32_t *__restrict__ bs,
+                                                           int8_t *__restrict__ qt, int nb) {
     const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (blk >= nblk) return;
     const int lane = threadIdx.x & 63;
     const float4 v = reinterpret_cast<const float4 *>(x + blk * 256)[lane];
     store_q8k_block(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z),
-                    round_to_fp16(v.w), lane, blk, qs, d, bs);
+                    round_to_fp16(v.w), lane, blk, qs, d, bs, qt, nb);
 }
 
 // Q8_0: 32-value blocks, 8 lanes each, 8 blocks per wave (flattened).
@@ -65,7 +69,8 @@ __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict
                                                          size_t nblk, float *__restrict__ h,
                                                          int8_t *__restrict__ qs,
                                                          float *__restrict__ d,
-                                                         int32_t *__restrict__ bs) {
+                                                         int32_t *__restrict__ bs,
+                                                         int8_t *__restrict__ qt, int nb) {
     const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (blk >= nblk) return;
     const int lane = threadIdx.x & 63;
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict
     r.w = (g.w / (1.0f + expf(-g.w))) * u.w;
     if (h) reinterpret_cast<float4 *>(h + blk * 256)[lane] = r;
     store_q8k_block(round_to_fp16(r.x), round_to_fp16(r.y), round_to_fp16(r.z),
-                    round_to_fp16(r.w), lane, blk, qs, d, bs);
+                    round_to_fp16(r.w), lane, blk, qs, d, bs, qt, nb);
 }
 
 // rmsnorm_fp16_rows_fast (E:4264-4314) + its Q8_K (E:4303-4305): one
@@ -93,7 +98,8 @@ __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restric
                                                           const float *__restrict__ gamma, int K,
                                                           float *__restrict__ y, int8_t *__restrict__ qs,
                                                           float *__restrict__ d,
-                                                          int32_t *__restrict__ bs) {
+                                                          int32_t *__restrict__ bs,
+                                                          int8_t *__restrict__ qt) {
     __shared__ float part[4];
     const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
     const size_t m = blockIdx.x;
@@ -130,7 +136,7 @@ __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restric
         r.z = round_to_fp16(h[j].z * inv_rms * round_to_fp16(g.z));
         r.w = round_to_fp16(h[j].w * inv_rms * round_to_fp16(g.w));
         if (y) reinterpret_cast<float4 *>(y + m * size_t(K))[q] = r;
-        store_q8k_block(r.x, r.y, r.z, r.w, lane, m * nbk + size_t(4 * j + wid), qs, d, bs);
+        store_q8k_block(r.x, r.y, r.z, r.w, lane, m * nbk + size_t(4 * j + wid), qs, d, bs, qt, int(nbk));
     }
 }
 
@@ -206,7 +212,8 @@ hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStrea
     const unsigned grid = unsigned((nblk + 3) / 4);
     hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk,
                        reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
-                       reinterpret_cast<int32_t *>(base + L.bs_off));
+                       reinterpret_cast<int32_t *>(base + L.bs_off), reinterpret_cast<int8_t *>(base + L.tile_off),
+                       K / 256);
     return hipGetLastError();
 }
 
@@ -229,7 +236,8 @@ hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, f
     const unsigned grid = unsigned((nblk + 3) / 4);
     hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(grid), dim3(256), 0, s, gate, up, nblk, h,
                        reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
-                       reinterpret_cast<int32_t *>(base + L.bs_off));
+                       reinterpret_cast<int32_t *>(base + L.bs_off), reinterpret_cast<int8_t *>(base + L.tile_off),
+                       N / 256);
     return hipGetLastError();
 }
 
@@ -240,9 +248,10 @@ hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, 
     int8_t *qs = reinterpret_cast<int8_t *>(base);
     float *d = reinterpret_cast<float *>(base + L.d_off);
     int32_t *bs = reinterpret_cast<int32_t *>(base + L.bs_off);
+    int8_t *qt = reinterpret_cast<int8_t *>(base + L.tile_off);
     const int nj = (K / 4 + 255) / 256;  // float4s per thread
 #define QMM_RMS(NJ) \
-    hipLaunchKernelGGL(rmsnorm_q8k_kernel<NJ>, dim3(unsigned(M)), dim3(256), 0, s, x, gamma, K, y, qs, d, bs)
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel<NJ>, dim3(unsigned(M)), dim3(256), 0, s, x, gamma, K, y, qs, d, bs, qt)
     if (nj <= 3) QMM_RMS(3);
     else if (nj <= 4) QMM_RMS(4);
     else if (nj <= 10) QMM_RMS(10);

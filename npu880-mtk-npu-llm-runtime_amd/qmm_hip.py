@@ -66,6 +66,7 @@ _SIGNATURES = [
     ("qmm_q8k_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_d_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_bsum_offset", C.c_size_t, [C.c_int, C.c_int]),
+    ("qmm_q8k_tile_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_d_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_malloc", C.c_int, [_p, C.c_size_t, C.POINTER(_p)]),
@@ -123,6 +124,25 @@ def load_library(path: str = LIB_PATH):
 def row_bytes(type_id: int, cols: int) -> int:
     """ggml_row_bytes (E:3940-3942), computed by the library."""
     return int(load_library().qmm_row_bytes(type_id, cols))
+
+
+def q8k_tile(qs: np.ndarray) -> np.ndarray:
+    """Codes [M][K] -> the tiles section of a Q8_K buffer (flat int8): for
+    token tile t, block j and 64-value chunk h, 1 KB whose 16-B slot 16c + n
+    holds token 16t + n's codes at block offsets 64h + 8c..+7, then
+    64h + 32 + 8c..+7 (slots of tokens past M are zero here)."""
+    M, K = qs.shape
+    T, nb = (M + 15) // 16, K // 256
+    p = np.zeros((T * 16, K), np.int8)
+    p[:M] = qs
+    # axes (t, n, j, h, half, c, byte) -> (t, j, h, c, n, half, byte)
+    return np.ascontiguousarray(p.reshape(T, 16, nb, 4, 2, 4, 8).transpose(0, 2, 3, 5, 1, 4, 6)).reshape(-1)
+
+
+def q8k_untile(t: np.ndarray, M: int, K: int) -> np.ndarray:
+    """Inverse of q8k_tile: the first M tokens' codes in [M][K] order."""
+    T, nb = (M + 15) // 16, K // 256
+    return np.ascontiguousarray(t.reshape(T, nb, 4, 4, 16, 2, 8).transpose(0, 4, 1, 2, 5, 3, 6)).reshape(T * 16, K)[:M]
 
 
 def q8k_bytes(M: int, K: int) -> int:
@@ -422,12 +442,19 @@ class Context:
         bs = self.d2h(buf, np.int32, (M, K // 32), offset=int(lib.qmm_q8k_bsum_offset(M, K)))
         return d, qs, bs
 
+    def read_q8k_tiles(self, buf, M: int, K: int) -> np.ndarray:
+        """The tiles section of a device Q8_K buffer, put back in [M][K] order."""
+        T = (M + 15) // 16
+        t = self.d2h(buf, np.int8, (T * 16 * K,), offset=int(self.lib.qmm_q8k_tile_offset(M, K)))
+        return q8k_untile(t, M, K)
+
     def write_q8k(self, buf, d, qs, bs):
         M, K = qs.shape
         lib = self.lib
         self.h2d(buf, np.ascontiguousarray(qs, np.int8))
         self.h2d(buf, np.ascontiguousarray(d, np.float32), offset=int(lib.qmm_q8k_d_offset(M, K)))
         self.h2d(buf, np.ascontiguousarray(bs, np.int32), offset=int(lib.qmm_q8k_bsum_offset(M, K)))
+        self.h2d(buf, q8k_tile(qs), offset=int(lib.qmm_q8k_tile_offset(M, K)))
 
     def read_q8_0(self, buf, M: int, K: int):
         qs = self.d2h(buf, np.int8, (M, K))

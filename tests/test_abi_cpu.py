@@ -4,6 +4,7 @@ need no device. No kernels run here."""
 import ctypes as C
 import re
 
+import numpy as np
 import pytest
 
 import qmm_hip
@@ -46,9 +47,32 @@ def test_row_bytes_and_layout_sizes():
     d_off, bs_off, total = lib.qmm_q8k_d_offset(M, K), lib.qmm_q8k_bsum_offset(M, K), lib.qmm_q8k_bytes(M, K)
     assert d_off >= M * K and d_off % 256 == 0
     assert bs_off >= d_off + 4 * M * K // 256 and bs_off % 256 == 0
-    assert total >= bs_off + 4 * M * K // 32
+    tile_off = lib.qmm_q8k_tile_offset(M, K)
+    assert tile_off >= bs_off + 4 * M * K // 32 and tile_off % 256 == 0
+    assert total >= tile_off + 16 * K  # one 16-token tile for M = 3
     assert lib.qmm_q8_0_d_offset(M, K) >= M * K and lib.qmm_q8_0_bytes(M, K) >= M * K + 4 * M * K // 32
     assert lib.qmm_q8k_bytes(0, K) == 0
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (16, 512), (37, 768)])
+def test_q8k_tiles_order(M, K):
+    """The tiles section's order, from its definition: slot 16c + n of chunk
+    h of block j of token tile t holds token 16t + n's codes at block
+    offsets 64h + 8c .. +7, then 64h + 32 + 8c .. +7."""
+    rng = np.random.default_rng(M + K)
+    qs = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    t = qmm_hip.q8k_tile(qs)
+    assert t.size == (M + 15) // 16 * 16 * K
+    assert np.array_equal(qmm_hip.q8k_untile(t, M, K), qs)
+    nb = K // 256
+    for m in range(M):
+        for j in range(nb):
+            for h in range(4):
+                for c in range(4):
+                    slot = t[(((m // 16) * nb + j) * 4 + h) * 1024 + 16 * (16 * c + m % 16):][:16]
+                    base = 256 * j + 64 * h + 8 * c
+                    assert np.array_equal(slot[:8], qs[m, base:base + 8])
+                    assert np.array_equal(slot[8:], qs[m, base + 32:base + 40])
 
 
 def test_status_strings_and_null_context():

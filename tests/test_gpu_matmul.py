@@ -141,8 +141,9 @@ def test_mfma_extreme_scales(ctx, oracle, type_id, M):
 
 
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K])
-def test_mfma_residual(ctx, oracle, type_id):
-    _run(ctx, oracle, type_id, 200, 2560, 9, seed=7, residual=True)
+@pytest.mark.parametrize("M", [9, 33])
+def test_mfma_residual(ctx, oracle, type_id, M):
+    _run(ctx, oracle, type_id, 200, 2560, M, seed=7 + M, residual=True)
 
 
 @pytest.mark.parametrize("name", ["qkv", "o", "gate", "down", "q8_0"])
@@ -242,7 +243,7 @@ def test_task_groups_large(ctx, oracle, type_id, specs):
         ctx.free(b)
 
 
-@pytest.mark.parametrize("M", [1, 6, 70])
+@pytest.mark.parametrize("M", [1, 6, 40, 70])
 def test_task_groups_one_launch(ctx, oracle, M):
     """Many tasks of one type (more than one launch's group of 8), tiny-N tasks
     and residuals interleaved with another type: the E:7954-7959 /

@@ -18,7 +18,7 @@ def _inputs(M, K, seed):
     return x.astype(np.float32)
 
 
-@pytest.mark.parametrize("M,K", [(1, 256), (3, 2560), (5, 9728), (64, 2560)])
+@pytest.mark.parametrize("M,K", [(1, 256), (3, 2560), (5, 9728), (37, 768), (64, 2560)])
 def test_quantize_q8k_bit_exact(ctx, oracle, M, K):
     say(f"quantize_q8k M={M} K={K}")
     x = _inputs(M, K, seed=M * 31 + K)
@@ -31,6 +31,8 @@ def test_quantize_q8k_bit_exact(ctx, oracle, M, K):
     assert np.array_equal(d.view(np.uint32), ed.view(np.uint32))
     assert np.array_equal(qs, eqs)
     assert np.array_equal(bs, ebs)
+    # the tiles section: the same codes in matrix-core operand order
+    assert np.array_equal(ctx.read_q8k_tiles(out, M, K), qs)
     ctx.free(xb)
     ctx.free(out)
 
@@ -70,6 +72,7 @@ def test_swiglu_requant(ctx, oracle):
     ed, eqs, ebs = oracle.quantize_q8k(h)
     assert np.array_equal(d.view(np.uint32), ed.view(np.uint32))
     assert np.array_equal(qs, eqs) and np.array_equal(bs, ebs)
+    assert np.array_equal(ctx.read_q8k_tiles(out, M, N), qs)
     for b in (gb, ub, hb, out):
         ctx.free(b)
 

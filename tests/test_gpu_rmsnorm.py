@@ -35,6 +35,7 @@ def test_rmsnorm_q8k(ctx, oracle, M, K):
     ed, eqs, ebs = oracle.quantize_q8k(y)
     assert np.array_equal(d.view(np.uint32), ed.view(np.uint32))
     assert np.array_equal(qs, eqs) and np.array_equal(bs, ebs)
+    assert np.array_equal(ctx.read_q8k_tiles(q, M, K), qs)
     # and equal to the oracle's own codes in every block where y agrees
     same = (y == ry).reshape(M, K // 256, 256).all(axis=2)
     assert np.array_equal(qs.reshape(M, -1, 256)[same], rqs.reshape(M, -1, 256)[same])
