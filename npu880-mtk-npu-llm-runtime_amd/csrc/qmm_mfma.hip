@@ -1068,16 +1068,24 @@ static hipError_t launch_part_r(const MatArgs *tasks, int n, const Q8KView &x, i
     return hipGetLastError();
 }
 
-// One tile per CU only: with a single wave per SIMD the matrix and vector
-// work of a wave do not overlap, and two or three tiles per CU in sequence
-// measured slower than the chunked tile kernel (Q4_K 9728 x 2560, M = 64:
-// 21.9 against 17.6 us).
+// One tile per workgroup. Up to 32 tokens a workgroup needs few enough
+// registers for three per CU, so any number of tiles runs as one wave of
+// workgroups; past 32 tokens only one fits a CU, and the tiles must not
+// outnumber the CUs (several tiles per workgroup in sequence, one wave per
+// SIMD, measured slower than the chunked tile kernel: Q4_K 9728 x 2560,
+// M = 64, 21.9 against 17.6 us).
 template <class F, int TT>
 static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
     int tiles = 0;
     for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
-    if (tiles > mfma_cu_count()) return hipErrorNotSupported;
+    if (TT > 2 && tiles > mfma_cu_count()) return hipErrorNotSupported;
     return launch_part_r<F, TT, 3, 1>(tasks, n, x, tiles, s);
+}
+
+static int group_tiles(const MatArgs *tasks, int n) {
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
+    return tiles;
 }
 
 template <class F, int TT>
@@ -1113,10 +1121,20 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // up to 32 tokens over K <= 3072: the resident-tile kernel
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
-        if (a.M <= 16 && a.K <= 3072) e = launch_res<F, 1>(tasks, n, x, s);
-        else if (a.M <= 32 && a.K <= 3072) e = launch_part<G, 2>(tasks, n, x, s);
-        else if (a.M <= 48 && a.K <= 3072) e = launch_part<G, 3>(tasks, n, x, s);
-        else if (a.M <= 64 && a.K <= 3072) e = launch_part<G, 4>(tasks, n, x, s);
+        if (a.K <= 3072) {
+            if (a.M <= 16) {
+                // several resident tiles per CU where the tiles outnumber
+                // the CUs (measured faster there), else one per workgroup
+                if (group_tiles(tasks, n) > mfma_cu_count()) e = launch_res<F, 1>(tasks, n, x, s);
+                if (e == hipErrorNotSupported) e = launch_part<F, 1>(tasks, n, x, s);
+            } else if (a.M <= 32) {
+                e = launch_part<G, 2>(tasks, n, x, s);
+            } else if (a.M <= 48) {
+                e = launch_part<G, 3>(tasks, n, x, s);
+            } else if (a.M <= 64) {
+                e = launch_part<G, 4>(tasks, n, x, s);
+            }
+        }
         if (e != hipErrorNotSupported) return e;
     }
     //                          WR WT PR PT KS TR PD  LDS budget
