@@ -620,7 +620,8 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
 struct ResArgs {
     int tiles;                // row tiles of the group
     int acr;                  // codes row stride in LDS, 16-B units (K / 16 + 1)
-    int off_a, off_d, lds;    // LDS offsets of the codes and the scales; LDS bytes
+    int off_a, off_d, off_t;  // LDS offsets of the codes, the scales, the terms
+    int lds;                  // LDS bytes
 };
 
 template <class F, int NBK>
@@ -814,54 +815,53 @@ __global__ __launch_bounds__(256 * RTM) void res_kernel(MatGroup grp, Q8KView x,
     }
 }
 
-// ============================================ resident tiles, codes in registers
-// Up to 16 * TT tokens (TT <= 4) of a k-quant over K <= NBK * 4 * 256: one
-// workgroup per CU owns RT <= RTM consecutive 16-row tiles, as above, but
-// with one wave per K part for all of them: wave kp loads the codes of its
-// blocks for every token straight into registers from the tiles section
-// of the Q8_K buffer (1 KB per wave load, once per CU), moves its part of
-// every tile into LDS, and computes tile after tile as each part lands.
-// Per tile the 4 parts' fp32 terms meet in a chain through LDS (part kp
-// adds its terms, in block order, to the sum of parts 0..kp-1), so every
-// output is the reference's block-ordered fp32 sum; each block's weights
-// are decoded once for all tokens.
-template <class F, int TT, int NBK, int RTM>
-__global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
+// ============================================== one tile, codes in registers
+// Up to 16 * TT tokens (TT <= 4) of a k-quant over K <= NBK * 4 * 256: a
+// workgroup owns one 16-row tile and every token, one wave per K part.
+// Wave kp moves its part of the 16 rows into LDS, the token scales arrive
+// in LDS (then transposed to [block][token]), and the part's codes for
+// every token load straight into registers from the tiles section of the
+// Q8_K buffer (1 KB per wave load); each block's weights are decoded once
+// for all tokens. The fp32 terms of the 4 parts then meet in LDS, and each
+// wave sums a quarter of the outputs over all blocks in block order, so
+// every output is the reference's block-ordered fp32 sum.
+template <class F, int TT, int NBK>
+struct PartCfg {
     using P = ResPart<F, NBK>;
+    // terms of a wave, [block][token tile][r][lane] floats: in its own
+    // (spent) part region when they fit, else in a region of their own
+    static constexpr bool kOwn = NBK * TT <= P::NI;
+    static constexpr int TERMS = kOwn ? 0 : 4 * NBK * TT * 1024;
+};
+
+template <class F, int TT, int NBK>
+__global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
+    using C = PartCfg<F, TT, NBK>;
+    using P = typename C::P;
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, cl = lane >> 4;
-    const int G = int(gridDim.x);
-    const int t0 = int(blockIdx.x) * ra.tiles / G, nrt = (int(blockIdx.x) + 1) * ra.tiles / G - t0;
-    const int M = grp.t[0].M, K = grp.t[0].K, nb = K / 256;
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    const int n0 = bx * 16, M = a.M, K = a.K, nb = K / 256;
     const int j0 = kp * nb / 4, nbk = (kp + 1) * nb / 4 - j0;
     const uint32_t lds0 = lds_addr(lds);
 
-    // this wave's part of each tile (P::NI transfers per tile slot; slots
-    // past the workgroup's tiles read zeros), then the block scales of all
-    // tokens (dealt out to the waves), then the codes
-    const MatArgs *ta[RTM];
-    int n0r[RTM];
-    uint32_t part0r[RTM];
+    // this wave's part of the tile's rows (rows past N and bytes past the
+    // tile read zeros), then the token scales (dealt out to the waves)
+    const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
+    const uint32_t bl = uint32_t(wstart & 15);
+    const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
+                              (bl + uint32_t(min(16, a.N - n0)) * uint32_t(a.row_bytes) + 15u) & ~15u);
+    const uint32_t part0 = bl + uint32_t(j0) * uint32_t(F::BB);  // part start in row 0, from the 16-B base
+    uint8_t *ws = lds + kp * (P::NI * 1024);
 #pragma unroll
-    for (int r = 0; r < RTM; ++r) {
-        int bx = 0;
-        ta[r] = &grp.t[group_task(grp, t0 + min(r, nrt - 1), bx)];
-        n0r[r] = bx * 16;
-        const uintptr_t wstart = reinterpret_cast<uintptr_t>(ta[r]->w) + size_t(n0r[r]) * ta[r]->row_bytes;
-        const uint32_t bl = uint32_t(wstart & 15);
-        const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
-                                  (bl + uint32_t(min(16, ta[r]->N - n0r[r])) * uint32_t(ta[r]->row_bytes) + 15u) & ~15u);
-        part0r[r] = bl + uint32_t(j0) * uint32_t(F::BB);
-        const uint32_t wl = lds0 + uint32_t((r * 4 + kp) * P::NI * 1024);
-#pragma unroll
-        for (int i = 0; i < P::NI; ++i) {
-            const int p = i * 64 + lane;
-            const int row = p / P::RU, u = p - row * P::RU;
-            const uint32_t o = ((uint32_t(row) * uint32_t(ta[r]->row_bytes) + part0r[r]) & ~15u) + 16u * uint32_t(u);
-            dma16(rw, (r < nrt && nbk > 0 && row < 16) ? o : kFar, wl + uint32_t(i * 1024));
-        }
+    for (int i = 0; i < P::NI; ++i) {
+        const int p = i * 64 + lane;
+        const int row = p / P::RU, u = p - row * P::RU;
+        const uint32_t o = ((uint32_t(row) * uint32_t(a.row_bytes) + part0) & ~15u) + 16u * uint32_t(u);
+        dma16(rw, (nbk > 0 && row < 16) ? o : kFar, lds_addr(ws) + uint32_t(i * 1024));
     }
     const int nscale = (M * nb + 63) / 64;
     const v4i32 ra_d = buf_rsrc(x.d, uint32_t(M) * uint32_t(nb) * 4u);
@@ -895,121 +895,116 @@ __global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResA
         dxt[e] = reinterpret_cast<const float *>(lds + ra.off_d)[min(tok, M - 1) * nb + j];
     }
     lds_barrier();
-    float4 *slot = reinterpret_cast<float4 *>(lds + ra.lds - 2 * TT * 1024) + lane;
 
-    static_for<0, RTM>([&](auto R) __attribute__((always_inline)) {
-        constexpr int r = decltype(R)::value;
-        const MatArgs &a = *ta[r];
-        const uint8_t *wrow = lds + (r * 4 + kp) * (P::NI * 1024) + nl * (P::RU * 16) +
-                              int((uint32_t(nl) * uint32_t(a.row_bytes) + part0r[r]) & 15u);
-        float term[NBK][TT][4];
+    const uint8_t *wrow = ws + nl * (P::RU * 16) + int((uint32_t(nl) * uint32_t(a.row_bytes) + part0) & 15u);
+    float term[NBK][TT][4];
 #pragma unroll
-        for (int jb = 0; jb < NBK; ++jb) {
+    for (int jb = 0; jb < NBK; ++jb) {
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
+        for (int t = 0; t < TT; ++t)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) term[jb][t][q] = 0.0f;
-            if (r >= nrt || jb >= nbk) continue;
-            const int j = j0 + jb;
-            const typename F::W wv = F::load_lds(wrow + jb * F::BB, cl);
-            Scales<F> sc;
-            decode_scales<F>(wv, sc);
-            [[maybe_unused]] SplitB sb;
-            [[maybe_unused]] uint32_t scw[2], mw[2];
+            for (int q = 0; q < 4; ++q) term[jb][t][q] = 0.0f;
+        if (jb >= nbk) continue;
+        const int j = j0 + jb;
+        const typename F::W wv = F::load_lds(wrow + jb * F::BB, cl);
+        Scales<F> sc;
+        decode_scales<F>(wv, sc);
+        [[maybe_unused]] SplitB sb;
+        [[maybe_unused]] uint32_t scw[2], mw[2];
+        if constexpr (F::kSplit) {
+            if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+            else split_b(wv, cl, sb);
+        } else {
+            scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scw, mw);
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            int S[4] = {0, 0, 0, 0};
+            int4v Mb = {0, 0, 0, 0};
             if constexpr (F::kSplit) {
-                if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
-                else split_b(wv, cl, sb);
+                int4v D1 = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    D1 = mfma16x16x64(av[jb][t][h], sb.b1[h], D1);
+                    D2 = mfma16x16x64(av[jb][t][h], sb.b2[h], D2);
+                    if constexpr (F::kMin) Mb = mfma16x16x64(av[jb][t][h], sb.bm[h], Mb);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) S[q] = (D1[q] << F::kShift) + D2[q];
             } else {
-                scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scw, mw);
-            }
+                // Q4_K / Q5_K: one 16x16x32 MFMA per sub-block, its scale
+                // applied in int32; the mins of sub-blocks 2h, 2h + 1 as
+                // one 16x16x64 MFMA against broadcast bytes
+                int4v D[8];
 #pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                int S[4] = {0, 0, 0, 0};
-                int4v Mb = {0, 0, 0, 0};
-                if constexpr (F::kSplit) {
-                    int4v D1 = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
-#pragma unroll
-                    for (int h = 0; h < 4; ++h) {
-                        D1 = mfma16x16x64(av[jb][t][h], sb.b1[h], D1);
-                        D2 = mfma16x16x64(av[jb][t][h], sb.b2[h], D2);
-                        if constexpr (F::kMin) Mb = mfma16x16x64(av[jb][t][h], sb.bm[h], Mb);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) S[q] = (D1[q] << F::kShift) + D2[q];
-                } else {
-                    int4v D[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const uint4 &qv = av[jb][t][u >> 1];
-                        const uint2 au = (u & 1) ? make_uint2(qv.z, qv.w) : make_uint2(qv.x, qv.y);
-                        D[u] = mfma16x16x32(au, F::bop(wv, u, cl));
-                    }
-#pragma unroll
-                    for (int h = 0; h < 4; ++h) {
-                        const uint32_t m0 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t(2 * h & 3));
-                        const uint32_t m1 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t((2 * h + 1) & 3));
-                        Mb = mfma16x16x64(av[jb][t][h], make_uint4(m0, m0, m1, m1), Mb);
-                    }
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const int su = int(__builtin_amdgcn_ubfe(scw[u >> 2], 8 * (u & 3), 8));
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) S[q] += __mul24(su, D[u][q]);
-                    }
+                for (int u = 0; u < 8; ++u) {
+                    const uint4 &qv = av[jb][t][u >> 1];
+                    const uint2 au = (u & 1) ? make_uint2(qv.z, qv.w) : make_uint2(qv.x, qv.y);
+                    D[u] = mfma16x16x32(au, F::bop(wv, u, cl));
                 }
-                const float4 dx4 = *reinterpret_cast<const float4 *>(dxt + j * 64 + 16 * t + 4 * cl);
-                const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float dx = dxr[q];
-                    if constexpr (F::kMin) term[jb][t][q] = dx * (sc.d * (float)S[q] - sc.dmin * (float)Mb[q]);  // E:11026
-                    else term[jb][t][q] = (sc.d * dx) * (float)S[q];                                          // E:11101 / E:3405
+                for (int h = 0; h < 4; ++h) {
+                    const uint32_t m0 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t(2 * h & 3));
+                    const uint32_t m1 = __builtin_amdgcn_perm(0u, mw[h >> 1], 0x01010101u * uint32_t((2 * h + 1) & 3));
+                    Mb = mfma16x16x64(av[jb][t][h], make_uint4(m0, m0, m1, m1), Mb);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int su = int(__builtin_amdgcn_ubfe(scw[u >> 2], 8 * (u & 3), 8));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) S[q] += __mul24(su, D[u][q]);
                 }
             }
-        }
-        // the chain over the 4 parts of tile r (two slots of TT KB, used
-        // alternately); part 3 stores the outputs
-        float v[TT][4];
-        for (int p = 0; p < 4; ++p) {
-            if (kp == p) {
+            const float4 dx4 = *reinterpret_cast<const float4 *>(dxt + j * 64 + 16 * t + 4 * cl);
+            const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
-                for (int t = 0; t < TT; ++t) {
-                    float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    if (p > 0) s0 = slot[((p - 1) & 1) * TT * 64 + t * 64];
-                    v[t][0] = s0.x; v[t][1] = s0.y; v[t][2] = s0.z; v[t][3] = s0.w;
-#pragma unroll
-                    for (int jb = 0; jb < NBK; ++jb)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (jb < nbk) v[t][q] = v[t][q] + term[jb][t][q];
-                    if (p < 3) slot[(p & 1) * TT * 64 + t * 64] = make_float4(v[t][0], v[t][1], v[t][2], v[t][3]);
-                }
-            }
-            if (p < 3) lds_barrier();
-        }
-        if (kp == 3 && r < nrt) {
-            const int n = n0r[r] + nl;
-            if (n < a.N) {
-#pragma unroll
-                for (int t = 0; t < TT; ++t)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int tok = 16 * t + 4 * cl + q;
-                        if (tok >= M) continue;
-                        float y = v[t][q];
-                        if (a.res) y = y + a.res[size_t(tok) * a.ldr + n];
-                        a.y[size_t(tok) * a.ldy + n] = y;
-                    }
+            for (int q = 0; q < 4; ++q) {
+                const float dx = dxr[q];
+                if constexpr (F::kMin) term[jb][t][q] = dx * (sc.d * (float)S[q] - sc.dmin * (float)Mb[q]);  // E:11026
+                else term[jb][t][q] = (sc.d * dx) * (float)S[q];                                          // E:11101 / E:3405
             }
         }
-        // the next tile's chain reuses the slots: part 0 writes only after
-        // part 3 has read (the barrier between tiles)
-        lds_barrier();
-    });
-}
+    }
 
-template <class F, int TT, int NBK, int RTM>
-static hipError_t launch_part_r(const MatArgs *tasks, int n, const Q8KView &x, int tiles, hipStream_t s);
+    // the terms meet in LDS; wave kp then sums output r = kp of each token
+    // tile over the 4 parts' blocks, in block order
+    auto terms_of = [&](int p) __attribute__((always_inline)) {
+        return reinterpret_cast<float *>(C::kOwn ? lds + p * (P::NI * 1024) : lds + ra.off_t + p * (NBK * TT * 1024));
+    };
+    float *mine = terms_of(kp);
+#pragma unroll
+    for (int jb = 0; jb < NBK; ++jb)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (jb < nbk) mine[((jb * TT + t) * 4 + q) * 64 + lane] = term[jb][t][q];
+    lds_barrier();
+    const int n = n0 + nl;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        float xs[4][NBK];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float *src = terms_of(p);
+#pragma unroll
+            for (int jb = 0; jb < NBK; ++jb) xs[p][jb] = src[((jb * TT + t) * 4 + kp) * 64 + lane];
+        }
+        float v = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int nbp = (p + 1) * nb / 4 - p * nb / 4;
+#pragma unroll
+            for (int jb = 0; jb < NBK; ++jb)
+                if (jb < nbp) v = v + xs[p][jb];
+        }
+        const int tok = 16 * t + 4 * cl + kp;
+        if (tok < M && n < a.N) {
+            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+            a.y[size_t(tok) * a.ldy + n] = v;
+        }
+    }
+}
 
 int mfma_cu_count();
 
@@ -1043,18 +1038,29 @@ static hipError_t launch_res_r(const MatArgs *tasks, int n, const Q8KView &x, in
     return hipGetLastError();
 }
 
-// Part-kernel launch if the parts, scales and chain slots fit one CU's LDS;
-// returns hipErrorNotSupported (nothing launched) otherwise.
-template <class F, int TT, int NBK, int RTM>
-static hipError_t launch_part_r(const MatArgs *tasks, int n, const Q8KView &x, int tiles, hipStream_t s) {
-    using P = ResPart<F, NBK>;
+// Part-kernel launch if the parts, scales and terms fit one CU's LDS;
+// returns hipErrorNotSupported (nothing launched) otherwise. One tile per
+// workgroup. Up to 32 tokens a workgroup needs few enough registers for
+// three per CU, so any number of tiles runs as one wave of workgroups; past
+// 32 tokens only one fits a CU, and the tiles must not outnumber the CUs
+// (several tiles per workgroup in sequence, one wave per SIMD, measured
+// slower than the chunked tile kernel: Q4_K 9728 x 2560, M = 64, 21.9
+// against 17.6 us).
+template <class F, int TT>
+static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    constexpr int NBK = 3;
+    using C = PartCfg<F, TT, NBK>;
+    using P = typename C::P;
     const MatArgs &a = tasks[0];
     const int nb = a.K / 256;
-    if (nb > 4 * NBK || !x.qt) return hipErrorNotSupported;
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
+    if (nb > 4 * NBK || !x.qt || (TT > 2 && tiles > mfma_cu_count())) return hipErrorNotSupported;
     ResArgs ra{};
     ra.tiles = tiles;
-    ra.off_d = RTM * 4 * P::NI * 1024;
-    ra.lds = ra.off_d + (a.M * nb + 63) / 64 * 256 + nb * 64 * 4 + 2 * TT * 1024;
+    ra.off_d = 4 * P::NI * 1024;
+    ra.off_t = ra.off_d + (a.M * nb + 63) / 64 * 256 + nb * 64 * 4;
+    ra.lds = ra.off_t + C::TERMS;
     if (ra.lds > 160 * 1024) return hipErrorNotSupported;
     MatGroup g{};
     g.n = n;
@@ -1063,23 +1069,8 @@ static hipError_t launch_part_r(const MatArgs *tasks, int n, const Q8KView &x, i
         g.t[i] = tasks[i];
         g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
     }
-    const unsigned grid = unsigned(max((tiles + RTM - 1) / RTM, min(tiles, mfma_cu_count())));
-    hipLaunchKernelGGL((part_kernel<F, TT, NBK, RTM>), dim3(grid), dim3(256), size_t(ra.lds), s, g, x, ra);
+    hipLaunchKernelGGL((part_kernel<F, TT, NBK>), dim3(unsigned(tiles)), dim3(256), size_t(ra.lds), s, g, x, ra);
     return hipGetLastError();
-}
-
-// One tile per workgroup. Up to 32 tokens a workgroup needs few enough
-// registers for three per CU, so any number of tiles runs as one wave of
-// workgroups; past 32 tokens only one fits a CU, and the tiles must not
-// outnumber the CUs (several tiles per workgroup in sequence, one wave per
-// SIMD, measured slower than the chunked tile kernel: Q4_K 9728 x 2560,
-// M = 64, 21.9 against 17.6 us).
-template <class F, int TT>
-static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
-    int tiles = 0;
-    for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
-    if (TT > 2 && tiles > mfma_cu_count()) return hipErrorNotSupported;
-    return launch_part_r<F, TT, 3, 1>(tasks, n, x, tiles, s);
 }
 
 static int group_tiles(const MatArgs *tasks, int n) {
