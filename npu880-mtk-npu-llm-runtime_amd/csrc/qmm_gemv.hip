@@ -236,6 +236,68 @@ struct FmtQ6K {
     }
 };
 
+// Q6_K, 4 lanes per block (the form the library launches): lane k takes
+// half hf = k / 2 and positions l in [16 (k % 2), +16) of every 32-value run
+// i = 0..3 of that half (value 32i + l of the half: ql[64hf + l] low nibble
+// for i = 0, ql[64hf + 32 + l] low for i = 1, the high nibbles for i = 2, 3;
+// qh[32hf + l] bits 2i, 2i + 1; scale sc[8hf + 2i + k % 2]), so each run
+// has one scale per lane. The codes stay unsigned: a run's sum of
+// (q - 32) x is sum q x - 32 sum x, both exact int32 dot products.
+struct FmtQ6K4 {
+    static constexpr int G = 4, BB = 210, QK = 256;
+    static constexpr bool kStaged = true;
+    struct Raw { uint4 a, b, h; uint2 s; uint32_t d; };
+    struct Act { uint4 x[4]; float dx; };
+    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into LDS
+        const int hf = k >> 1, l0 = 16 * (k & 1);
+        Raw r;
+        r.a = lds16_a2(blk + 64 * hf + l0);
+        r.b = lds16_a2(blk + 64 * hf + 32 + l0);
+        r.h = lds16_a2(blk + 128 + 32 * hf + l0);
+        r.s = lds8_a2(blk + 192 + 8 * hf);  // sc[8hf .. 8hf+7]
+        r.d = lds16b_a2(blk + 208);
+        return r;
+    }
+    __device__ static Act load_act(const LdsAct &x, int b, int k) {
+        const int8_t *xb = x.qs + b * 272 + 128 * (k >> 1) + 16 * (k & 1);
+        return {{ld16(xb), ld16(xb + 32), ld16(xb + 64), ld16(xb + 96)}, x.d[b]};
+    }
+    __device__ static float compute(const Raw &r, const Act &a, int k) {
+        const uint32_t M4 = 0x0F0F0F0Fu;
+        const uint32_t av[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, bv[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t hv[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+        int dot[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t q[4] = {(av[w] & M4) | ((hv[w] & 0x03030303u) << 4),
+                                   (bv[w] & M4) | ((hv[w] & 0x0C0C0C0Cu) << 2),
+                                   ((av[w] >> 4) & M4) | (hv[w] & 0x30303030u),
+                                   ((bv[w] >> 4) & M4) | ((hv[w] & 0xC0C0C0C0u) >> 2)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t xw = i == 0 ? (w == 0 ? a.x[0].x : w == 1 ? a.x[0].y : w == 2 ? a.x[0].z : a.x[0].w)
+                                  : i == 1 ? (w == 0 ? a.x[1].x : w == 1 ? a.x[1].y : w == 2 ? a.x[1].z : a.x[1].w)
+                                  : i == 2 ? (w == 0 ? a.x[2].x : w == 1 ? a.x[2].y : w == 2 ? a.x[2].z : a.x[2].w)
+                                           : (w == 0 ? a.x[3].x : w == 1 ? a.x[3].y : w == 2 ? a.x[3].z : a.x[3].w);
+                dot[i] = sdot4(int(q[i]), int(xw), dot[i]);
+                xs[i] = sdot4(int(xw), 0x01010101, xs[i]);
+            }
+        }
+        // sc[8hf + 2i + k % 2]: bytes k % 2, 2 + k % 2, 4 + k % 2, 6 + k % 2
+        const uint64_t s64 = (uint64_t(r.s.y) << 32) | r.s.x;
+        const int is = k & 1;
+        int S = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int sc = int(int8_t(uint8_t(s64 >> (8 * (is + 2 * i)))));
+            S += __mul24(sc, dot[i] - 32 * xs[i]);
+        }
+        S = group4_sum(S);
+        const float d = fp16_bits_to_f32(r.d);
+        return (d * a.dx) * (float)S;  // E:11101
+    }
+};
+
 // ----------------------------------------------------------------- Q8_0
 // Block (34 B, 2-B aligned): d f16 @0, int8 qs[32] @2. Lane k of 4: values
 // [8k, 8k+8). Activations are Q8_0 (E:3394-3406). Read from the LDS stage.
@@ -670,7 +732,7 @@ size_t gemv_lds_bytes(uint32_t type, int K) {
     switch (type) {
         case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K);
         case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, kGemvR, kGemvU>(K);
-        case kQ6_K: return gemv_lds_bytes_t<FmtQ6K, kGemvR, kGemvU>(K);
+        case kQ6_K: return gemv_lds_bytes_t<FmtQ6K4, kGemvR, 3>(K);
         case kQ8_0: return gemv_lds_bytes_t<FmtQ80, kGemvR, kGemvU>(K);
         default: return 0;
     }
@@ -752,7 +814,7 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
     switch (type) {
         case kQ4_K: return launch_gemv_rows<FmtQ4K4, 3>(tasks, n, x32, xk, x0, s);
         case kQ5_K: return launch_gemv_rows<FmtQ5K, kGemvU>(tasks, n, x32, xk, x0, s);
-        case kQ6_K: return launch_gemv_rows<FmtQ6K, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ6_K: return launch_gemv_rows<FmtQ6K4, 3>(tasks, n, x32, xk, x0, s);
         case kQ8_0: return launch_gemv_rows<FmtQ80, kGemvU>(tasks, n, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
     }
