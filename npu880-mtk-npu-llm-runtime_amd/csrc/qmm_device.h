@@ -140,10 +140,6 @@ __device__ inline uint16_t f32_to_fp16_bits(float x) {
 
 // ------------------------------------------------------------ int helpers
 __device__ inline int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-// Per-byte (q - 32) for bytes holding 0..63: ((q | 0x80) - 0x20) ^ 0x80.
-__device__ inline uint32_t sub32_bytes(uint32_t q) {
-    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-}
 __device__ inline uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t byte_shift) {
     return __builtin_amdgcn_alignbyte(hi, lo, byte_shift);
 }

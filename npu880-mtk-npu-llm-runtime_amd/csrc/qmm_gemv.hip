@@ -182,60 +182,7 @@ struct FmtQ5K {
 
 // ----------------------------------------------------------------- Q6_K
 // Block (210 B, 2-B aligned): ql[128] @0, qh[64] @128, int8 sc[16] @192,
-// d f16 @208. Lane k: half hf = k/4, l0 = 8 * (k%4), is = (k%4)/2. For
-// l in [l0, l0+8): values 128hf + 32i + l (i = 0..3) with scale
-// sc[8hf + is + 2i] (E:712-740 / E:11075-11099). Read from the LDS stage.
-struct FmtQ6K {
-    static constexpr int G = 8, BB = 210, QK = 256;
-    static constexpr bool kStaged = true;
-    struct Raw { uint2 a, b, h, s; uint32_t d; };
-    struct Act { uint2 x[4]; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into LDS
-        const int hf = k >> 2, l0 = 8 * (k & 3);
-        Raw r;
-        r.a = lds8_a2(blk + 64 * hf + l0);
-        r.b = lds8_a2(blk + 64 * hf + 32 + l0);
-        r.h = lds8_a2(blk + 128 + 32 * hf + l0);
-        r.s = lds8_a2(blk + 192 + 8 * hf);  // sc[8hf .. 8hf+7]
-        r.d = lds16b_a2(blk + 208);
-        return r;
-    }
-    __device__ static Act load_act(const LdsAct &x, int b, int k) {
-        const int hf = k >> 2, l0 = 8 * (k & 3);
-        const int8_t *xb = x.qs + b * 272 + 128 * hf + l0;
-        return {{ld8(xb), ld8(xb + 32), ld8(xb + 64), ld8(xb + 96)}, x.d[b]};
-    }
-    __device__ static float compute(const Raw &r, const Act &a, int k) {
-        const int is = (k & 3) >> 1;
-        const uint32_t M4 = 0x0F0F0F0Fu;
-        const uint32_t av[2] = {r.a.x, r.a.y}, bv[2] = {r.b.x, r.b.y}, hv[2] = {r.h.x, r.h.y};
-        int dot[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const uint32_t q1 = (av[w] & M4) | ((hv[w] & 0x03030303u) << 4);
-            const uint32_t q2 = (bv[w] & M4) | ((hv[w] & 0x0C0C0C0Cu) << 2);
-            const uint32_t q3 = ((av[w] >> 4) & M4) | (hv[w] & 0x30303030u);
-            const uint32_t q4 = ((bv[w] >> 4) & M4) | ((hv[w] & 0xC0C0C0C0u) >> 2);
-            dot[0] = sdot4(int(sub32_bytes(q1)), int(w ? a.x[0].y : a.x[0].x), dot[0]);
-            dot[1] = sdot4(int(sub32_bytes(q2)), int(w ? a.x[1].y : a.x[1].x), dot[1]);
-            dot[2] = sdot4(int(sub32_bytes(q3)), int(w ? a.x[2].y : a.x[2].x), dot[2]);
-            dot[3] = sdot4(int(sub32_bytes(q4)), int(w ? a.x[3].y : a.x[3].x), dot[3]);
-        }
-        // sc[8hf + is + 2i], i = 0..3: bytes is, is+2, is+4, is+6 of the 8
-        // scale bytes of this half.
-        const uint64_t s64 = (uint64_t(r.s.y) << 32) | r.s.x;
-        int S = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int sc = int(int8_t(uint8_t(s64 >> (8 * (is + 2 * i)))));
-            S += __mul24(sc, dot[i]);
-        }
-        S = group8_sum(S);
-        const float d = fp16_bits_to_f32(r.d);
-        return (d * a.dx) * (float)S;  // E:11101
-    }
-};
-
+// d f16 @208 (E:712-740 / E:11075-11099). Read from the LDS stage.
 // Q6_K, 4 lanes per block (the form the library launches): lane k takes
 // half hf = k / 2 and positions l in [16 (k % 2), +16) of every 32-value run
 // i = 0..3 of that half (value 32i + l of the half: ql[64hf + l] low nibble
