@@ -635,7 +635,9 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-        stage_load(min(gw + stride, ngroups - 1));  // the next group, in flight during the math
+        // the next group, in flight during the math (none for a wave's last:
+        // a clamped duplicate would cost the address units as much as a new one)
+        if (gw + stride < ngroups) stage_load(gw + stride);
         int b = g % nb;
         typename F::Raw rs[U];
         typename F::Act as[U];
