@@ -412,8 +412,10 @@ __host__ __device__ inline size_t gemv_lds_bytes_t(int K) {
 // FUSED: x32 is quantized in the kernel; otherwise prek / pre0 hold the
 // prequantized activation row.
 // GRP: several tasks of the type in one launch (a MatGroup argument);
-// otherwise one task, passed alone (a smaller argument block)
-template <class F, int R, int U, bool FUSED, bool GRP>
+// otherwise one task, passed alone (a smaller argument block).
+// NC: 16-B stage loads per lane that a batch needs (at most NST; every
+// issued load costs address-unit time even when its lanes are clamped)
+template <class F, int R, int U, bool FUSED, bool GRP, int NC>
 __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGroup, MatArgs> grp,
                                                    const float *__restrict__ x32,
                                                    Q8KView prek, Q80View pre0) {
@@ -455,17 +457,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     // the 16-B boundary at or below their start; chunk indices are clamped so
     // that every lane issues its loads (duplicates rewrite identical bytes).
     const int span_mis = int(reinterpret_cast<uintptr_t>(span) & 15);
-    uint4 st[NST > 0 ? NST : 1];
+    static_assert(NC <= NST, "stage loads beyond the stage");
+    uint4 st[NC > 0 ? NC : 1];
     auto stage_load = [&](int t0) __attribute__((always_inline)) {
         const int nb_batch = max(min(SLOTS * U, nblk - t0), 1);
         const uint8_t *base = span + size_t(t0) * F::BB - span_mis;
         const int nchunks = (span_mis + nb_batch * F::BB + 15) >> 4;
 #pragma unroll
-        for (int j = 0; j < NST; ++j) st[j] = ld16_nt(base + 16 * min(64 * j + lane, nchunks - 1));
+        for (int j = 0; j < NC; ++j) st[j] = ld16_nt(base + 16 * min(64 * j + lane, nchunks - 1));
     };
     auto stage_store = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+        for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
     };
 
     // 1. the activation row into registers
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
 // workgroup, and a wave loads its next group's bytes into registers while it
 // computes the current one (one batch per group: R nb <= SLOTS U). After the
 // fill the waves never synchronize with each other.
-template <class F, int R, int U, bool FUSED>
+template <class F, int R, int U, bool FUSED, int NC>
 __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const float *__restrict__ x32,
                                                            Q8KView prek, Q80View pre0) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -597,14 +600,15 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
 
     // a group's bytes from the 16-B boundary at or below its first byte;
     // chunk indices clamped so every lane issues its loads
-    uint4 st[NST];
+    static_assert(NC <= NST, "stage loads beyond the stage");
+    uint4 st[NC];
     auto stage_load = [&](int gr) __attribute__((always_inline)) {
         const int rows = max(0, min(R, a.N - gr * R));
         const uint8_t *span = a.w + size_t(rows > 0 ? gr * R : 0) * a.row_bytes;
         const int mis = int(reinterpret_cast<uintptr_t>(span) & 15);
         const int nchunks = (mis + max(rows * nb, 1) * F::BB + 15) >> 4;
 #pragma unroll
-        for (int j = 0; j < NST; ++j) st[j] = ld16_nt(span - mis + 16 * min(64 * j + lane, nchunks - 1));
+        for (int j = 0; j < NC; ++j) st[j] = ld16_nt(span - mis + 16 * min(64 * j + lane, nchunks - 1));
     };
 
     int gw = int(blockIdx.x) * 4 + wid;
@@ -632,7 +636,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
-        for (int j = 0; j < NST; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+        for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
         // the next group, in flight during the math (none for a wave's last:
@@ -700,13 +704,30 @@ static int cu_count() {
     }
     return cus[dev];
 }
+// Calls launch(std::integral_constant<int, NC>) with the fewest 16-B stage
+// loads per lane (NST - 2 .. NST) that cover a batch of `blocks` blocks from
+// any 16-B misalignment.
+template <class F, int U, class L>
+static hipError_t with_stage_chunks(int blocks, L &&launch) {
+    constexpr int NST = stage_chunks<F, U>();
+    const int need = ((15 + blocks * F::BB + 15) / 16 + 63) / 64;
+    if constexpr (NST >= 3)
+        if (need <= NST - 2) return launch(std::integral_constant<int, NST - 2>{});
+    if constexpr (NST >= 2)
+        if (need <= NST - 1) return launch(std::integral_constant<int, NST - 1>{});
+    return launch(std::integral_constant<int, NST>{});
+}
+
 template <class F, int R, int U>
 static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, const Q8KView &xk, const Q80View &x0,
                                         size_t lds, int wgs, hipStream_t s) {
     const dim3 grid{unsigned(wgs)};
-    if (x32) hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, true>), grid, dim3(256), lds, s, a, x32, xk, x0);
-    else hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, false>), grid, dim3(256), lds, s, a, x32, xk, x0);
-    return hipGetLastError();
+    return with_stage_chunks<F, U>(R * (a.K / F::QK), [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (x32) hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, true, NC>), grid, dim3(256), lds, s, a, x32, xk, x0);
+        else hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, false, NC>), grid, dim3(256), lds, s, a, x32, xk, x0);
+        return hipGetLastError();
+    });
 }
 
 template <class F, int R, int U>
@@ -732,14 +753,18 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
             return launch_gemv_persist_t<F, R, U>(tasks[0], x32, xk, x0, lds, wgs, s);
         }
     }
-    if (n == 1) {
-        if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
-        else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, false>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
-    } else {
-        if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, true>), grid, dim3(256), lds, s, g, x32, xk, x0);
-        else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, true>), grid, dim3(256), lds, s, g, x32, xk, x0);
-    }
-    return hipGetLastError();
+    const int blocks = min(R * (tasks[0].K / F::QK), (64 / F::G) * U);
+    return with_stage_chunks<F, U>(blocks, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (n == 1) {
+            if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, false, NC>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
+            else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, false, NC>), grid, dim3(256), lds, s, g.t[0], x32, xk, x0);
+        } else {
+            if (x32) hipLaunchKernelGGL((gemv_kernel<F, R, U, true, true, NC>), grid, dim3(256), lds, s, g, x32, xk, x0);
+            else hipLaunchKernelGGL((gemv_kernel<F, R, U, false, true, NC>), grid, dim3(256), lds, s, g, x32, xk, x0);
+        }
+        return hipGetLastError();
+    });
 }
 
 // Rows per wave by the launch's total rows and K (measured per shape): the
