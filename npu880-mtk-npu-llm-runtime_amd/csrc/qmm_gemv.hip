@@ -273,8 +273,14 @@ template <> struct IsQ80<FmtQ80> { static constexpr bool v = true; };
 // ------------------------------------------------------ activation fill
 // 16 lanes per 256-value chunk: lane sub of row r in wave w handles values
 // 16 * sub .. +16 of chunk c = 16 * round + 4w + r. Round 0 is loaded before
-// the weights are requested.
+// the weights are requested. A wave whose chunks of a round all lie past the
+// row skips that round (x_has): clamped loads would still cost it issue time
+// ahead of its weight loads.
 struct XPre { float4 v[4]; };
+
+__device__ inline bool x_has(int round, int K) {
+    return 16 * round + 4 * int(threadIdx.x >> 6) < ((K + 255) >> 8);
+}
 
 __device__ inline int x_chunk(int round, int K) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -339,8 +345,9 @@ template <bool Q80>
 __device__ inline void x_fill(const XPre &p0, const float *__restrict__ x, int K, const LdsAct &a) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int nc = (K + 255) >> 8;
-    x_quant<Q80>(p0, x_chunk(0, K), K, 4 * wid + (lane >> 4) < nc, a);
+    if (x_has(0, K)) x_quant<Q80>(p0, x_chunk(0, K), K, 4 * wid + (lane >> 4) < nc, a);
     for (int round = 1; 16 * round < nc; ++round) {
+        if (!x_has(round, K)) break;
         XPre p;
         const int c = x_chunk(round, K);
         x_load(x, K, c, p);
@@ -353,15 +360,18 @@ struct CPre { uint4 q[4]; int32_t bs[2]; float d[2]; };
 
 template <bool Q80>
 __device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t *bs, int K, CPre &p) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, t0 = 64 * int(threadIdx.x >> 6);
     const int nq = K >> 4, nd = Q80 ? (K >> 5) : (K >> 8);
-    // clamped indices: every load is issued (duplicates are never stored)
+    // clamped indices (duplicates are never stored); a load none of whose
+    // lanes is in range is not issued (the test is uniform over the wave)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p.q[i] = ld16(qs + 16 * min(t + 256 * i, nq - 1));
+    for (int i = 0; i < 4; ++i)
+        if (t0 + 256 * i < nq) p.q[i] = ld16(qs + 16 * min(t + 256 * i, nq - 1));
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        if constexpr (!Q80) p.bs[i] = bs[min(t + 256 * i, (K >> 5) - 1)];
-        p.d[i] = d[min(t + 256 * i, nd - 1)];
+        if constexpr (!Q80)
+            if (t0 + 256 * i < (K >> 5)) p.bs[i] = bs[min(t + 256 * i, (K >> 5) - 1)];
+        if (t0 + 256 * i < nd) p.d[i] = d[min(t + 256 * i, nd - 1)];
     }
 }
 
@@ -474,7 +484,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     // 1. the activation row into registers
     XPre xp;
     CPre cp;
-    if constexpr (FUSED) x_load(x32, K, x_chunk(0, K), xp);
+    if constexpr (FUSED) {
+        if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
+    }
     else cpre_load<q80>(pq, pd, pb, K, cp);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first in issue order
     // 2. weights of the first batch
@@ -616,7 +628,9 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     // 1. the activation row, then the first group's bytes
     XPre xp;
     CPre cp;
-    if constexpr (FUSED) x_load(x32, K, x_chunk(0, K), xp);
+    if constexpr (FUSED) {
+        if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
+    }
     else cpre_load<q80>(pq, pd, pb, K, cp);
     __builtin_amdgcn_sched_barrier(0);
     stage_load(min(gw, ngroups - 1));
