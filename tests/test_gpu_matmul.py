@@ -51,6 +51,35 @@ def test_gemv_tall_tensors(ctx, oracle, type_id, N, K, residual):
     _run(ctx, oracle, type_id, N, K, 1, seed=1100 + type_id, residual=residual)
 
 
+@pytest.mark.parametrize("type_id,N,K,residual", [(TYPE_Q4_K, 9727, 2560, True), (TYPE_Q6_K, 8195, 768, False),
+                                                  (TYPE_Q8_0, 8200, 288, True), (TYPE_Q4_K, 8192, 3072, False)])
+def test_gemv_two_group_grid(ctx, oracle, type_id, N, K, residual):
+    """The persistent batch-1 grid where no wave has more than two row groups
+    (60 % of the waves have a second, prefetched): ragged last groups, groups
+    that start 8 B past a 16-B boundary (Q6_K at K = 768, Q8_0 at K = 288),
+    K = 3072."""
+    _run(ctx, oracle, type_id, N, K, 1, seed=1200 + N + type_id, residual=residual)
+
+
+def test_gemv_two_group_grid_unaligned_base(ctx, oracle):
+    """The same grid on a weight pointer 8 B past a 16-B boundary: rows
+    1..N of an uploaded N + 1 (840-B Q6_K rows)."""
+    N, K = 8192, 1024
+    say(f"Q6_K N={N} K={K} M=1 from row 1")
+    w = synth.weights(TYPE_Q6_K, N + 1, K, seed=1300)
+    rb = qmm_hip.row_bytes(TYPE_Q6_K, K)
+    x = synth.activations(1, K, seed=1301)
+    wb = ctx.weight_upload(w, TYPE_Q6_K, N + 1, K)
+    xb = ctx.upload(x)
+    yb = ctx.malloc(N * 4)
+    ctx.gemm_multi_dispatch(xb, 1, K, [qmm_hip.MatrixTask(wb.ptr + rb, TYPE_Q6_K, N, K, yb, N)])
+    ctx.sync()
+    ref = oracle.gemm_multi(x, [dict(w=w[rb:], type=TYPE_Q6_K, rows=N)])[0]
+    check_outputs(ctx.d2h(yb, np.float32, (1, N)), ref, "Q6_K from row 1")
+    for b in (wb, xb, yb):
+        ctx.free(b)
+
+
 @pytest.mark.parametrize("type_id,N,K", [(TYPE_Q6_K, 2560, 9728), (TYPE_Q5_K, 4096, 2560),
                                          (TYPE_Q8_0, 2560, 2560), (TYPE_Q4_K, 2560, 4096)])
 def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
