@@ -488,6 +488,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
         if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
     }
     else cpre_load<q80>(pq, pd, pb, K, cp);
+    if constexpr (FUSED) wait_vmcnt<0>();  // x before the weights, as in the persistent kernel
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads first in issue order
     // 2. weights of the first batch
     typename F::Raw raw[U];
@@ -632,6 +633,10 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
     }
     else cpre_load<q80>(pq, pd, pb, K, cp);
+    // a wave that loads x waits for it before it requests weights (measured:
+    // weights first 5.09 us, x first 4.88; all waves held until x is in
+    // 5.20): x is the critical path and weight requests slow its arrival
+    if constexpr (FUSED) wait_vmcnt<0>();
     __builtin_amdgcn_sched_barrier(0);
     stage_load(min(gw, ngroups - 1));
     __builtin_amdgcn_sched_barrier(0);
