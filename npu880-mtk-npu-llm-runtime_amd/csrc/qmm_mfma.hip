@@ -161,10 +161,6 @@ struct MQ6KS : MQ6K {
 };
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-__device__ inline uint32_t bytes_times(uint32_t q, uint32_t f) {  // per byte, q_b * f < 256
-    const u16x2 v = __builtin_bit_cast(u16x2, q) * u16x2{uint16_t(f), uint16_t(f)};
-    return __builtin_bit_cast(uint32_t, v);
-}
 __device__ inline int4v mfma16x16x64(const uint4 &a, const uint4 &b, int4v c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int4v, a), __builtin_bit_cast(int4v, b), c,
                                                  0, 0, 0);
@@ -172,18 +168,31 @@ __device__ inline int4v mfma16x16x64(const uint4 &a, const uint4 &b, int4v c) {
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 // B operands of one row tile's block: [chunk][high part | low part | mins]
 struct SplitB { uint4 b1[4], b2[4], bm[4]; };
-__device__ inline void split_b(const MQ4K::W &w, const int (&sc)[8], const int (&m)[8], SplitB &o) {
+// byte b of w in both 16-bit halves / in all four bytes
+__device__ inline u16x2 byte_pair(uint32_t w, int b) {
+    return __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, w, 0x0C000C00u | (uint32_t(b) * 0x00010001u)));
+}
+__device__ inline uint32_t byte_bcast(uint32_t w, int b) { return __builtin_amdgcn_perm(0u, w, uint32_t(b) * 0x01010101u); }
+__device__ inline uint32_t bytes_times(uint32_t q, u16x2 f) {  // per byte, q_b * f < 256
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * f);
+}
+// scw / mw: the 8 scales / mins of the block four to a dword (sub-block u is
+// byte u & 3 of word u >> 2, as scales_k4_packed gives them); a scale
+// s = 8 (s >> 3) + (s & 7) splits into the high and low parts per byte at once
+__device__ inline void split_b(const MQ4K::W &w, const uint32_t (&scw)[2], const uint32_t (&mw)[2], SplitB &o) {
+    const uint32_t shw[2] = {(scw[0] >> 3) & 0x07070707u, (scw[1] >> 3) & 0x07070707u};
+    const uint32_t slw[2] = {scw[0] & 0x07070707u, scw[1] & 0x07070707u};
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
         const uint2 q = w.q[h];
+        const int d = h >> 1, b0 = 2 * (h & 1), b1 = b0 + 1;  // sub-blocks 2h, 2h + 1
         const uint32_t lo0 = q.x & 0x0F0F0F0Fu, lo1 = q.y & 0x0F0F0F0Fu;
         const uint32_t hi0 = (q.x >> 4) & 0x0F0F0F0Fu, hi1 = (q.y >> 4) & 0x0F0F0F0Fu;
-        const uint32_t sh0 = uint32_t(sc[2 * h]) >> 3, sl0 = uint32_t(sc[2 * h]) & 7u;
-        const uint32_t sh1 = uint32_t(sc[2 * h + 1]) >> 3, sl1 = uint32_t(sc[2 * h + 1]) & 7u;
+        const u16x2 sh0 = byte_pair(shw[d], b0), sl0 = byte_pair(slw[d], b0);
+        const u16x2 sh1 = byte_pair(shw[d], b1), sl1 = byte_pair(slw[d], b1);
         o.b1[h] = make_uint4(bytes_times(lo0, sh0), bytes_times(lo1, sh0), bytes_times(hi0, sh1), bytes_times(hi1, sh1));
         o.b2[h] = make_uint4(bytes_times(lo0, sl0), bytes_times(lo1, sl0), bytes_times(hi0, sl1), bytes_times(hi1, sl1));
-        const uint32_t m0 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h]), 0u);
-        const uint32_t m1 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h + 1]), 0u);
+        const uint32_t m0 = byte_bcast(mw[d], b0), m1 = byte_bcast(mw[d], b1);
         o.bm[h] = make_uint4(m0, m0, m1, m1);
     }
 }
@@ -200,14 +209,14 @@ __device__ inline void fold4(uint32_t q, u16x2 sp, u16x2 cp, uint32_t &lo, uint3
     hi = __builtin_amdgcn_perm(po, pe, 0x07030501u);
 }
 
-__device__ inline void split_b(const MQ5K::W &w, const int (&sc)[8], const int (&m)[8], SplitB &o) {
+__device__ inline void split_b(const MQ5K::W &w, const uint32_t (&scw)[2], const uint32_t (&mw)[2], SplitB &o) {
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
         uint32_t hi[4], lo[4];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int u = 2 * h + k;
-            const u16x2 sp = {uint16_t(sc[u]), uint16_t(sc[u])};
+            const u16x2 sp = byte_pair(scw[u >> 2], u & 3);
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const uint32_t v = e ? w.q[h].y : w.q[h].x, qv = e ? w.qh.y : w.qh.x;
@@ -217,8 +226,7 @@ __device__ inline void split_b(const MQ5K::W &w, const int (&sc)[8], const int (
         }
         o.b1[h] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
         o.b2[h] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        const uint32_t m0 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h]), 0u);
-        const uint32_t m1 = __builtin_amdgcn_perm(0u, uint32_t(m[2 * h + 1]), 0u);
+        const uint32_t m0 = byte_bcast(mw[h >> 1], 2 * (h & 1)), m1 = byte_bcast(mw[h >> 1], 2 * (h & 1) + 1);
         o.bm[h] = make_uint4(m0, m0, m1, m1);
     }
 }
@@ -455,7 +463,8 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
 #pragma unroll
         for (int jj = 0; jj < KCB / KS; ++jj) {
             const int j = jj * KS + kp;
-            const bool valid = ch * KCB + j < nb;
+            // (one block per chunk: every chunk walked is inside K)
+            const bool valid = KCB == 1 || ch * KCB + j < nb;
             // block index into the codes and scales: of the chunk's slot, or of
             // the resident arrays (block 0 stands in for blocks past K)
             const int jr = C::AR ? (valid ? ch * KCB + j : 0) : j;
@@ -472,7 +481,11 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
                 const float d = valid ? sc.d : 0.0f, dmin = valid ? sc.dmin : 0.0f;
                 [[maybe_unused]] SplitB sb;
                 if constexpr (F::kSplit) {
-                    if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+                    if constexpr (F::kMin) {
+                uint32_t scp[2], mp[2];
+                scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scp, mp);
+                split_b(wv, scp, mp, sb);
+            }
                     else split_b(wv, cl, sb);
                 }
 #pragma unroll
@@ -710,7 +723,11 @@ __global__ __launch_bounds__(256 * RTM) void res_kernel(MatGroup grp, Q8KView x,
         [[maybe_unused]] SplitB sb;
         [[maybe_unused]] uint32_t scw[2], mw[2];
         if constexpr (F::kSplit) {
-            if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+            if constexpr (F::kMin) {
+                uint32_t scp[2], mp[2];
+                scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scp, mp);
+                split_b(wv, scp, mp, sb);
+            }
             else split_b(wv, cl, sb);
         } else {
             scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scw, mw);
@@ -912,7 +929,11 @@ __global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResA
         [[maybe_unused]] SplitB sb;
         [[maybe_unused]] uint32_t scw[2], mw[2];
         if constexpr (F::kSplit) {
-            if constexpr (F::kMin) split_b(wv, sc.sc, sc.m, sb);
+            if constexpr (F::kMin) {
+                uint32_t scp[2], mp[2];
+                scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scp, mp);
+                split_b(wv, scp, mp, sb);
+            }
             else split_b(wv, cl, sb);
         } else {
             scales_k4_packed(wv.h.y, wv.h.z, wv.h.w, scw, mw);
