@@ -145,17 +145,28 @@ struct MQ6KS : MQ6K {
     static constexpr bool kSplit = true;
     static constexpr int kShift = 8;  // S = (D1 << 8) + D2
     struct W { uint2 a[2], b[2], qh[2]; uint2 s0, s1; uint32_t d; };
+    // Every field lies a multiple of 8 B from the 2-B aligned block start, so
+    // one misalignment (0 or 2 B) serves all: each 8-B field is three dword
+    // reads and two funnel shifts, the third dword read whatever the
+    // misalignment (at most bytes 208..211 of the block: the staged row
+    // holds them).
     __device__ static W load_lds(const uint8_t *blk, int c) {
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        auto rd8 = [&](int dw) __attribute__((always_inline)) {
+            const uint32_t w0 = q[dw], w1 = q[dw + 1], w2 = q[dw + 2];
+            return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
+        };
         W w;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-            w.a[hf] = lds8_a2(blk + 64 * hf + 8 * c);
-            w.b[hf] = lds8_a2(blk + 64 * hf + 32 + 8 * c);
-            w.qh[hf] = lds8_a2(blk + 128 + 32 * hf + 8 * c);
+            w.a[hf] = rd8(16 * hf + 2 * c);
+            w.b[hf] = rd8(16 * hf + 8 + 2 * c);
+            w.qh[hf] = rd8(32 + 8 * hf + 2 * c);
         }
-        w.s0 = lds8_a2(blk + 192);
-        w.s1 = lds8_a2(blk + 200);
-        w.d = lds16b_a2(blk + 208);
+        w.s0 = rd8(48);
+        w.s1 = rd8(50);
+        w.d = (q[52] >> (8 * sh)) & 0xFFFFu;
         return w;
     }
 };
