@@ -195,14 +195,25 @@ struct FmtQ6K4 {
     static constexpr bool kStaged = true;
     struct Raw { uint4 a, b, h; uint2 s; uint32_t d; };
     struct Act { uint4 x[4]; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into LDS
+    // blk points into LDS, 2-B aligned. Every field lies a multiple of 8 B
+    // from it, so one misalignment (0 or 2 B) serves all: aligned dword reads
+    // (the last one read whatever the misalignment: at most 2 B past the
+    // block, inside the stage) and funnel shifts.
+    __device__ static Raw load(const uint8_t *blk, int k) {
         const int hf = k >> 1, l0 = 16 * (k & 1);
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        auto rd16 = [&](int dw) __attribute__((always_inline)) {
+            const uint32_t w0 = q[dw], w1 = q[dw + 1], w2 = q[dw + 2], w3 = q[dw + 3], w4 = q[dw + 4];
+            return make_uint4(funnel(w1, w0, sh), funnel(w2, w1, sh), funnel(w3, w2, sh), funnel(w4, w3, sh));
+        };
         Raw r;
-        r.a = lds16_a2(blk + 64 * hf + l0);
-        r.b = lds16_a2(blk + 64 * hf + 32 + l0);
-        r.h = lds16_a2(blk + 128 + 32 * hf + l0);
-        r.s = lds8_a2(blk + 192 + 8 * hf);  // sc[8hf .. 8hf+7]
-        r.d = lds16b_a2(blk + 208);
+        r.a = rd16(16 * hf + l0 / 4);
+        r.b = rd16(16 * hf + 8 + l0 / 4);
+        r.h = rd16(32 + 8 * hf + l0 / 4);
+        const uint32_t s0 = q[48 + 2 * hf], s1 = q[49 + 2 * hf], s2 = q[50 + 2 * hf];
+        r.s = make_uint2(funnel(s1, s0, sh), funnel(s2, s1, sh));  // sc[8hf .. 8hf+7]
+        r.d = (q[52] >> (8 * sh)) & 0xFFFFu;
         return r;
     }
     __device__ static Act load_act(const LdsAct &x, int b, int k) {
