@@ -199,25 +199,6 @@ __device__ inline uint32_t ld16b_a2(const uint8_t *p) {
     return (w >> (sh * 8)) & 0xFFFFu;
 }
 
-// LDS reads at 2-B aligned offsets (stage of 2-B aligned blocks)
-__device__ inline uint2 lds8_a2(const uint8_t *p) {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[sh ? 2 : 1];
-    return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
-}
-// 16 bytes at a 2-B aligned LDS offset
-__device__ inline uint4 lds16_a2(const uint8_t *p) {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(p - sh);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[sh ? 4 : 3];
-    return make_uint4(funnel(w1, w0, sh), funnel(w2, w1, sh), funnel(w3, w2, sh), funnel(w4, w3, sh));
-}
-__device__ inline uint32_t lds16b_a2(const uint8_t *p) {
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
-    return (*reinterpret_cast<const uint32_t *>(p - sh) >> (sh * 8)) & 0xFFFFu;
-}
-
 // ------------------------------------------------------ Q8 quantization
 // Q8_K / Q8_0 codes of fp16-rounded values (quantize_row_fp16_to_q8_k
 // E:947-988): id = 127 / amax, correctly rounded, computed once per block;

@@ -264,7 +264,17 @@ struct FmtQ80 {
     static constexpr bool kStaged = true;
     struct Raw { uint2 q; uint32_t d; };
     struct Act { uint2 x; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) { return {lds8_a2(blk + 2 + 8 * k), lds16b_a2(blk)}; }
+    // blk in LDS, 2-B aligned (misalignment sh = 0 or 2): the codes at blk + 2 +
+    // 8 k start sh ^ 2 bytes into dword 2 k + sh / 2 of blk - sh; the third
+    // dword is read whatever the shift (at most 4 B past the block, inside the
+    // staged bytes' region)
+    __device__ static Raw load(const uint8_t *blk, int k) {
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3), s2 = sh ^ 2u;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        const uint32_t *p = q + 2 * k + (sh >> 1);
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+        return {make_uint2(funnel(w1, w0, s2), funnel(w2, w1, s2)), (q[0] >> (8 * sh)) & 0xFFFFu};
+    }
     __device__ static Act load_act(const LdsAct &x, int b, int k) {
         return {ld8(x.qs + lds_pad(b * 32 + 8 * k)), x.d[b]};
     }

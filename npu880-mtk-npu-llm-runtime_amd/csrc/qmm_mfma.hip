@@ -100,7 +100,17 @@ struct MQ80 {
     static constexpr bool kMin = false, kSplit = false;
     struct W { uint2 q; uint32_t d; };
     __device__ static W load(const uint8_t *blk, int c) { return {ld8_a2(blk + 2 + 8 * c), ld16b_a2(blk)}; }
-    __device__ static W load_lds(const uint8_t *blk, int c) { return {lds8_a2(blk + 2 + 8 * c), lds16b_a2(blk)}; }
+    // blk in LDS, 2-B aligned (misalignment sh = 0 or 2): the codes at blk + 2 +
+    // 8 c start sh ^ 2 bytes into dword 2 c + sh / 2 of blk - sh; the third
+    // dword is read whatever the shift (at most 4 B past the block, inside the
+    // staged bytes' region)
+    __device__ static W load_lds(const uint8_t *blk, int c) {
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3), s2 = sh ^ 2u;
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        const uint32_t *p = q + 2 * c + (sh >> 1);
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+        return {make_uint2(funnel(w1, w0, s2), funnel(w2, w1, s2)), (q[0] >> (8 * sh)) & 0xFFFFu};
+    }
     __device__ static int koff(int u, int c) { (void)u; return 8 * c; }
     __device__ static uint2 bop(const W &w, int u, int c) { (void)u; (void)c; return w.q; }
 };
