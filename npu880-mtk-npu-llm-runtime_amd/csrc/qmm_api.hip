@@ -11,6 +11,7 @@
 // the GEMV kernels, M >= 2 to the MFMA kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -107,6 +108,10 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // the LM-head epilogue: rows of one tensor (contiguous, or gathered by id)
 // on prequantized activations, then the running argmax update
+int gemv_argmax_fused(qmm_context *ctx, const void *q8k, const void *q80, int K, qmm_matrix_task *t,
+                      const uint32_t *ids, uint32_t row_base, bool round16, void *part, float *best_val,
+                      uint32_t *best_id, bool *done);
+
 int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w, uint32_t type,
               int rows, uint32_t row_base, const uint32_t *ids, float *logits_out, float *best_val,
               uint32_t *best_id) {
@@ -117,7 +122,9 @@ int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, 
     if (!aligned(best_val, 4) || !aligned(best_id, 4)) return fail(ctx, QMM_EALIGN, "best_val/best_id must be 4-B aligned");
     const size_t rb = qmm_row_bytes(type, K);
     const size_t logit_b = logits_out ? 0 : align256(size_t(M) * rows * 4);
-    const size_t part_b = align256(qmm::argmax_scratch_bytes(M, rows));
+    // partials: per 1024-row slice, or (M = 1) per workgroup of the fused grid
+    const size_t part_b = align256(std::max(qmm::argmax_scratch_bytes(M, rows),
+                                            M == 1 ? size_t(qmm::kMaxArgmaxParts) * sizeof(qmm::Best) : size_t(0)));
     const size_t gather_b = ids ? align256(size_t(rows) * rb) : 0;
     int rc = use_device(ctx);
     if (rc) return rc;
@@ -142,6 +149,11 @@ int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, 
     t.res_stride = 0;
     t.rows = rows;
     t.cols = K;
+    if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
+        bool done = false;
+        rc = gemv_argmax_fused(ctx, q8k, q80, K, &t, ids, row_base, ids == nullptr, part, best_val, best_id, &done);
+        if (rc || done) return rc;
+    }
     rc = qmm_gemm_multi_dispatch_prequantized(ctx, q8k, q80, M, K, &t, 1);
     if (rc) return rc;
     hipError_t e = qmm::launch_argmax(logits, M, rows, size_t(rows), /*round16=*/ids == nullptr, ids, row_base,
@@ -229,6 +241,53 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
                                       : qmm::launch_mfma(tasks[t0].type, group, n, xk, x0, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
     }
+    return QMM_OK;
+}
+
+// M = 1 LM head: the prequantized dispatch's checks, then the GEMV with the
+// running argmax fused and the final combine. *done stays false (nothing
+// launched) where the fused grid does not apply.
+int gemv_argmax_fused(qmm_context *ctx, const void *q8k, const void *q80, int K, qmm_matrix_task *t,
+                      const uint32_t *ids, uint32_t row_base, bool round16, void *part, float *best_val,
+                      uint32_t *best_id, bool *done) {
+    *done = false;
+    bool need_q8k, need_q80;
+    int rc = check_tasks(ctx, 1, K, t, 1, &need_q8k, &need_q80);
+    if (rc) return rc;
+    if (need_q8k && !q8k) return fail(ctx, QMM_EINVAL, "K-quant task without Q8_K activations");
+    if (need_q80 && !q80) return fail(ctx, QMM_EINVAL, "Q8_0 task without Q8_0 activations");
+    if ((q8k && !aligned(q8k, 16)) || (q80 && !aligned(q80, 16)))
+        return fail(ctx, QMM_EALIGN, "activation buffers must be 16-B aligned");
+    qmm::Q8KView xk{nullptr, nullptr, nullptr, nullptr};
+    qmm::Q80View x0{nullptr, nullptr};
+    if (need_q8k) {
+        const qmm::Q8KLayout L(1, K);
+        const uint8_t *b = static_cast<const uint8_t *>(q8k);
+        xk = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off),
+              reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off)};
+    }
+    if (need_q80) {
+        const qmm::Q80Layout L(1, K);
+        const uint8_t *b = static_cast<const uint8_t *>(q80);
+        x0 = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off)};
+    }
+    qmm::MatArgs a;
+    a.w = static_cast<const uint8_t *>(t->w_base);
+    a.row_bytes = t->row_bytes;
+    a.N = t->rows;
+    a.K = K;
+    a.M = 1;
+    a.y = t->dst;
+    a.ldy = size_t(t->rows);
+    a.res = nullptr;
+    a.ldr = size_t(t->rows);
+    int nparts = 0;
+    hipError_t e = qmm::launch_gemv_argmax(t->type, a, xk, x0, round16, part, &nparts, ctx->stream);
+    if (e == hipErrorNotSupported) return QMM_OK;
+    if (e != hipSuccess) return hip_fail(ctx, e, "GEMV + argmax launch");
+    e = qmm::launch_argmax_final(part, nparts, ids, row_base, best_val, best_id, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "argmax launch");
+    *done = true;
     return QMM_OK;
 }
 

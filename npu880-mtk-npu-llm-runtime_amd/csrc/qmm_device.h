@@ -123,6 +123,20 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
                        const Q80View &x0, hipStream_t s);
 // dynamic LDS bytes the GEMV needs for K (must stay <= 64 KiB)
 size_t gemv_lds_bytes(uint32_t type, int K);
+// M = 1 GEMV of one task with the LM head's running (max, argmax) fused into
+// its persistent grid: each workgroup writes one partial (value, row) to part
+// (round16: values rounded to fp16 first); *nparts receives their number
+// (<= kMaxArgmaxParts) for launch_argmax_final. hipErrorNotSupported, with
+// nothing launched, where that grid does not apply.
+constexpr int kMaxArgmaxParts = 4096;
+struct AmaxOut {
+    void *part;
+    int round16;
+};
+hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
+                              void *part, int *nparts, hipStream_t s);
+hipError_t launch_argmax_final(const void *part, int nparts, const uint32_t *ids, uint32_t row_base,
+                               float *best_val, uint32_t *best_id, hipStream_t s);
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s);
 
@@ -197,6 +211,31 @@ __device__ inline uint32_t ld16b_a2(const uint8_t *p) {
     const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
     const uint32_t w = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p - sh));
     return (w >> (sh * 8)) & 0xFFFFu;
+}
+
+// ------------------------------------------------- running (max, argmax)
+// (value, row) with kNone for empty; better(a, b) takes b when a is empty,
+// b is larger, or b is equal and at an earlier row — so any reduction order
+// gives the first row holding the maximum, as a scan in row order would
+struct Best {
+    float v;
+    uint32_t i;
+};
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+__device__ inline Best better(Best a, Best b) {
+    if (b.i == kNone) return a;
+    if (a.i == kNone || b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+__device__ inline Best wave_best(Best b) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        Best o;
+        o.v = __shfl_xor(b.v, off, 64);
+        o.i = uint32_t(__shfl_xor(int(b.i), off, 64));
+        b = better(b, o);
+    }
+    return b;
 }
 
 // ------------------------------------------------------ Q8 quantization

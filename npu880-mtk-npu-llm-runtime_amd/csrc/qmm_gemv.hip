@@ -605,9 +605,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
 // workgroup, and a wave loads its next group's bytes into registers while it
 // computes the current one (one batch per group: R nb <= SLOTS U). After the
 // fill the waves never synchronize with each other.
-template <class F, int R, int U, bool FUSED, int NC>
+template <class F, int R, int U, bool FUSED, int NC, bool AMAX>
 __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const float *__restrict__ x32,
-                                                           Q8KView prek, Q80View pre0) {
+                                                           Q8KView prek, Q80View pre0, AmaxOut am) {
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
@@ -667,6 +667,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     lds_barrier();
     // 3. groups
     const int adv = SLOTS % nb;
+    Best wb{-INFINITY, kNone};  // AMAX: the wave's running (max, first row)
     for (; gw < ngroups; gw += stride) {
         const int row0 = gw * R;
         const int nrows = min(R, a.N - row0);
@@ -717,6 +718,21 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
             const int row = row0 + lane;
             if (a.res) acc = acc + a.res[row];
             a.y[row] = acc;
+            if constexpr (AMAX) {
+                const float v = am.round16 ? round_to_fp16(acc) : acc;  // as the argmax kernels compare
+                if (v == v) wb = better(wb, Best{v, uint32_t(row)});
+            }
+        }
+    }
+    if constexpr (AMAX) {  // one partial per workgroup (per wave was slower: 4x the partials to combine)
+        __shared__ Best wsb[4];
+        wb = wave_best(wb);
+        if (lane == 0) wsb[wid] = wb;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            Best r = wsb[0];
+            for (int w = 1; w < 4; ++w) r = better(r, wsb[w]);
+            static_cast<Best *>(am.part)[blockIdx.x] = r;
         }
     }
 }
@@ -758,16 +774,41 @@ static hipError_t with_stage_chunks(int blocks, L &&launch) {
     return launch(std::integral_constant<int, NST>{});
 }
 
-template <class F, int R, int U>
+template <class F, int R, int U, bool AMAX = false>
 static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, const Q8KView &xk, const Q80View &x0,
-                                        size_t lds, int wgs, hipStream_t s) {
+                                        size_t lds, int wgs, hipStream_t s, AmaxOut am = {}) {
     const dim3 grid{unsigned(wgs)};
     return with_stage_chunks<F, U>(R * (a.K / F::QK), [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
-        if (x32) hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, true, NC>), grid, dim3(256), lds, s, a, x32, xk, x0);
-        else hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, false, NC>), grid, dim3(256), lds, s, a, x32, xk, x0);
+        if (x32) hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, true, NC, AMAX>), grid, dim3(256), lds, s, a, x32, xk, x0, am);
+        else hipLaunchKernelGGL((gemv_persist_kernel<F, R, U, false, NC, AMAX>), grid, dim3(256), lds, s, a, x32, xk, x0, am);
         return hipGetLastError();
     });
+}
+
+// The persistent grid of one task (R = kGemvR) with the running argmax
+// fused; NotSupported (nothing launched) where that grid does not apply.
+template <class F, int U>
+static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
+                                       void *part, int *nparts, hipStream_t s) {
+    constexpr int R = kGemvR;
+    const int nb = a.K / F::QK, cus = cu_count();
+    const int wg0 = ((a.N + R - 1) / R + 3) / 4;
+    if (a.N < (IsQ80<F>::v ? 8192 : 4096) || R * nb > (64 / F::G) * U || wg0 < 2 * cus) return hipErrorNotSupported;
+    const int wgs = min(3 * cus, wg0 * 5 / 8);
+    if (wgs > kMaxArgmaxParts) return hipErrorNotSupported;
+    *nparts = wgs;
+    return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
+                                                AmaxOut{part, round16 ? 1 : 0});
+}
+
+hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
+                              void *part, int *nparts, hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, part, nparts, s);
+        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, part, nparts, s);
+        default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
+    }
 }
 
 template <class F, int R, int U>

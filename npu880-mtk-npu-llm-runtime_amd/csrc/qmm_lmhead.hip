@@ -13,29 +13,6 @@
 
 namespace qmm {
 
-struct Best {
-    float v;
-    uint32_t i;  // kNone: empty
-};
-constexpr uint32_t kNone = 0xFFFFFFFFu;
-
-// b replaces a: a is empty, or b is larger, or b is equal and earlier
-__device__ inline Best better(Best a, Best b) {
-    if (b.i == kNone) return a;
-    if (a.i == kNone || b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
-    return a;
-}
-
-__device__ inline Best wave_best(Best b) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        Best o;
-        o.v = __shfl_xor(b.v, off, 64);
-        o.i = uint32_t(__shfl_xor(int(b.i), off, 64));
-        b = better(b, o);
-    }
-    return b;
-}
 
 __device__ inline Best block_best(Best b, Best *sh) {
     b = wave_best(b);
@@ -112,6 +89,14 @@ hipError_t launch_argmax(const float *logits, int M, int rows, size_t ldl, bool 
         hipLaunchKernelGGL(argmax_partial_kernel<false>, g, dim3(256), 0, s, logits, rows, ldl, part, nslices);
     hipLaunchKernelGGL(argmax_final_kernel, dim3(unsigned(M)), dim3(256), 0, s, part, nslices, ids, row_base,
                        best_val, best_id);
+    return hipGetLastError();
+}
+
+// one token: combine nparts partials in order, then the strict update
+hipError_t launch_argmax_final(const void *part, int nparts, const uint32_t *ids, uint32_t row_base,
+                               float *best_val, uint32_t *best_id, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, s, static_cast<const Best *>(part), nparts, ids,
+                       row_base, best_val, best_id);
     return hipGetLastError();
 }
 
