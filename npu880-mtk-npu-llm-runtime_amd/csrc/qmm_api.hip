@@ -197,11 +197,11 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
     return QMM_OK;
 }
 
-// x32 != nullptr (M = 1 only): the GEMV kernels quantize x themselves.
-int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q80, int M, int K,
-              const qmm_matrix_task *tasks, int n_tasks) {
-    qmm::Q8KView xk{nullptr, nullptr, nullptr, nullptr};
-    qmm::Q80View x0{nullptr, nullptr};
+// Kernel views of prequantized activation buffers (a null buffer gives a
+// null view).
+void act_views(const void *q8k, const void *q80, int M, int K, qmm::Q8KView &xk, qmm::Q80View &x0) {
+    xk = {nullptr, nullptr, nullptr, nullptr};
+    x0 = {nullptr, nullptr};
     if (q8k) {
         const qmm::Q8KLayout L(M, K);
         const uint8_t *b = static_cast<const uint8_t *>(q8k);
@@ -213,6 +213,14 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
         const uint8_t *b = static_cast<const uint8_t *>(q80);
         x0 = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off)};
     }
+}
+
+// x32 != nullptr (M = 1 only): the GEMV kernels quantize x themselves.
+int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q80, int M, int K,
+              const qmm_matrix_task *tasks, int n_tasks) {
+    qmm::Q8KView xk;
+    qmm::Q80View x0;
+    act_views(q8k, q80, M, K, xk, x0);
     // tasks of one type run as one launch (up to kMaxGroup per launch), in
     // order of first appearance; outputs are disjoint, so grouping changes
     // no result
@@ -258,19 +266,9 @@ int gemv_argmax_fused(qmm_context *ctx, const void *q8k, const void *q80, int K,
     if (need_q80 && !q80) return fail(ctx, QMM_EINVAL, "Q8_0 task without Q8_0 activations");
     if ((q8k && !aligned(q8k, 16)) || (q80 && !aligned(q80, 16)))
         return fail(ctx, QMM_EALIGN, "activation buffers must be 16-B aligned");
-    qmm::Q8KView xk{nullptr, nullptr, nullptr, nullptr};
-    qmm::Q80View x0{nullptr, nullptr};
-    if (need_q8k) {
-        const qmm::Q8KLayout L(1, K);
-        const uint8_t *b = static_cast<const uint8_t *>(q8k);
-        xk = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off),
-              reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off)};
-    }
-    if (need_q80) {
-        const qmm::Q80Layout L(1, K);
-        const uint8_t *b = static_cast<const uint8_t *>(q80);
-        x0 = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off)};
-    }
+    qmm::Q8KView xk;  // (the caller has made the context's device current)
+    qmm::Q80View x0;
+    act_views(need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, 1, K, xk, x0);
     qmm::MatArgs a;
     a.w = static_cast<const uint8_t *>(t->w_base);
     a.row_bytes = t->row_bytes;
