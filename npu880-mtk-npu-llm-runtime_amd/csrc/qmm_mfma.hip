@@ -486,6 +486,10 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
             const int j = jj * KS + kp;
             // (one block per chunk: every chunk walked is inside K)
             const bool valid = KCB == 1 || ch * KCB + j < nb;
+            // one K phase: a block past K adds nothing, skipped (the test is the
+            // same in every lane); K-split terms of every block are summed
+            if constexpr (KS == 1)
+                if (!valid) continue;
             // block index into the codes and scales: of the chunk's slot, or of
             // the resident arrays (block 0 stands in for blocks past K)
             const int jr = C::AR ? (valid ? ch * KCB + j : 0) : j;
@@ -537,7 +541,10 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
                                 Mb = mfma16x16x32_acc(av, make_uint2(mb, mb), Mb);
                             }
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) S[r] += __mul24(sc.sc[u], D[r]);
+                            for (int r = 0; r < 4; ++r) {
+                                if constexpr (F::NU == 1) S[r] = D[r];  // Q8_0: the unit scale is 1
+                                else S[r] += __mul24(sc.sc[u], D[r]);
+                            }
                         }
                     }
                     // dx of output tokens 4 cl + r of this token tile (tokens
