@@ -324,6 +324,15 @@ __device__ inline void scales_k4_packed(uint32_t s0, uint32_t s1, uint32_t s2, u
     m[1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
 }
 
+// a * b + c on 24-bit signed operands (|a|, |b| < 2^23) as one v_mad_i32_i24:
+// written out, the compiler reassociates a sum of such products into separate
+// multiplies and adds
+__device__ inline int mad_i24(int a, int b, int c) {
+    int d;
+    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+
 __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
     const long av = (long)(((uint64_t)a.y << 32) | a.x);
     const long bv = (long)(((uint64_t)b.y << 32) | b.x);
@@ -804,7 +813,7 @@ __global__ __launch_bounds__(256 * RTM) void res_kernel(MatGroup grp, Q8KView x,
                 for (int u = 0; u < 8; ++u) {
                     const int su = int(__builtin_amdgcn_ubfe(scw[u >> 2], 8 * (u & 3), 8));
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) S[r] += __mul24(su, D[u][r]);
+                    for (int r = 0; r < 4; ++r) S[r] = mad_i24(su, D[u][r], S[r]);  // |D| <= 32 * 31 * 127
                 }
             }
 #pragma unroll
