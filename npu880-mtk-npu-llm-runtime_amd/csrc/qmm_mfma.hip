@@ -367,9 +367,14 @@ struct TileCfg {
     static constexpr int ROWS = 16 * WR * PR;
     static constexpr int TOK = TR * WT * PT;  // tokens resident per chunk
     static constexpr int wcr(int k) { return ((k * F::BB + 30) / 16) | 1; }  // odd: rows 4 banks apart
+    // AT: the codes come from the Q8_K tiles section, already in MFMA operand
+    // order (1 KB per 16-token tile, block and 64-value chunk; a lane's 16 B
+    // contiguous): one 16-B LDS read per operand, no bank conflicts, no row
+    // padding (folded formats with 16-token tiles streamed per chunk)
+    static constexpr bool AT = F::kSplit && !AR && TR == 16;
     static constexpr int acr(int k) { return k * F::QK / 16 + 1; }
     static constexpr int nwi(int k) { return (ROWS * wcr(k) + 63) / 64; }
-    static constexpr int nai(int k) { return AR ? 0 : (TOK * acr(k) + 63) / 64; }
+    static constexpr int nai(int k) { return AR ? 0 : AT ? (TOK / 16) * k * (F::QK / 64) : (TOK * acr(k) + 63) / 64; }
     static constexpr int ndi(int k) { return AR ? 0 : (k * TOK + 63) / 64; }
     // resident codes (rows of K / 16 + 1 units of 16 B) and scales ([block][token])
     static constexpr int AR_BYTES = AR ? (TOK * (KMAX / 16 + 1) + 63) / 64 * 1024 : 0;
@@ -420,7 +425,9 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     // dword, and a 2-B aligned format's last bytes may share one with the end)
     const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
                               (bl + uint32_t(rows_valid) * uint32_t(a.row_bytes) + 15u) & ~15u);
-    const v4i32 ra = buf_rsrc(x.qs, uint32_t(a.M) * uint32_t(K));
+    v4i32 ra;  // the codes: [M][K], or the tiles section of ceil(M / 16) * 16 tokens
+    if constexpr (C::AT) ra = buf_rsrc(x.qt, uint32_t((a.M + 15) & ~15) * uint32_t(K));
+    else ra = buf_rsrc(x.qs, uint32_t(a.M) * uint32_t(K));
     const v4i32 rd = buf_rsrc(x.d, uint32_t(a.M) * uint32_t(nb) * 4u);
     const uint32_t lds0 = lds_addr(lds);
 
@@ -435,9 +442,16 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     }
 #pragma unroll
     for (int s = 0; s < C::NAW; ++s) {
-        const int p = (s * 4 + wid) * 64 + lane;
-        const int tok = p / C::ACR, pc = p - tok * C::ACR;
-        ao[s] = tok < C::TOK ? uint32_t(m0 + tok) * uint32_t(K) + 16u * uint32_t(pc) : kFar;
+        if constexpr (C::AT) {  // transfer i: token tile i / 4 KCB, block (i / 4) mod KCB, chunk i mod 4
+            const int i = s * 4 + wid, tt = i / (4 * KCB), j = (i >> 2) % KCB, h = i & 3;
+            ao[s] = i < C::NAI ? ((uint32_t(m0 / 16 + tt) * uint32_t(nb) + uint32_t(j)) * 4u + uint32_t(h)) * 1024u +
+                                     16u * uint32_t(lane)
+                               : kFar;
+        } else {
+            const int p = (s * 4 + wid) * 64 + lane;
+            const int tok = p / C::ACR, pc = p - tok * C::ACR;
+            ao[s] = tok < C::TOK ? uint32_t(m0 + tok) * uint32_t(K) + 16u * uint32_t(pc) : kFar;
+        }
     }
 #pragma unroll
     for (int s = 0; s < C::NDW; ++s) {
@@ -450,7 +464,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
         const bool live = ch < nchunks;
         const uint32_t base = lds0 + uint32_t(sl * C::SLOT), dump = lds0 + uint32_t(C::OFF_DUMP);
         const uint32_t cw = uint32_t(ch) * uint32_t(KCB * F::BB);
-        const uint32_t ca = uint32_t(ch) * uint32_t(KCB * F::QK);
+        const uint32_t ca = uint32_t(ch) * uint32_t(KCB * (C::AT ? 4096 : F::QK));  // 4 KB per block and token tile
         const uint32_t cd = uint32_t(ch) * uint32_t(KCB) * 4u;
 #pragma unroll
         for (int s = 0; s < C::NWW; ++s) {
@@ -532,8 +546,13 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
                         int4v D1 = {0, 0, 0, 0}, D2 = {0, 0, 0, 0};
 #pragma unroll
                         for (int h = 0; h < 4; ++h) {
-                            const uint2 a0 = ld8(arow + 64 * h + 8 * cl), a1 = ld8(arow + 64 * h + 32 + 8 * cl);
-                            const uint4 av = make_uint4(a0.x, a0.y, a1.x, a1.y);
+                            uint4 av;
+                            if constexpr (C::AT) {
+                                av = ld16(as + (((pt * WT + wt) * KCB + j) * 4 + h) * 1024 + 16 * lane);
+                            } else {
+                                const uint2 a0 = ld8(arow + 64 * h + 8 * cl), a1 = ld8(arow + 64 * h + 32 + 8 * cl);
+                                av = make_uint4(a0.x, a0.y, a1.x, a1.y);
+                            }
                             D1 = mfma16x16x64(av, sb.b1[h], D1);
                             D2 = mfma16x16x64(av, sb.b2[h], D2);
                             if constexpr (F::kMin) Mb = mfma16x16x64(av, sb.bm[h], Mb);
@@ -1149,6 +1168,8 @@ static hipError_t launch_res(const MatArgs *tasks, int n, const Q8KView &x, hipS
 
 template <class C, class F>
 static hipError_t launch_tile_t(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    if constexpr (C::AT)
+        if (!x.qt) return hipErrorInvalidValue;  // the codes are read from the tiles section
     MatGroup g{};
     g.n = n;
     g.wg0[0] = 0;
@@ -1164,8 +1185,9 @@ static hipError_t launch_tile_t(const MatArgs *tasks, int n, const typename ActO
 template <class F>
 static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     const MatArgs &a = tasks[0];
-    // buffer offsets are 32-bit with kFar past every range
-    if (size_t(a.M) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
+    // buffer offsets are 32-bit with kFar past every range (the tiles section
+    // holds ceil(M / 16) * 16 tokens)
+    if (size_t((a.M + 15) & ~15) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
     using G = typename Folded<F>::T;
     // up to 32 tokens over K <= 3072: the resident-tile kernel
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
