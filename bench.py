@@ -458,9 +458,9 @@ def main():
         "tokens_per_s_equiv": round(value * 1e9 / DECODE_BYTES_PER_TOKEN, 1),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic(TRAFFIC_PROFILE),
-                     "kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, true, 6> (fused Q8_K quantizer)",
+                     "kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, true, 6, false> (fused Q8_K quantizer)",
                      "us_per_launch": round(ms * 1e3, 3), "algorithmic_bytes": step_bytes},
-        "gemv_prequantized": {"kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, false, 6> on Q8_K input", "us_per_launch": round(ms_k * 1e3, 3),
+        "gemv_prequantized": {"kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, false, 6, false> on Q8_K input", "us_per_launch": round(ms_k * 1e3, 3),
                               "algorithmic_bytes": kern_bytes, "gbs": round(ach_pre, 1)},
         "cache_resident_us_per_launch": round(ms_hot * 1e3, 3),
         "parity": parity,
