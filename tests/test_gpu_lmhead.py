@@ -126,3 +126,28 @@ def test_eval_rows_many(ctx, oracle):
     assert np.array_equal(ctx.d2h(bi, np.uint32, (1,)), ei)
     for b in (wb, idb, bv, bi, qb):
         ctx.free(b)
+
+
+def test_lm_head_nan_row(ctx, oracle):
+    """A row whose logit is NaN (a NaN scale in its first Q6_K block: d at
+    byte 208) at the position of the maximum, in a chunk tall enough for the
+    GEMV's fused argmax: never taken, as under the reference's strict `>`."""
+    N, K = 30000, 2560
+    say("lm head NaN row")
+    w, q, qb = _setup(ctx, oracle, TYPE_Q6_K, N, K, 1, seed=680)
+    rb = synth.row_bytes(TYPE_Q6_K, K)
+    lg_all, _, _ = oracle.lm_head_argmax(q, w, TYPE_Q6_K, N, 0, np.full(1, -1e30, np.float32), np.zeros(1, np.uint32))
+    top = int(np.argmax(lg_all[0]))
+    w[top * rb + 208:top * rb + 210] = [0x00, 0x7E]  # fp16 NaN
+    wb = ctx.weight_upload(w, TYPE_Q6_K, N, K)
+    bv = ctx.upload(np.full(1, -1e30, np.float32))
+    bi = ctx.upload(np.zeros(1, np.uint32))
+    ctx.lm_head_argmax(qb, None, 1, K, wb, TYPE_Q6_K, N, 0, None, bv, bi)
+    ctx.sync()
+    lg, ebv, ebi = oracle.lm_head_argmax(q, w, TYPE_Q6_K, N, 0, np.full(1, -1e30, np.float32), np.zeros(1, np.uint32))
+    assert np.isnan(lg[0, top]) and ebi[0] != top
+    got_v, got_i = ctx.d2h(bv, np.float32, (1,)), ctx.d2h(bi, np.uint32, (1,))
+    assert np.array_equal(got_v.view(np.uint32), ebv.view(np.uint32)), (got_v, ebv)
+    assert np.array_equal(got_i, ebi), (got_i, ebi)
+    for b in (wb, bv, bi, qb):
+        ctx.free(b)
