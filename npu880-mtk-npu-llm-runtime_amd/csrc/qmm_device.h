@@ -68,6 +68,7 @@ struct LdsAct {
     const int8_t *qs;
     const float *d;
     const int32_t *bs;
+    const int32_t *bs16;  // Q8_K: sums of 16 codes, [block][run order of the Q6_K lanes]
 };
 __host__ __device__ inline int lds_pad(int v) { return v + ((v >> 8) << 4); }
 

@@ -194,7 +194,7 @@ struct FmtQ6K4 {
     static constexpr int G = 4, BB = 210, QK = 256;
     static constexpr bool kStaged = true;
     struct Raw { uint4 a, b, h; uint2 s; uint32_t d; };
-    struct Act { uint4 x[4]; float dx; };
+    struct Act { uint4 x[4]; int4 xs; float dx; };  // xs: the lane's four 16-code sums
     // blk points into LDS, 2-B aligned. Every field lies a multiple of 8 B
     // from it, so one misalignment (0 or 2 B) serves all: aligned dword reads
     // (the last one read whatever the misalignment: at most 2 B past the
@@ -218,13 +218,15 @@ struct FmtQ6K4 {
     }
     __device__ static Act load_act(const LdsAct &x, int b, int k) {
         const int8_t *xb = x.qs + b * 272 + 128 * (k >> 1) + 16 * (k & 1);
-        return {{ld16(xb), ld16(xb + 32), ld16(xb + 64), ld16(xb + 96)}, x.d[b]};
+        return {{ld16(xb), ld16(xb + 32), ld16(xb + 64), ld16(xb + 96)},
+                *reinterpret_cast<const int4 *>(x.bs16 + 16 * b + 4 * k), x.d[b]};
     }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
         const uint32_t M4 = 0x0F0F0F0Fu;
         const uint32_t av[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, bv[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
         const uint32_t hv[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
-        int dot[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0};
+        int dot[4] = {0, 0, 0, 0};
+        const int xs[4] = {a.xs.x, a.xs.y, a.xs.z, a.xs.w};  // the runs' code sums, from the fill
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const uint32_t q[4] = {(av[w] & M4) | ((hv[w] & 0x03030303u) << 4),
@@ -238,7 +240,6 @@ struct FmtQ6K4 {
                                   : i == 2 ? (w == 0 ? a.x[2].x : w == 1 ? a.x[2].y : w == 2 ? a.x[2].z : a.x[2].w)
                                            : (w == 0 ? a.x[3].x : w == 1 ? a.x[3].y : w == 2 ? a.x[3].z : a.x[3].w);
                 dot[i] = sdot4(int(q[i]), int(xw), dot[i]);
-                xs[i] = sdot4(int(xw), 0x01010101, xs[i]);
             }
         }
         // sc[8hf + 2i + k % 2]: bytes k % 2, 2 + k % 2, 4 + k % 2, 6 + k % 2
@@ -322,7 +323,12 @@ __device__ inline void x_load(const float *__restrict__ x, int K, int c, XPre &p
 // Quantize the lane's 16 values of chunk c into the LDS row: Q8_K
 // (quantize_row_fp16_to_q8_k, E:925-990) or Q8_0 (E:1016-1064), after
 // rounding each value to fp16. `store` is false for clamped duplicates.
-template <bool Q80>
+// position of the 16-value group at offset o (a multiple of 16) of block b in
+// the bs16 row: lane k = 2 (o >> 7) + ((o >> 4) & 1) of a Q6_K block reads
+// its four runs (o >> 5) & 3 = 0..3 as one 16-B word at 16 b + 4 k
+__device__ inline int bs16_pos(int b, int o) { return 16 * b + 4 * (2 * (o >> 7) + ((o >> 4) & 1)) + ((o >> 5) & 3); }
+
+template <bool Q80, bool BS16 = false>
 __device__ inline void x_quant(const XPre &p, int c, int K, bool store, const LdsAct &a) {
     const int sub = threadIdx.x & 15;
     float h[16];
@@ -346,10 +352,12 @@ __device__ inline void x_quant(const XPre &p, int c, int K, bool store, const Ld
     q.z = quant4_rne(h[8], h[9], h[10], h[11], id, s2);
     q.w = quant4_rne(h[12], h[13], h[14], h[15], id, s3);
     int sum = s0 + s1 + s2 + s3;
+    const int sum16 = sum;
     sum += __builtin_amdgcn_mov_dpp(sum, 0xB1, 0xF, 0xF, false);  // the 32-value pair
     const int v0 = c * 256 + 16 * sub;
     store = store && v0 < K;
     if (store) {
+        if constexpr (BS16) const_cast<int32_t *>(a.bs16)[bs16_pos(c, 16 * sub)] = sum16;
         *reinterpret_cast<uint4 *>(const_cast<int8_t *>(a.qs) + lds_pad(v0)) = q;
         if ((sub & 1) == 0) {
             if constexpr (Q80) {
@@ -362,17 +370,17 @@ __device__ inline void x_quant(const XPre &p, int c, int K, bool store, const Ld
     }
 }
 
-template <bool Q80>
+template <bool Q80, bool BS16 = false>
 __device__ inline void x_fill(const XPre &p0, const float *__restrict__ x, int K, const LdsAct &a) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int nc = (K + 255) >> 8;
-    if (x_has(0, K)) x_quant<Q80>(p0, x_chunk(0, K), K, 4 * wid + (lane >> 4) < nc, a);
+    if (x_has(0, K)) x_quant<Q80, BS16>(p0, x_chunk(0, K), K, 4 * wid + (lane >> 4) < nc, a);
     for (int round = 1; 16 * round < nc; ++round) {
         if (!x_has(round, K)) break;
         XPre p;
         const int c = x_chunk(round, K);
         x_load(x, K, c, p);
-        x_quant<Q80>(p, c, K, 16 * round + 4 * wid + (lane >> 4) < nc, a);
+        x_quant<Q80, BS16>(p, c, K, 16 * round + 4 * wid + (lane >> 4) < nc, a);
     }
 }
 
@@ -396,7 +404,10 @@ __device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t
     }
 }
 
-template <bool Q80>
+__device__ inline int sum16_codes(uint4 q) {
+    return sdot4(int(q.w), 0x01010101, sdot4(int(q.z), 0x01010101, sdot4(int(q.y), 0x01010101, sdot4(int(q.x), 0x01010101, 0))));
+}
+template <bool Q80, bool BS16 = false>
 __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d, const int32_t *bs,
                                  int K, const LdsAct &a) {
     const int t = threadIdx.x;
@@ -404,11 +415,19 @@ __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d
     int8_t *lq = const_cast<int8_t *>(a.qs);
     float *ld = const_cast<float *>(a.d);
     int32_t *lb = const_cast<int32_t *>(a.bs);
+    int32_t *l16 = const_cast<int32_t *>(a.bs16);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (t + 256 * i < nq) *reinterpret_cast<uint4 *>(lq + lds_pad(16 * (t + 256 * i))) = p.q[i];
-    for (int i = t + 1024; i < nq; i += 256)
-        *reinterpret_cast<uint4 *>(lq + lds_pad(16 * i)) = ld16(qs + 16 * i);
+        if (t + 256 * i < nq) {
+            const int g = t + 256 * i;
+            *reinterpret_cast<uint4 *>(lq + lds_pad(16 * g)) = p.q[i];
+            if constexpr (BS16) l16[bs16_pos(g >> 4, 16 * (g & 15))] = sum16_codes(p.q[i]);
+        }
+    for (int i = t + 1024; i < nq; i += 256) {
+        const uint4 q = ld16(qs + 16 * i);
+        *reinterpret_cast<uint4 *>(lq + lds_pad(16 * i)) = q;
+        if constexpr (BS16) l16[bs16_pos(i >> 4, 16 * (i & 15))] = sum16_codes(q);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         if (t + 256 * i < nbs) lb[t + 256 * i] = p.bs[i];
@@ -421,13 +440,26 @@ __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d
 // ------------------------------------------------------------ the kernel
 constexpr int kGemvR = 4, kGemvU = 5;
 
-// LDS carve-up: padded codes | d | bsum32 (Q8_K only) | per-wave block
-// terms and a 64-float dump | per-wave weight stage (staged formats)
-__host__ __device__ inline size_t gemv_act_lds_bytes(bool q80, int K) {
+// LDS carve-up: padded codes | d | bsum32 (Q8_K only) | bs16 (Q8_K only,
+// 16-B aligned) | per-wave block terms and a 64-float dump | per-wave weight
+// stage (staged formats)
+__host__ __device__ inline size_t gemv_bs16_off(bool q80, int K) {
     const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
     const size_t nd = q80 ? size_t(K / 32) : size_t(K / 256);
     const size_t nbs = q80 ? 0 : size_t(K / 32);
     return (codes + 4 * nd + 4 * nbs + 15) & ~size_t(15);
+}
+__host__ __device__ inline size_t gemv_act_lds_bytes(bool q80, int K) {
+    return gemv_bs16_off(q80, K) + (q80 ? 0 : size_t(K / 16) * 4);
+}
+__device__ inline LdsAct gemv_act_view(uint8_t *lds, bool q80, int K) {
+    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
+    LdsAct act;
+    act.qs = reinterpret_cast<const int8_t *>(lds);
+    act.d = reinterpret_cast<const float *>(lds + codes);
+    act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
+    act.bs16 = reinterpret_cast<const int32_t *>(lds + gemv_bs16_off(q80, K));
+    return act;
 }
 template <class F, int U>
 __host__ __device__ constexpr int stage_chunks() {  // 16-B loads per lane per batch
@@ -469,11 +501,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     const uint8_t *span = a.w + size_t(nrows > 0 ? row0 : 0) * a.row_bytes;
     const int flast = max(nblk, 1) - 1;
 
-    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
-    LdsAct act;
-    act.qs = reinterpret_cast<const int8_t *>(lds);
-    act.d = reinterpret_cast<const float *>(lds + codes);
-    act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
+    const LdsAct act = gemv_act_view(lds, q80, K);
     const size_t act_bytes = gemv_act_lds_bytes(q80, K);
     const size_t terms_bytes = (size_t(4) * (R * nb + 64) * sizeof(float) + 15) & ~size_t(15);
     float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * (R * nb + 64);
@@ -521,8 +549,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     }
     __builtin_amdgcn_sched_barrier(0);
     // 3. activations into LDS while the weights are in flight
-    if constexpr (FUSED) x_fill<q80>(xp, x32, K, act);
-    else cpre_fill<q80>(cp, pq, pd, pb, K, act);
+    if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
+    else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     if constexpr (F::kStaged) stage_store();
     lds_barrier();
     // 4. block terms. b = f mod nb advances by SLOTS mod nb per wave step;
@@ -617,11 +645,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     const int K = a.K, nb = K / F::QK;
     const int ngroups = (a.N + R - 1) / R;
 
-    const size_t codes = (size_t(lds_pad(K)) + 15) & ~size_t(15);
-    LdsAct act;
-    act.qs = reinterpret_cast<const int8_t *>(lds);
-    act.d = reinterpret_cast<const float *>(lds + codes);
-    act.bs = reinterpret_cast<const int32_t *>(lds + codes + 4 * (q80 ? K / 32 : K / 256));
+    const LdsAct act = gemv_act_view(lds, q80, K);
     const size_t act_bytes = gemv_act_lds_bytes(q80, K);
     const size_t terms_bytes = (size_t(4) * (R * nb + 64) * sizeof(float) + 15) & ~size_t(15);
     float *contrib = reinterpret_cast<float *>(lds + act_bytes) + wid * (R * nb + 64);
@@ -662,8 +686,8 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     stage_load(min(gw, ngroups - 1));
     __builtin_amdgcn_sched_barrier(0);
     // 2. the activations into LDS, once
-    if constexpr (FUSED) x_fill<q80>(xp, x32, K, act);
-    else cpre_fill<q80>(cp, pq, pd, pb, K, act);
+    if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
+    else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     lds_barrier();
     // 3. groups
     const int adv = SLOTS % nb;
