@@ -21,6 +21,11 @@
  *    block, blocks accumulated in order (eval_single_lm_row_dot
  *    E:10986-11105, sdot_row_q*_batch E:3109-3408); outputs are the fp32
  *    sums the reference casts to fp16 at E:3582-3613.
+ *  - F32 / F16 weight rows (sdot_row_f32_batch / _f16_batch, E:3410-3440)
+ *    are dotted with the fp16-rounded input in fp32; their sums are added in
+ *    a fixed parallel order, not the reference's row order, so they match it
+ *    to the stated tolerance (max|d| / max|ref| <= 1e-3), not bit for bit.
+ *    Their K must be a multiple of 32 and their rows 16-B aligned.
  */
 #ifndef QMM_HIP_H
 #define QMM_HIP_H
@@ -43,6 +48,8 @@ extern "C" {
 #define QMM_ENOTFOUND 7  /* no GGUF tensor of that name */
 
 /* ggml type ids (E:115-120) */
+#define QMM_TYPE_F32 0
+#define QMM_TYPE_F16 1
 #define QMM_TYPE_Q8_0 8
 #define QMM_TYPE_Q4_K 12
 #define QMM_TYPE_Q5_K 13
@@ -77,7 +84,11 @@ int qmm_set_stream(qmm_context *ctx, void *hip_stream);
 void *qmm_get_stream(qmm_context *ctx);
 int qmm_synchronize(qmm_context *ctx);
 /* Pre-size the internal activation buffers for M x K dispatches so that
- * later dispatches up to that size allocate nothing (graph capture). */
+ * later dispatches up to that size allocate nothing (graph capture: a
+ * capture that would need a larger buffer fails with QMM_ENOMEM). While
+ * instantiated graphs are alive, a call that needs a larger buffer gets a
+ * new one and the old one is kept — the graphs go on using it — until the
+ * last graph is destroyed (qmm_graph_destroy) or the context is. */
 int qmm_reserve(qmm_context *ctx, int max_M, int max_K);
 const char *qmm_status_string(int status);
 const char *qmm_last_error(const qmm_context *ctx);
@@ -97,12 +108,16 @@ size_t qmm_row_bytes(uint32_t type, int64_t cols);
  * t (tokens 16t..16t+15), block j and 64-value chunk h, 1 KB at
  * ((t * K/256 + j) * 4 + h) * 1024 whose 16-B slot 16c + n holds token
  * 16t + n's codes at block offsets 64h + 8c..+7 then 64h + 32 + 8c..+7.
+ * At qmm_q8k_h_offset: the fp16 values the codes were quantized from,
+ * [M][K] (the reference keeps them as x_fp16 beside its quantized input,
+ * E:879-886, and dots its F32 / F16 rows with them, E:3410-3440).
  * Every producer (qmm_quantize_q8k, qmm_swiglu_q8k, qmm_rmsnorm_q8k)
- * writes all four sections. */
+ * writes all five sections. */
 size_t qmm_q8k_bytes(int M, int K);
 size_t qmm_q8k_d_offset(int M, int K);
 size_t qmm_q8k_bsum_offset(int M, int K);
 size_t qmm_q8k_tile_offset(int M, int K);
+size_t qmm_q8k_h_offset(int M, int K);
 /* Q8_0 activations (BlockQ8_0_Fast E:874-877): qs int8[M][K] at 0,
  * d f32[M][K/32] at qmm_q8_0_d_offset. */
 size_t qmm_q8_0_bytes(int M, int K);
@@ -154,15 +169,52 @@ int qmm_lm_head_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M
 /* Indexed rows (the pre-evaluated candidate / end-of-text rows, E:11141-11148,
  * and the extended-script row lists, exec_cyrillic_lm_work_item E:9473-9579):
  * the fp32 dots of rows row_ids[0..n_ids) (device array) of the tensor at
- * w_tensor, and the running argmax over them in list order, fp32 values,
- * strictly greater; best_id receives row ids. vals_out [M][n_ids] may be NULL. */
+ * w_tensor (tensor_rows rows), and the running argmax over them in list
+ * order, fp32 values, strictly greater; best_id receives row ids. An id at
+ * or past tensor_rows is never read: its value is -1e30 (E:11150), so it
+ * never replaces a seed of -1e30. vals_out [M][n_ids] may be NULL. */
 int qmm_eval_rows_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
-                         const void *w_tensor, uint32_t type, const uint32_t *row_ids, int n_ids,
-                         float *vals_out, float *best_val, uint32_t *best_id);
+                         const void *w_tensor, int64_t tensor_rows, uint32_t type,
+                         const uint32_t *row_ids, int n_ids, float *vals_out, float *best_val,
+                         uint32_t *best_id);
+
+/* The chunked vocabulary scan of run_final_norm_and_lm_head_batch_sdot
+ * (E:11107-11262) after its RMSNorm, on the device with no host round trip
+ * between chunks. */
+typedef struct {
+    int chunk_rows;          /* rows per vocabulary chunk (the engine's lm_chunk_rows) */
+    const float *thresholds; /* host array: the scan stops after chunk c < n_thresholds when every
+                                active position's best is >= thresholds[c] (chunk_thresh,
+                                E:11245-11256); NULL / 0 = no early exit */
+    int n_thresholds;
+    int first_checkpoint;    /* first chunk that may end the scan: 0, or 6 where all 7 chunks are
+                                required (g_require_full_7chunks, E:11254) */
+    float prune_margin;      /* speculative pruning margin (1e-3f, E:11208) */
+} qmm_lm_scan_params;
+/* best_val / best_id [M] (device) are seeded with -1e30 / 0 (E:11139-11140);
+ * then every position evaluates the rows pre_ids[0..n_pre) (device; the
+ * end-of-text rows, E:11143-11146) and, when draft_ids (device [M]) is given,
+ * position p < M - 1 its draft candidate draft_ids[p + 1] (-1e30 past the
+ * vocabulary, E:11147-11153), fp32 values, strictly greater. Then the
+ * vocab_rows rows are scanned in chunks (fp16-rounded logits, strict >,
+ * E:11158-11183); after each chunk the first position p whose best is not
+ * its draft candidate and beats the candidate's logit by more than the
+ * margin ends the active batch at p + 1 (E:11203-11209: later positions are
+ * no longer updated), and at a checkpoint the scan stops when every active
+ * position's best reaches the chunk's threshold. A chunk after the stop
+ * reads no weights. scan_state (device int32[4]) receives: chunks read,
+ * active positions, 1 if the scan stopped early, 0. The script-specific
+ * extended rows (E:11194-11240) are the caller's: qmm_eval_rows_argmax. */
+int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,
+                     const void *w_lm, uint32_t type, int vocab_rows,
+                     const qmm_lm_scan_params *params, const uint32_t *pre_ids, int n_pre,
+                     const uint32_t *draft_ids, float *best_val, uint32_t *best_id,
+                     int32_t *scan_state);
 
 /* -------------------------------------------------------------- dequant */
 /* dequant_contiguous_fast (E:3856-3902): rows x cols packed blocks -> fp16
- * bits [rows][cols] (for validation; not on the matmul path). */
+ * bits [rows][cols] (for validation; not on the matmul path). F16 rows are
+ * copied, F32 values rounded to fp16 (E:3857-3860, E:3876-3879). */
 int qmm_dequantize_f16(qmm_context *ctx, const void *w_blocks, uint32_t type, int64_t rows,
                        int64_t cols, uint16_t *dst);
 
@@ -174,7 +226,8 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K,
                             qmm_matrix_task *tasks, int n_tasks);
 /* The prequantized form (the engine's g_sdot_input_q8k_prequantized flag,
  * E:4186, E:4207-4208, made explicit): q8k / q80 are device buffers in the
- * layouts above; either may be NULL when no task needs it. */
+ * layouts above; either may be NULL when no task needs it (F32 / F16 tasks
+ * read the fp16 section of q8k). */
 int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80,
                                          int M, int K, qmm_matrix_task *tasks, int n_tasks);
 
@@ -184,7 +237,9 @@ int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, cons
 int qmm_graph_begin(qmm_context *ctx);
 int qmm_graph_end(qmm_context *ctx, void **graph_exec);
 int qmm_graph_launch(qmm_context *ctx, void *graph_exec);
-int qmm_graph_destroy(void *graph_exec);
+/* Waits for the context's stream, then destroys the graph; buffers the
+ * context replaced while graphs were alive are freed with the last one. */
+int qmm_graph_destroy(qmm_context *ctx, void *graph_exec);
 /* HIP events on the context stream: begin records, end records and waits,
  * returning the elapsed milliseconds. */
 int qmm_timer_begin(qmm_context *ctx);

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/qmm_hip.h"
 #include "qmm_device.h"
@@ -28,6 +29,12 @@ struct qmm_context {
     void *lm = nullptr;   // LM-head epilogue scratch: logits | argmax slices | gathered rows
     size_t lm_cap = 0;
     bool capturing = false;
+    // Instantiated graphs still alive (qmm_graph_end .. qmm_graph_destroy):
+    // while any is, a buffer that must grow is replaced but not freed — the
+    // graphs keep reading and writing the old one — and is freed once the
+    // last of them is destroyed.
+    int live_graphs = 0;
+    std::vector<void *> retired;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::string err;
 };
@@ -56,112 +63,67 @@ int use_device(qmm_context *ctx) {
 }
 
 bool supported(uint32_t t) {
-    return t == qmm::kQ8_0 || t == qmm::kQ4_K || t == qmm::kQ5_K || t == qmm::kQ6_K;
+    return t == qmm::kF32 || t == qmm::kF16 || t == qmm::kQ8_0 || t == qmm::kQ4_K || t == qmm::kQ5_K ||
+           t == qmm::kQ6_K;
 }
-int block_values(uint32_t t) { return t == qmm::kQ8_0 ? 32 : 256; }
+bool is_float(uint32_t t) { return t == qmm::kF32 || t == qmm::kF16; }
+// values per block; F32 / F16 rows are read in 16-B pieces of 8 fp16 / 4
+// fp32 values and 32-value MFMA steps, so their K must be a multiple of 32
+int block_values(uint32_t t) { return t == qmm::kQ8_0 ? 32 : is_float(t) ? 32 : 256; }
 
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
-int ensure_act(qmm_context *ctx, size_t bytes) {
-    if (bytes <= ctx->act_cap) return QMM_OK;
+// Grow one of the context's device buffers to `bytes`. During a capture
+// nothing may be allocated; while instantiated graphs hold the old buffer it
+// is retired (kept) instead of freed.
+int grow(qmm_context *ctx, void *&buf, size_t &cap, size_t bytes, const char *what) {
+    if (bytes <= cap) return QMM_OK;
     if (ctx->capturing)
-        return fail(ctx, QMM_ENOMEM,
-                    "activation buffers too small during graph capture: call qmm_reserve first");
-    if (ctx->act) {
-        hipError_t e = hipFree(ctx->act);
-        ctx->act = nullptr;
-        ctx->act_cap = 0;
-        if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
+        return fail(ctx, QMM_ENOMEM, std::string(what) +
+                                         " too small during graph capture: size it before capturing (qmm_reserve)");
+    if (buf) {
+        if (ctx->live_graphs > 0) {
+            ctx->retired.push_back(buf);
+        } else {
+            (void)hipStreamSynchronize(ctx->stream);
+            hipError_t e = hipFree(buf);
+            if (e != hipSuccess) {
+                buf = nullptr;
+                cap = 0;
+                return hip_fail(ctx, e, "hipFree");
+            }
+        }
+        buf = nullptr;
+        cap = 0;
     }
-    hipError_t e = hipMalloc(&ctx->act, bytes);
+    hipError_t e = hipMalloc(&buf, bytes);
     if (e != hipSuccess) {
-        ctx->act = nullptr;
+        buf = nullptr;
         (void)hipGetLastError();
-        return fail(ctx, QMM_ENOMEM, "hipMalloc of activation buffers failed");
+        return fail(ctx, QMM_ENOMEM, std::string("hipMalloc of ") + what + " failed");
     }
-    ctx->act_cap = bytes;
+    cap = bytes;
     return QMM_OK;
 }
 
-int ensure_lm(qmm_context *ctx, size_t bytes) {
-    if (bytes <= ctx->lm_cap) return QMM_OK;
-    if (ctx->capturing)
-        return fail(ctx, QMM_ENOMEM, "LM-head scratch too small during graph capture: run once before capturing");
-    if (ctx->lm) {
-        (void)hipStreamSynchronize(ctx->stream);
-        hipError_t e = hipFree(ctx->lm);
-        ctx->lm = nullptr;
-        ctx->lm_cap = 0;
-        if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
-    }
-    hipError_t e = hipMalloc(&ctx->lm, bytes);
-    if (e != hipSuccess) {
-        ctx->lm = nullptr;
-        (void)hipGetLastError();
-        return fail(ctx, QMM_ENOMEM, "hipMalloc of LM-head scratch failed");
-    }
-    ctx->lm_cap = bytes;
-    return QMM_OK;
+int ensure_act(qmm_context *ctx, size_t bytes) {
+    return grow(ctx, ctx->act, ctx->act_cap, bytes, "activation buffers");
+}
+
+int ensure_lm(qmm_context *ctx, size_t bytes) { return grow(ctx, ctx->lm, ctx->lm_cap, bytes, "LM-head scratch"); }
+
+void free_retired(qmm_context *ctx) {
+    if (ctx->retired.empty()) return;
+    (void)hipStreamSynchronize(ctx->stream);
+    for (void *p : ctx->retired) (void)hipFree(p);
+    ctx->retired.clear();
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-// the LM-head epilogue: rows of one tensor (contiguous, or gathered by id)
-// on prequantized activations, then the running argmax update
-int gemv_argmax_fused(qmm_context *ctx, const void *q8k, const void *q80, int K, qmm_matrix_task *t,
-                      const uint32_t *ids, uint32_t row_base, bool round16, void *part, float *best_val,
-                      uint32_t *best_id, bool *done);
-
-int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w, uint32_t type,
-              int rows, uint32_t row_base, const uint32_t *ids, float *logits_out, float *best_val,
-              uint32_t *best_id) {
-    if (!ctx) return QMM_EINVAL;
-    if (!w || !best_val || !best_id || M <= 0 || K <= 0 || rows <= 0)
-        return fail(ctx, QMM_EINVAL, "bad LM-head arguments");
-    if (!supported(type)) return fail(ctx, QMM_ETYPE, "unsupported ggml type");
-    if (!aligned(best_val, 4) || !aligned(best_id, 4)) return fail(ctx, QMM_EALIGN, "best_val/best_id must be 4-B aligned");
-    const size_t rb = qmm_row_bytes(type, K);
-    const size_t logit_b = logits_out ? 0 : align256(size_t(M) * rows * 4);
-    // partials: per 1024-row slice, or (M = 1) per workgroup of the fused grid
-    const size_t part_b = align256(std::max(qmm::argmax_scratch_bytes(M, rows),
-                                            M == 1 ? size_t(qmm::kMaxArgmaxParts) * sizeof(qmm::Best) : size_t(0)));
-    const size_t gather_b = ids ? align256(size_t(rows) * rb) : 0;
-    int rc = use_device(ctx);
-    if (rc) return rc;
-    if ((rc = ensure_lm(ctx, logit_b + part_b + gather_b))) return rc;
-    uint8_t *scr = static_cast<uint8_t *>(ctx->lm);
-    float *logits = logits_out ? logits_out : reinterpret_cast<float *>(scr);
-    void *part = scr + logit_b;
-    const void *wrows = w;
-    if (ids) {
-        uint8_t *g = scr + logit_b + part_b;
-        hipError_t e = qmm::launch_gather_rows(static_cast<const uint8_t *>(w), rb, ids, rows, g, ctx->stream);
-        if (e != hipSuccess) return hip_fail(ctx, e, "row gather launch");
-        wrows = g;
-    }
-    qmm_matrix_task t{};
-    t.w_base = wrows;
-    t.type = type;
-    t.row_bytes = rb;
-    t.dst = logits;
-    t.dst_stride = size_t(rows);
-    t.residual = nullptr;
-    t.res_stride = 0;
-    t.rows = rows;
-    t.cols = K;
-    if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
-        bool done = false;
-        rc = gemv_argmax_fused(ctx, q8k, q80, K, &t, ids, row_base, ids == nullptr, part, best_val, best_id, &done);
-        if (rc || done) return rc;
-    }
-    rc = qmm_gemm_multi_dispatch_prequantized(ctx, q8k, q80, M, K, &t, 1);
-    if (rc) return rc;
-    hipError_t e = qmm::launch_argmax(logits, M, rows, size_t(rows), /*round16=*/ids == nullptr, ids, row_base,
-                                      best_val, best_id, part, ctx->stream);
-    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "argmax launch");
-}
-
 // Validate the task list against (M, K) and assign start_row.
+// need_q8k: a K-quant task, or an F32 / F16 task (they read the fp16
+// section of the Q8_K buffer when M >= 2 or the input is prequantized)
 int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_tasks,
                 bool *need_q8k, bool *need_q80) {
     if (M <= 0 || K <= 0) return fail(ctx, QMM_EINVAL, "M and K must be positive");
@@ -183,11 +145,11 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
             if (!T.w_base || !T.dst) return fail(ctx, QMM_EINVAL, "task " + std::to_string(t) + ": null weight or dst");
             if (M > 1 && T.dst_stride < size_t(T.rows)) return fail(ctx, QMM_EINVAL, "task " + std::to_string(t) + ": dst_stride < rows");
             if (T.residual && M > 1 && T.res_stride < size_t(T.rows)) return fail(ctx, QMM_EINVAL, "task " + std::to_string(t) + ": res_stride < rows");
-            const uintptr_t wa = (T.type == qmm::kQ4_K || T.type == qmm::kQ5_K) ? 16 : 2;
+            const uintptr_t wa = (T.type == qmm::kQ4_K || T.type == qmm::kQ5_K || is_float(T.type)) ? 16 : 2;
             if (!aligned(T.w_base, wa)) return fail(ctx, QMM_EALIGN, "task " + std::to_string(t) + ": weight base misaligned for its format");
             if (!aligned(T.dst, 4) || (T.residual && !aligned(T.residual, 4))) return fail(ctx, QMM_EALIGN, "task " + std::to_string(t) + ": dst/residual not 4-B aligned");
         }
-        if (M == 1 && qmm::gemv_lds_bytes(T.type, K) > 65536)
+        if (M == 1 && qmm::gemv_mixed_lds_bytes(T.type, K) > 65536)
             return fail(ctx, QMM_ESHAPE, "task " + std::to_string(t) + ": K too large for the batch-1 kernel");
         if (T.type == qmm::kQ8_0) *need_q80 = true;
         else *need_q8k = true;
@@ -200,13 +162,14 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
 // Kernel views of prequantized activation buffers (a null buffer gives a
 // null view).
 void act_views(const void *q8k, const void *q80, int M, int K, qmm::Q8KView &xk, qmm::Q80View &x0) {
-    xk = {nullptr, nullptr, nullptr, nullptr};
+    xk = {nullptr, nullptr, nullptr, nullptr, nullptr};
     x0 = {nullptr, nullptr};
     if (q8k) {
         const qmm::Q8KLayout L(M, K);
         const uint8_t *b = static_cast<const uint8_t *>(q8k);
         xk = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off),
-              reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off)};
+              reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off),
+              reinterpret_cast<const uint16_t *>(b + L.h_off)};
     }
     if (q80) {
         const qmm::Q80Layout L(M, K);
@@ -215,15 +178,52 @@ void act_views(const void *q8k, const void *q80, int M, int K, qmm::Q8KView &xk,
     }
 }
 
+qmm::MatArgs mat_args(const qmm_matrix_task &T, int M, int K, const int32_t *scan = nullptr) {
+    qmm::MatArgs a;
+    a.w = static_cast<const uint8_t *>(T.w_base);
+    a.type = T.type;
+    a.row_bytes = T.row_bytes;
+    a.N = T.rows;
+    a.K = K;
+    a.M = M;
+    a.y = T.dst;
+    a.ldy = M > 1 ? T.dst_stride : size_t(T.rows);
+    a.res = T.residual;
+    a.ldr = M > 1 ? T.res_stride : size_t(T.rows);
+    a.scan = scan;
+    return a;
+}
+
 // x32 != nullptr (M = 1 only): the GEMV kernels quantize x themselves.
+// Launches: tasks of one type go together (up to kMaxGroup per launch, in
+// order of first appearance); a group of several types — the engine's
+// {qkv, gate, alpha, beta} and {q, k, v} groups (E:7954-7959, E:8110-8114) —
+// runs as one launch whose workgroups each take their own task's format,
+// where that launch applies (M = 1 always; 2 <= M <= 64 with K <= 3072 and
+// no Q8_0 task). Outputs are disjoint, so grouping changes no result.
 int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q80, int M, int K,
-              const qmm_matrix_task *tasks, int n_tasks) {
+              const qmm_matrix_task *tasks, int n_tasks, const int32_t *scan = nullptr) {
     qmm::Q8KView xk;
     qmm::Q80View x0;
     act_views(q8k, q80, M, K, xk, x0);
-    // tasks of one type run as one launch (up to kMaxGroup per launch), in
-    // order of first appearance; outputs are disjoint, so grouping changes
-    // no result
+    int nlive = 0;
+    bool mixed = false;
+    for (int t = 0; t < n_tasks; ++t) {
+        if (tasks[t].rows == 0) continue;
+        ++nlive;
+        for (int u = 0; u < t; ++u)
+            if (tasks[u].rows > 0 && tasks[u].type != tasks[t].type) mixed = true;
+    }
+    if (mixed && nlive <= qmm::kMaxGroup) {
+        qmm::MatArgs group[qmm::kMaxGroup];
+        int n = 0;
+        for (int t = 0; t < n_tasks; ++t)
+            if (tasks[t].rows > 0) group[n++] = mat_args(tasks[t], M, K, scan);
+        const hipError_t e = (M == 1) ? qmm::launch_gemv_mixed(group, n, x32, xk, x0, ctx->stream)
+                                      : qmm::launch_mfma_mixed(group, n, xk, ctx->stream);
+        if (e == hipSuccess) return QMM_OK;
+        if (e != hipErrorNotSupported) return hip_fail(ctx, e, "matmul launch");
+    }
     bool done[256] = {};
     for (int t0 = 0; t0 < n_tasks; ++t0) {
         if (done[t0] || tasks[t0].rows == 0) continue;
@@ -233,16 +233,7 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
             const qmm_matrix_task &T = tasks[t];
             if (done[t] || T.rows == 0 || T.type != tasks[t0].type) continue;
             done[t] = true;
-            qmm::MatArgs &a = group[n++];
-            a.w = static_cast<const uint8_t *>(T.w_base);
-            a.row_bytes = T.row_bytes;
-            a.N = T.rows;
-            a.K = K;
-            a.M = M;
-            a.y = T.dst;
-            a.ldy = M > 1 ? T.dst_stride : size_t(T.rows);
-            a.res = T.residual;
-            a.ldr = M > 1 ? T.res_stride : size_t(T.rows);
+            group[n++] = mat_args(T, M, K, scan);
             if (n == qmm::kMaxGroup) break;
         }
         const hipError_t e = (M == 1) ? qmm::launch_gemv(tasks[t0].type, group, n, x32, xk, x0, ctx->stream)
@@ -252,41 +243,119 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
     return QMM_OK;
 }
 
-// M = 1 LM head: the prequantized dispatch's checks, then the GEMV with the
-// running argmax fused and the final combine. *done stays false (nothing
-// launched) where the fused grid does not apply.
-int gemv_argmax_fused(qmm_context *ctx, const void *q8k, const void *q80, int K, qmm_matrix_task *t,
-                      const uint32_t *ids, uint32_t row_base, bool round16, void *part, float *best_val,
-                      uint32_t *best_id, bool *done) {
-    *done = false;
-    bool need_q8k, need_q80;
-    int rc = check_tasks(ctx, 1, K, t, 1, &need_q8k, &need_q80);
-    if (rc) return rc;
-    if (need_q8k && !q8k) return fail(ctx, QMM_EINVAL, "K-quant task without Q8_K activations");
+// Checks of a prequantized input for a validated task list.
+int check_pre(qmm_context *ctx, const void *q8k, const void *q80, bool need_q8k, bool need_q80) {
+    if (need_q8k && !q8k) return fail(ctx, QMM_EINVAL, "K-quant or F32/F16 task without Q8_K activations");
     if (need_q80 && !q80) return fail(ctx, QMM_EINVAL, "Q8_0 task without Q8_0 activations");
     if ((q8k && !aligned(q8k, 16)) || (q80 && !aligned(q80, 16)))
         return fail(ctx, QMM_EALIGN, "activation buffers must be 16-B aligned");
-    qmm::Q8KView xk;  // (the caller has made the context's device current)
-    qmm::Q80View x0;
-    act_views(need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, 1, K, xk, x0);
-    qmm::MatArgs a;
-    a.w = static_cast<const uint8_t *>(t->w_base);
-    a.row_bytes = t->row_bytes;
-    a.N = t->rows;
-    a.K = K;
-    a.M = 1;
-    a.y = t->dst;
-    a.ldy = size_t(t->rows);
-    a.res = nullptr;
-    a.ldr = size_t(t->rows);
-    int nparts = 0;
-    hipError_t e = qmm::launch_gemv_argmax(t->type, a, xk, x0, round16, part, &nparts, ctx->stream);
-    if (e == hipErrorNotSupported) return QMM_OK;
-    if (e != hipSuccess) return hip_fail(ctx, e, "GEMV + argmax launch");
-    e = qmm::launch_argmax_final(part, nparts, ids, row_base, best_val, best_id, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "argmax launch");
-    *done = true;
     return QMM_OK;
+}
+
+// LM-head scratch of one call: logits (unless the caller takes them) |
+// argmax partials (per 1024-row slice, or at M = 1 per workgroup of the
+// fused grid) | gathered rows (indexed form)
+struct LmScratch {
+    size_t logit_b, part_b, gather_b;
+    size_t total() const { return logit_b + part_b + gather_b; }
+};
+LmScratch lm_scratch(int M, int rows, size_t row_bytes, bool own_logits, bool gathered) {
+    LmScratch L;
+    L.logit_b = own_logits ? 0 : align256(size_t(M) * rows * 4);
+    L.part_b = align256(std::max(qmm::argmax_scratch_bytes(M, rows),
+                                 M == 1 ? size_t(qmm::kMaxArgmaxParts) * sizeof(qmm::Best) : size_t(0)));
+    L.gather_b = gathered ? align256(size_t(rows) * row_bytes) : 0;
+    return L;
+}
+
+// The task of `rows` rows of one tensor (contiguous from w, or gathered by
+// id) on M prequantized activation rows, validated before anything is
+// launched.
+int lm_task(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w, uint32_t type, int rows,
+            float *dst, qmm_matrix_task &t) {
+    if (!w || M <= 0 || K <= 0 || rows <= 0) return fail(ctx, QMM_EINVAL, "bad LM-head arguments");
+    if (!supported(type)) return fail(ctx, QMM_ETYPE, "unsupported ggml type");
+    t = qmm_matrix_task{};
+    t.w_base = w;
+    t.type = type;
+    t.row_bytes = qmm_row_bytes(type, K);
+    t.dst = dst ? dst : reinterpret_cast<float *>(uintptr_t(256));  // (placeholder until the scratch exists)
+    t.dst_stride = size_t(rows);
+    t.rows = rows;
+    t.cols = K;
+    bool need_q8k, need_q80;
+    int rc = check_tasks(ctx, M, K, &t, 1, &need_q8k, &need_q80);
+    if (rc) return rc;
+    return check_pre(ctx, q8k, q80, need_q8k, need_q80);
+}
+
+// One chunk or row list through the LM-head epilogue into (best_val,
+// best_id): ids != NULL gathers rows ids[0..rows) of the tensor at w (ids at
+// or past id_limit are never read and count as -1e30, E:11150); else rows
+// [row_base, row_base + rows) start at w. scr: this call's scratch (laid out
+// by lm_scratch); scan: a scan's state or NULL. Arguments are validated.
+int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, qmm_matrix_task t,
+                  uint32_t row_base, const uint32_t *ids, uint32_t id_limit, float *logits_out, float *best_val,
+                  uint32_t *best_id, uint8_t *scr, int32_t *scan, const qmm::ScanStep *step) {
+    const int rows = t.rows;
+    const LmScratch L = lm_scratch(M, rows, t.row_bytes, logits_out != nullptr, ids != nullptr);
+    float *logits = logits_out ? logits_out : reinterpret_cast<float *>(scr);
+    void *part = scr + L.logit_b;
+    hipError_t e;
+    if (ids) {
+        uint8_t *g = scr + L.logit_b + L.part_b;
+        e = qmm::launch_gather_rows(static_cast<const uint8_t *>(t.w_base), t.row_bytes, ids, id_limit, rows, g, scan,
+                                    ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "row gather launch");
+        t.w_base = g;
+    }
+    t.dst = logits;
+    qmm::Q8KView xk;
+    qmm::Q80View x0;
+    act_views(q8k, q80, M, K, xk, x0);
+    const bool round16 = ids == nullptr;  // chunk scans compare fp16 logits (E:11175), indexed rows fp32
+    if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
+        int nparts = 0;
+        e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, scan), xk, x0, round16, ids, id_limit, part, &nparts,
+                                    ctx->stream);
+        if (e == hipSuccess) {
+            e = step ? qmm::launch_scan_final(part, nparts, row_base, best_val, best_id, step->cand, step->draft,
+                                              step->margin, step->thresh, step->checkpoint, step->c, scan, ctx->stream)
+                     : qmm::launch_argmax_final(part, nparts, ids, row_base, best_val, best_id, scan, ctx->stream);
+            return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "argmax launch");
+        }
+        if (e != hipErrorNotSupported) return hip_fail(ctx, e, "GEMV + argmax launch");
+    }
+    int rc = run_tasks(ctx, nullptr, q8k, q80, M, K, &t, 1, scan);
+    if (rc) return rc;
+    if (step) {
+        e = qmm::launch_argmax_partials(logits, M, rows, size_t(rows), part, scan, ctx->stream);
+        if (e == hipSuccess)
+            e = qmm::launch_scan_final(part, qmm::argmax_slices(rows), row_base, best_val, best_id, step->cand,
+                                       step->draft, step->margin, step->thresh, step->checkpoint, step->c, scan,
+                                       ctx->stream);
+    } else {
+        e = qmm::launch_argmax(logits, M, rows, size_t(rows), round16, ids, id_limit, row_base, best_val, best_id, part,
+                               scan, ctx->stream);
+    }
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "argmax launch");
+}
+
+int lm_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w, uint32_t type,
+              int rows, uint32_t row_base, const uint32_t *ids, uint32_t id_limit, float *logits_out, float *best_val,
+              uint32_t *best_id) {
+    if (!ctx) return QMM_EINVAL;
+    if (!best_val || !best_id) return fail(ctx, QMM_EINVAL, "bad LM-head arguments");
+    if (!aligned(best_val, 4) || !aligned(best_id, 4) || (logits_out && !aligned(logits_out, 4)))
+        return fail(ctx, QMM_EALIGN, "best_val/best_id/logits must be 4-B aligned");
+    qmm_matrix_task t;
+    int rc = lm_task(ctx, q8k, q80, M, K, w, type, rows, logits_out, t);
+    if (rc) return rc;
+    if ((rc = use_device(ctx))) return rc;
+    const LmScratch L = lm_scratch(M, rows, t.row_bytes, logits_out != nullptr, ids != nullptr);
+    if ((rc = ensure_lm(ctx, L.total()))) return rc;
+    return lm_argmax_run(ctx, q8k, q80, M, K, t, row_base, ids, id_limit, logits_out, best_val, best_id,
+                         static_cast<uint8_t *>(ctx->lm), nullptr, nullptr);
 }
 
 }  // namespace
@@ -312,6 +381,8 @@ const char *qmm_last_error(const qmm_context *ctx) { return ctx ? ctx->err.c_str
 size_t qmm_row_bytes(uint32_t type, int64_t cols) {
     if (!supported(type) || cols <= 0 || cols % block_values(type)) return 0;
     switch (type) {
+        case qmm::kF32: return size_t(cols) * 4;
+        case qmm::kF16: return size_t(cols) * 2;
         case qmm::kQ8_0: return size_t(cols / 32) * 34;
         case qmm::kQ4_K: return size_t(cols / 256) * 144;
         case qmm::kQ5_K: return size_t(cols / 256) * 176;
@@ -324,6 +395,7 @@ size_t qmm_q8k_bytes(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M,
 size_t qmm_q8k_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).d_off : 0; }
 size_t qmm_q8k_bsum_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).bs_off : 0; }
 size_t qmm_q8k_tile_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).tile_off : 0; }
+size_t qmm_q8k_h_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).h_off : 0; }
 size_t qmm_q8_0_bytes(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).total : 0; }
 size_t qmm_q8_0_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).d_off : 0; }
 
@@ -357,6 +429,7 @@ int qmm_destroy(qmm_context *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->lm) (void)hipFree(ctx->lm);
+    for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -561,10 +634,7 @@ int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, cons
     bool need_q8k, need_q80;
     int rc = check_tasks(ctx, M, K, tasks, n_tasks, &need_q8k, &need_q80);
     if (rc) return rc;
-    if (need_q8k && !q8k) return fail(ctx, QMM_EINVAL, "K-quant task without Q8_K activations");
-    if (need_q80 && !q80) return fail(ctx, QMM_EINVAL, "Q8_0 task without Q8_0 activations");
-    if ((q8k && !aligned(q8k, 16)) || (q80 && !aligned(q80, 16)))
-        return fail(ctx, QMM_EALIGN, "activation buffers must be 16-B aligned");
+    if ((rc = check_pre(ctx, q8k, q80, need_q8k, need_q80))) return rc;
     if ((rc = use_device(ctx))) return rc;
     return run_tasks(ctx, nullptr, need_q8k ? q8k : nullptr, need_q80 ? q80 : nullptr, M, K, tasks,
                      n_tasks);
@@ -573,14 +643,87 @@ int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, cons
 int qmm_lm_head_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_rows,
                        uint32_t type, int rows, uint32_t row_base, float *logits_out, float *best_val,
                        uint32_t *best_id) {
-    return lm_argmax(ctx, q8k, q80, M, K, w_rows, type, rows, row_base, nullptr, logits_out, best_val, best_id);
+    return lm_argmax(ctx, q8k, q80, M, K, w_rows, type, rows, row_base, nullptr, 0u, logits_out, best_val, best_id);
 }
 
 int qmm_eval_rows_argmax(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_tensor,
-                         uint32_t type, const uint32_t *row_ids, int n_ids, float *vals_out, float *best_val,
-                         uint32_t *best_id) {
-    if (ctx && !row_ids) return fail(ctx, QMM_EINVAL, "row_ids is NULL");
-    return lm_argmax(ctx, q8k, q80, M, K, w_tensor, type, n_ids, 0, row_ids, vals_out, best_val, best_id);
+                         int64_t tensor_rows, uint32_t type, const uint32_t *row_ids, int n_ids, float *vals_out,
+                         float *best_val, uint32_t *best_id) {
+    if (!ctx) return QMM_EINVAL;
+    if (!row_ids) return fail(ctx, QMM_EINVAL, "row_ids is NULL");
+    if (tensor_rows <= 0 || tensor_rows > int64_t(UINT32_MAX)) return fail(ctx, QMM_EINVAL, "bad tensor_rows");
+    return lm_argmax(ctx, q8k, q80, M, K, w_tensor, type, n_ids, 0, row_ids, uint32_t(tensor_rows), vals_out, best_val,
+                     best_id);
+}
+
+int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_lm,
+                     uint32_t type, int vocab_rows, const qmm_lm_scan_params *params, const uint32_t *pre_ids,
+                     int n_pre, const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int32_t *scan_state) {
+    if (!ctx) return QMM_EINVAL;
+    if (!params || !best_val || !best_id || !scan_state || vocab_rows <= 0 || M <= 0 || n_pre < 0 ||
+        (n_pre > 0 && !pre_ids))
+        return fail(ctx, QMM_EINVAL, "bad LM-head scan arguments");
+    if (params->chunk_rows <= 0 || params->n_thresholds < 0 || (params->n_thresholds > 0 && !params->thresholds) ||
+        params->first_checkpoint < 0)
+        return fail(ctx, QMM_EINVAL, "bad LM-head scan parameters");
+    if (!aligned(best_val, 4) || !aligned(best_id, 4) || !aligned(scan_state, 4))
+        return fail(ctx, QMM_EALIGN, "best_val/best_id/scan_state must be 4-B aligned");
+    // validate every launch's task before the first launch
+    const int chunk = std::min(params->chunk_rows, vocab_rows);
+    const int nchunks = (vocab_rows + params->chunk_rows - 1) / params->chunk_rows;
+    qmm_matrix_task tc, tp, td;
+    int rc = lm_task(ctx, q8k, q80, M, K, w_lm, type, chunk, nullptr, tc);
+    if (!rc && n_pre > 0) rc = lm_task(ctx, q8k, q80, M, K, w_lm, type, n_pre, nullptr, tp);
+    if (!rc && draft_ids && M >= 2) rc = lm_task(ctx, q8k, q80, M, K, w_lm, type, M - 1, nullptr, td);
+    if (rc) return rc;
+    if ((rc = use_device(ctx))) return rc;
+    // scratch: candidate logits [M] | candidate dots [M][M - 1] | the largest call's area
+    const size_t rb = tc.row_bytes;
+    const size_t cand_b = align256(size_t(M) * 4), cdot_b = align256(size_t(M) * size_t(std::max(M - 1, 1)) * 4);
+    size_t area = lm_scratch(M, chunk, rb, false, false).total();
+    if (n_pre > 0) area = std::max(area, lm_scratch(M, n_pre, rb, false, true).total());
+    if (draft_ids && M >= 2) area = std::max(area, align256(size_t(M - 1) * rb));
+    if ((rc = ensure_lm(ctx, cand_b + cdot_b + area))) return rc;
+    uint8_t *scr = static_cast<uint8_t *>(ctx->lm);
+    float *cand = reinterpret_cast<float *>(scr);
+    float *cdot = reinterpret_cast<float *>(scr + cand_b);
+    uint8_t *work = scr + cand_b + cdot_b;
+    const uint8_t *wb = static_cast<const uint8_t *>(w_lm);
+    hipError_t e = qmm::launch_scan_init(M, best_val, best_id, cand, scan_state, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "scan init launch");
+    // the rows every position evaluates first (end-of-text rows), fp32, in list order (E:11143-11146)
+    if (n_pre > 0 && (rc = lm_argmax_run(ctx, q8k, q80, M, K, tp, 0, pre_ids, uint32_t(vocab_rows), nullptr, best_val,
+                                         best_id, work, nullptr, nullptr)))
+        return rc;
+    // each position's draft candidate (E:11147-11153)
+    if (draft_ids && M >= 2) {
+        e = qmm::launch_gather_rows(wb, rb, draft_ids + 1, uint32_t(vocab_rows), M - 1, work, nullptr, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "row gather launch");
+        td.w_base = work;
+        td.dst = cdot;
+        if ((rc = run_tasks(ctx, nullptr, q8k, q80, M, K, &td, 1))) return rc;
+        e = qmm::launch_scan_cand(M, cdot, draft_ids, uint32_t(vocab_rows), best_val, best_id, cand, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "candidate launch");
+    }
+    // the chunks (E:11158-11257): each does nothing once the scan has stopped
+    for (int c = 0; c < nchunks; ++c) {
+        const int r0 = c * params->chunk_rows;
+        qmm_matrix_task t = tc;
+        t.w_base = wb + size_t(r0) * rb;
+        t.rows = std::min(params->chunk_rows, vocab_rows - r0);
+        t.dst_stride = size_t(t.rows);
+        qmm::ScanStep step;
+        step.cand = cand;
+        step.draft = draft_ids;
+        step.margin = params->prune_margin;
+        step.thresh = c < params->n_thresholds ? params->thresholds[c] : -1e30f;  // E:11245-11246
+        step.checkpoint = params->n_thresholds > 0 && c >= params->first_checkpoint;
+        step.c = c;
+        if ((rc = lm_argmax_run(ctx, q8k, q80, M, K, t, uint32_t(r0), nullptr, 0u, nullptr, best_val, best_id, work,
+                                scan_state, &step)))
+            return rc;
+    }
+    return QMM_OK;
 }
 
 int qmm_graph_begin(qmm_context *ctx) {
@@ -606,6 +749,7 @@ int qmm_graph_end(qmm_context *ctx, void **graph_exec) {
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
     *graph_exec = ex;
+    ++ctx->live_graphs;  // its kernels hold the context's current buffers
     return QMM_OK;
 }
 
@@ -615,9 +759,14 @@ int qmm_graph_launch(qmm_context *ctx, void *graph_exec) {
     return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "hipGraphLaunch");
 }
 
-int qmm_graph_destroy(void *graph_exec) {
-    if (!graph_exec) return QMM_EINVAL;
-    return hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)) == hipSuccess ? QMM_OK : QMM_EHIP;
+int qmm_graph_destroy(qmm_context *ctx, void *graph_exec) {
+    if (!ctx || !graph_exec) return fail(ctx, QMM_EINVAL, "bad graph_destroy arguments");
+    int rc = use_device(ctx);
+    if (rc) return rc;
+    (void)hipStreamSynchronize(ctx->stream);  // (a replay may still be running)
+    const hipError_t e = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec));
+    if (ctx->live_graphs > 0 && --ctx->live_graphs == 0) free_retired(ctx);
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "hipGraphExecDestroy");
 }
 
 int qmm_timer_begin(qmm_context *ctx) {

@@ -10,6 +10,8 @@
 namespace qmm {
 
 // ggml type ids (E:115-120)
+constexpr uint32_t kF32 = 0;
+constexpr uint32_t kF16 = 1;
 constexpr uint32_t kQ8_0 = 8;
 constexpr uint32_t kQ4_K = 12;
 constexpr uint32_t kQ5_K = 13;
@@ -18,20 +20,24 @@ constexpr uint32_t kQ6_K = 14;
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Q8_K activation buffer layout (all sections 256-B aligned):
-//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32] | tiles
+//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32] | tiles | h fp16[M][K]
 // tiles: the codes again, in the order of an MFMA operand: for token tile t
 // (tokens 16t .. 16t + 15), 256-value block j and 64-value chunk h, 1 KB at
 // ((t * K/256 + j) * 4 + h) * 1024 whose 16-B slot 16c + n (c < 4, n < 16)
 // holds token 16t + n's codes at block offsets 64h + 8c .. +7, then
 // 64h + 32 + 8c .. +7 (slots of tokens past M are not written).
+// h: the fp16 values the codes were quantized from (the reference keeps them
+// beside its quantized input as x_fp16, E:879-886; its F32 / F16 rows are
+// dotted with them, E:3410-3440).
 struct Q8KLayout {
-    size_t d_off, bs_off, tile_off, total;
+    size_t d_off, bs_off, tile_off, h_off, total;
     __host__ __device__ Q8KLayout(int M, int K) {
         const size_t mk = size_t(M) * size_t(K);
         d_off = align256(mk);
         bs_off = align256(d_off + 4 * size_t(M) * size_t(K / 256));
         tile_off = align256(bs_off + 4 * size_t(M) * size_t(K / 32));
-        total = align256(tile_off + size_t((M + 15) / 16) * 16 * size_t(K));
+        h_off = align256(tile_off + size_t((M + 15) / 16) * 16 * size_t(K));
+        total = align256(h_off + 2 * mk);
     }
 };
 // byte offset in the tiles section of the 4 codes of token m at values
@@ -56,6 +62,7 @@ struct Q8KView {
     const float *d;     // [M][K/256]
     const int32_t *bs;  // [M][K/32]
     const int8_t *qt;   // the tiles section
+    const uint16_t *h;  // fp16 values [M][K]
 };
 struct Q80View {
     const int8_t *qs;  // [M][K]
@@ -72,9 +79,14 @@ struct LdsAct {
 };
 __host__ __device__ inline int lds_pad(int v) { return v + ((v >> 8) << 4); }
 
+// State of a chunked LM-head scan (int32 words in device memory): chunks
+// read, active_batch_len (E:11160), stopped (the checkpoint test passed).
+constexpr int kScanChunks = 0, kScanActive = 1, kScanStopped = 2, kScanPad = 3, kScanWords = 4;
+
 // One matmul launch: a task after validation.
 struct MatArgs {
     const uint8_t *w;  // packed rows
+    uint32_t type;     // ggml type id (kernels of one format ignore it)
     size_t row_bytes;
     int N;             // rows
     int K;             // cols
@@ -83,6 +95,7 @@ struct MatArgs {
     size_t ldy;
     const float *res;  // [M][ldr] or nullptr
     size_t ldr;
+    const int32_t *scan = nullptr;  // a scan's state: the launch does nothing once it has stopped
 };
 
 // Several tasks of one type in one launch (the dispatcher's task groups,
@@ -109,13 +122,34 @@ hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, f
                              void *out, hipStream_t s);
 hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, float *y,
                               void *out, hipStream_t s);
-// LM-head epilogue (qmm_lmhead.hip)
+// LM-head epilogue (qmm_lmhead.hip). ids: list positions name rows ids[i]
+// (NULL: row_base + i), ids at or past id_limit count as -1e30; st: a
+// scan's state or NULL.
 size_t argmax_scratch_bytes(int M, int rows);
-hipError_t launch_argmax(const float *logits, int M, int rows, size_t ldl, bool round16,
-                         const uint32_t *ids, uint32_t row_base, float *best_val, uint32_t *best_id,
-                         void *scratch, hipStream_t s);
-hipError_t launch_gather_rows(const uint8_t *w, size_t row_bytes, const uint32_t *ids, int n, uint8_t *dst,
-                              hipStream_t s);
+hipError_t launch_argmax(float *logits, int M, int rows, size_t ldl, bool round16, const uint32_t *ids,
+                         uint32_t id_limit, uint32_t row_base, float *best_val, uint32_t *best_id, void *scratch,
+                         const int32_t *st, hipStream_t s);
+hipError_t launch_gather_rows(const uint8_t *w, size_t row_bytes, const uint32_t *ids, uint32_t id_limit, int n,
+                              uint8_t *dst, const int32_t *st, hipStream_t s);
+hipError_t launch_scan_init(int M, float *best_val, uint32_t *best_id, float *cand, int32_t *st, hipStream_t s);
+hipError_t launch_scan_cand(int M, const float *vals, const uint32_t *draft, uint32_t vocab, float *best_val,
+                            uint32_t *best_id, float *cand, hipStream_t s);
+// one chunk of a scan: what its final step needs
+struct ScanStep {
+    const float *cand;     // each position's candidate logit
+    const uint32_t *draft; // draft ids or NULL
+    float margin, thresh;
+    bool checkpoint;
+    int c;
+};
+// after chunk c: the argmax update of the active tokens from their partials
+// (nslices per token), then pruning and the checkpoint test
+hipError_t launch_scan_final(const void *part, int nslices, uint32_t row_base, float *best_val, uint32_t *best_id,
+                             const float *cand, const uint32_t *draft, float margin, float thresh, bool checkpoint,
+                             int c, int32_t *st, hipStream_t s);
+hipError_t launch_argmax_partials(float *logits, int M, int rows, size_t ldl, void *scratch, const int32_t *st,
+                                  hipStream_t s);
+int argmax_slices(int rows);
 hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
                               uint16_t *dst, hipStream_t s);
 // M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;
@@ -124,6 +158,11 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
                        const Q80View &x0, hipStream_t s);
 // dynamic LDS bytes the GEMV needs for K (must stay <= 64 KiB)
 size_t gemv_lds_bytes(uint32_t type, int K);
+// M = 1, tasks of several types (and F32 / F16 tasks) in one launch; each
+// workgroup runs its own task's format. Its LDS need per type and K:
+hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk, const Q80View &x0,
+                             hipStream_t s);
+size_t gemv_mixed_lds_bytes(uint32_t type, int K);
 // M = 1 GEMV of one task with the LM head's running (max, argmax) fused into
 // its persistent grid: each workgroup writes one partial (value, row) to part
 // (round16: values rounded to fp16 first); *nparts receives their number
@@ -133,13 +172,19 @@ constexpr int kMaxArgmaxParts = 4096;
 struct AmaxOut {
     void *part;
     int round16;
+    const uint32_t *ids;  // the rows' ids (NULL: contiguous rows); ids >= id_limit count as -1e30
+    uint32_t id_limit;
 };
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
-                              void *part, int *nparts, hipStream_t s);
+                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s);
 hipError_t launch_argmax_final(const void *part, int nparts, const uint32_t *ids, uint32_t row_base,
-                               float *best_val, uint32_t *best_id, hipStream_t s);
+                               float *best_val, uint32_t *best_id, const int32_t *st, hipStream_t s);
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s);
+// M >= 2, tasks of several types (k-quants, F32, F16) in one launch;
+// hipErrorNotSupported (nothing launched) outside 2 <= M <= 64, K <= 3072,
+// K % 256 == 0, or with a Q8_0 task.
+hipError_t launch_mfma_mixed(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s);
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 
@@ -237,6 +282,11 @@ __device__ inline Best wave_best(Best b) {
         b = better(b, o);
     }
     return b;
+}
+
+// a scan that has stopped (uniform: every thread reads the same word)
+__device__ inline bool scan_stopped(const int32_t *st) {
+    return st && __builtin_amdgcn_readfirstlane(st[kScanStopped]) != 0;
 }
 
 // ------------------------------------------------------ Q8 quantization

@@ -478,19 +478,17 @@ __host__ __device__ inline size_t gemv_lds_bytes_t(int K) {
 // otherwise one task, passed alone (a smaller argument block).
 // NC: 16-B stage loads per lane that a batch needs (at most NST; every
 // issued load costs address-unit time even when its lanes are clamped)
-template <class F, int R, int U, bool FUSED, bool GRP, int NC>
-__global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGroup, MatArgs> grp,
-                                                   const float *__restrict__ x32,
-                                                   Q8KView prek, Q80View pre0) {
+// The work of one workgroup (task a, workgroup bx of that task); a device
+// function so that a launch of several formats can run it per workgroup.
+template <class F, int R, int U, bool FUSED, int NC>
+__device__ __attribute__((always_inline)) inline void gemv_wg(const MatArgs &a, int bx, const float *__restrict__ x32,
+                                                              const Q8KView &prek, const Q80View &pre0) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
     constexpr bool q80 = IsQ80<F>::v;
+    if (scan_stopped(a.scan)) return;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / G, k = lane % G;
-    int bx = int(blockIdx.x);
-    MatArgs a;
-    if constexpr (GRP) a = grp.t[group_task(grp, int(blockIdx.x), bx)];
-    else a = grp;
     const int K = a.K;
     const int nb = K / F::QK;
     const int row0 = (bx * 4 + wid) * R;
@@ -626,6 +624,127 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
     }
 }
 
+template <class F, int R, int U, bool FUSED, bool GRP, int NC>
+__global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGroup, MatArgs> grp,
+                                                   const float *__restrict__ x32,
+                                                   Q8KView prek, Q80View pre0) {
+    int bx = int(blockIdx.x);
+    if constexpr (GRP) gemv_wg<F, R, U, FUSED, NC>(grp.t[group_task(grp, int(blockIdx.x), bx)], bx, x32, prek, pre0);
+    else gemv_wg<F, R, U, FUSED, NC>(grp, bx, x32, prek, pre0);
+}
+
+// ------------------------------------------------------- F32 / F16 rows
+// sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440) on the fp16 input
+// (x32 rounded to fp16, or the h section of a Q8_K buffer): wave w of
+// workgroup bx takes rows (4 bx + w) R .. + R; a lane takes the 16-B pieces
+// lane, lane + 64, ... of a row, forms each product w * x in fp32 and adds
+// its products in order, and the wave adds the 64 lane sums by a fixed
+// butterfly. The sums' order is not the reference's row order: these
+// outputs meet the stated tolerance, not bit equality.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+template <bool F16W, bool FUSED>
+__device__ inline void float_piece(const uint8_t *wr, const float *x32, const uint16_t *xh, int p, float &acc) {
+    constexpr int V = F16W ? 8 : 4;  // values per 16-B piece of the row
+    const uint4 wq = ld16_nt(wr + 16 * p);
+    float xv[V], wv[V];
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int h = 0; h < V / 4; ++h) {
+            const float4 f = reinterpret_cast<const float4 *>(x32 + V * p)[h];
+            xv[4 * h] = round_to_fp16(f.x);
+            xv[4 * h + 1] = round_to_fp16(f.y);
+            xv[4 * h + 2] = round_to_fp16(f.z);
+            xv[4 * h + 3] = round_to_fp16(f.w);
+        }
+    } else {
+        uint32_t hw[V / 2];
+        if constexpr (F16W) {
+            const uint4 q = ld16(xh + V * p);
+            hw[0] = q.x; hw[1] = q.y; hw[2] = q.z; hw[3] = q.w;
+        } else {
+            const uint2 q = ld8(xh + V * p);
+            hw[0] = q.x; hw[1] = q.y;
+        }
+#pragma unroll
+        for (int i = 0; i < V / 2; ++i) {
+            xv[2 * i] = fp16_bits_to_f32(hw[i] & 0xFFFFu);
+            xv[2 * i + 1] = fp16_bits_to_f32(hw[i] >> 16);
+        }
+    }
+    const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (F16W) {
+            wv[2 * i] = fp16_bits_to_f32(ww[i] & 0xFFFFu);
+            wv[2 * i + 1] = fp16_bits_to_f32(ww[i] >> 16);
+        } else {
+            wv[i] = __builtin_bit_cast(float, ww[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const float pr = wv[i] * xv[i];  // E:3420 / E:3436 (products rounded, then added)
+        acc = acc + pr;
+    }
+}
+template <bool F16W, int R, bool FUSED>
+__device__ __attribute__((always_inline)) inline void gemv_float_wg(const MatArgs &a, int bx, const float *x32,
+                                                                    const uint16_t *xh) {
+    constexpr int V = F16W ? 8 : 4;
+    if (scan_stopped(a.scan)) return;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int npc = a.K / V;
+    for (int i = 0; i < R; ++i) {
+        const int row = (bx * 4 + wid) * R + i;
+        if (row >= a.N) break;  // the same in every lane of the wave
+        const uint8_t *wr = a.w + size_t(row) * a.row_bytes;
+        float acc = 0.0f;
+        int p = lane;
+        for (; p + 192 < npc; p += 256) {
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;  // (pieces in order: summed in order below)
+            float_piece<F16W, FUSED>(wr, x32, xh, p, a0);
+            float_piece<F16W, FUSED>(wr, x32, xh, p + 64, a1);
+            float_piece<F16W, FUSED>(wr, x32, xh, p + 128, a2);
+            float_piece<F16W, FUSED>(wr, x32, xh, p + 192, a3);
+            acc = acc + a0;
+            acc = acc + a1;
+            acc = acc + a2;
+            acc = acc + a3;
+        }
+        for (; p < npc; p += 64) float_piece<F16W, FUSED>(wr, x32, xh, p, acc);
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (a.res) acc = acc + a.res[row];
+            a.y[row] = acc;
+        }
+    }
+}
+
+// ------------------------------------------------- several formats at once
+// A task group whose types differ (the engine's {qkv, gate, alpha, beta} and
+// {q, k, v} groups, E:7954-7959, E:8110-8114) in one launch: each workgroup
+// runs the body of its own task's format. The dynamic LDS is the largest any
+// of the group's formats needs; every workgroup fills its own activations.
+template <int R, bool FUSED>
+__global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const float *__restrict__ x32, Q8KView prek,
+                                                         Q80View pre0) {
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    switch (a.type) {
+        case kQ4_K: gemv_wg<FmtQ4K4, R, 3, FUSED, stage_chunks<FmtQ4K4, 3>()>(a, bx, x32, prek, pre0); break;
+        case kQ5_K: gemv_wg<FmtQ5K, R, kGemvU, FUSED, 0>(a, bx, x32, prek, pre0); break;
+        case kQ6_K: gemv_wg<FmtQ6K4, R, 3, FUSED, stage_chunks<FmtQ6K4, 3>()>(a, bx, x32, prek, pre0); break;
+        case kQ8_0: gemv_wg<FmtQ80, R, kGemvU, FUSED, stage_chunks<FmtQ80, kGemvU>()>(a, bx, x32, prek, pre0); break;
+        case kF32: gemv_float_wg<false, R, FUSED>(a, bx, x32, prek.h); break;
+        case kF16: gemv_float_wg<true, R, FUSED>(a, bx, x32, prek.h); break;
+        default: break;
+    }
+}
+
 // --------------------------------------------- persistent batch-1 kernel
 // For one task with many more row groups than workgroups fit at once (the
 // LM head). A fixed grid: wave w of workgroup i takes the R-row groups
@@ -640,6 +759,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
     constexpr bool q80 = IsQ80<F>::v;
+    if (scan_stopped(a.scan)) return;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / G, k = lane % G;
     const int K = a.K, nb = K / F::QK;
@@ -741,6 +861,8 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
             for (; bb < nb; ++bb) acc += cr[bb];
             const int row = row0 + lane;
             if (a.res) acc = acc + a.res[row];
+            if constexpr (AMAX)
+                if (am.ids && am.ids[row] >= am.id_limit) acc = -1e30f;  // a row past the tensor (E:11150)
             a.y[row] = acc;
             if constexpr (AMAX) {
                 const float v = am.round16 ? round_to_fp16(acc) : acc;  // as the argmax kernels compare
@@ -814,7 +936,8 @@ static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, cons
 // fused; NotSupported (nothing launched) where that grid does not apply.
 template <class F, int U>
 static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
-                                       void *part, int *nparts, hipStream_t s) {
+                                       const uint32_t *ids, uint32_t id_limit, void *part, int *nparts,
+                                       hipStream_t s) {
     constexpr int R = kGemvR;
     const int nb = a.K / F::QK, cus = cu_count();
     const int wg0 = ((a.N + R - 1) / R + 3) / 4;
@@ -823,14 +946,14 @@ static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, cons
     if (wgs > kMaxArgmaxParts) return hipErrorNotSupported;
     *nparts = wgs;
     return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
-                                                AmaxOut{part, round16 ? 1 : 0});
+                                                AmaxOut{part, round16 ? 1 : 0, ids, id_limit});
 }
 
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
-                              void *part, int *nparts, hipStream_t s) {
+                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s) {
     switch (type) {
-        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, part, nparts, s);
-        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, part, nparts, s);
+        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s);
+        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s);
         default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
     }
 }
@@ -887,6 +1010,51 @@ static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32
     return launch_gemv_t<F, 1, U>(tasks, n, x32, xk, x0, s);
 }
 
+// dynamic LDS of one format's body at R rows per wave (F32 / F16: none)
+template <int R>
+static size_t gemv_wg_lds(uint32_t type, int K) {
+    switch (type) {
+        case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, R, 3>(K);
+        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, R, kGemvU>(K);
+        case kQ6_K: return gemv_lds_bytes_t<FmtQ6K4, R, 3>(K);
+        case kQ8_0: return gemv_lds_bytes_t<FmtQ80, R, kGemvU>(K);
+        default: return 0;
+    }
+}
+
+template <int R>
+static hipError_t launch_gemv_mixed_r(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
+                                      const Q80View &x0, hipStream_t s) {
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    size_t lds = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + ((tasks[i].N + R - 1) / R + 3) / 4;
+        lds = max(lds, gemv_wg_lds<R>(tasks[i].type, tasks[i].K));
+    }
+    const dim3 grid(unsigned(g.wg0[n]));
+    if (x32) hipLaunchKernelGGL((gemv_mixed_kernel<R, true>), grid, dim3(256), lds, s, g, x32, xk, x0);
+    else hipLaunchKernelGGL((gemv_mixed_kernel<R, false>), grid, dim3(256), lds, s, g, x32, xk, x0);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk, const Q80View &x0,
+                             hipStream_t s) {
+    if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) rows += tasks[i].N;
+    // rows per wave as for one k-quant launch of the group's size
+    if (rows >= 4096) return launch_gemv_mixed_r<kGemvR>(tasks, n, x32, xk, x0, s);
+    if (tasks[0].K <= 4096) return launch_gemv_mixed_r<2>(tasks, n, x32, xk, x0, s);
+    return launch_gemv_mixed_r<1>(tasks, n, x32, xk, x0, s);
+}
+
+size_t gemv_mixed_lds_bytes(uint32_t type, int K) {
+    return max(gemv_wg_lds<kGemvR>(type, K), max(gemv_wg_lds<2>(type, K), gemv_wg_lds<1>(type, K)));
+}
+
 hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                        const Q80View &x0, hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
@@ -895,6 +1063,8 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
         case kQ5_K: return launch_gemv_rows<FmtQ5K, kGemvU>(tasks, n, x32, xk, x0, s);
         case kQ6_K: return launch_gemv_rows<FmtQ6K4, 3>(tasks, n, x32, xk, x0, s);
         case kQ8_0: return launch_gemv_rows<FmtQ80, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kF32:
+        case kF16: return launch_gemv_mixed(tasks, n, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
     }
 }

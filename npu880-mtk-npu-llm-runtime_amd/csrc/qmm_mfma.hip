@@ -411,6 +411,7 @@ __global__ __launch_bounds__(256) void tile_kernel(MatGroup grp, typename ActOf<
     const int kp = wid % KS, pt = (wid / KS) % C::PT, pr = wid / (KS * C::PT);
     int bx;
     const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    if (scan_stopped(a.scan)) return;
     const int n0 = bx * C::ROWS, m0 = int(blockIdx.y) * C::TOK;
     const int K = a.K, nb = K / F::QK;
     const int nchunks = (nb + KCB - 1) / KCB;
@@ -706,6 +707,7 @@ __global__ __launch_bounds__(256 * RTM) void res_kernel(MatGroup grp, Q8KView x,
     using P = ResPart<F, NBK>;
     constexpr int W = 4 * RTM;
     extern __shared__ __align__(16) uint8_t lds[];
+    if (scan_stopped(grp.t[0].scan)) return;  // (every task of a group shares the scan)
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rt = wid % RTM, kp = wid / RTM;
@@ -908,15 +910,15 @@ struct PartCfg {
 };
 
 template <class F, int TT, int NBK>
-__global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
+__device__ __attribute__((always_inline)) inline void part_wg(const MatArgs &a, int bx, const Q8KView &x,
+                                                              const ResArgs &ra) {
     using C = PartCfg<F, TT, NBK>;
     using P = typename C::P;
     extern __shared__ __align__(16) uint8_t lds[];
+    if (scan_stopped(a.scan)) return;
     const int lane = threadIdx.x & 63;
     const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nl = lane & 15, cl = lane >> 4;
-    int bx = 0;
-    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
     const int n0 = bx * 16, M = a.M, K = a.K, nb = K / 256;
     const int j0 = kp * nb / 4, nbk = (kp + 1) * nb / 4 - j0;
     const uint32_t lds0 = lds_addr(lds);
@@ -1083,6 +1085,144 @@ __global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResA
     }
 }
 
+template <class F, int TT, int NBK>
+__global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    part_wg<F, TT, NBK>(a, bx, x, ra);
+}
+
+// ================================================== F32 / F16 weight rows
+// sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440) for M >= 2: the
+// fp16 input (the h section of the Q8_K buffer) against 16 weight rows per
+// wave on the matrix unit, fp32 accumulation — F16 rows by
+// v_mfma_f32_16x16x32_f16 (products of fp16 values are exact in fp32), F32
+// rows by v_mfma_f32_16x16x4_f32 on the input widened to fp32. Lane l
+// supplies token / row l % 16 and k-slice l / 16 (F32: the four k of a
+// 16-B piece go to four successive MFMAs, a k permutation shared by both
+// operands) and receives D[token 4 (l / 16) + r][row l % 16]. The sums'
+// order is not the reference's row order: within the stated tolerance, not
+// bit-exact. Rows past N and tokens past M repeat the last one (their
+// outputs are not kept), so every load stays inside the buffers.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+template <bool F16W>
+__device__ inline f32x4v float_tile(const MatArgs &a, int n0, int m0, int k0, int k1, const uint16_t *xh,
+                                    f32x4v acc) {
+    const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
+    const uint8_t *wr = a.w + size_t(min(n0 + nl, a.N - 1)) * a.row_bytes;
+    const uint16_t *xr = xh + size_t(min(m0 + nl, a.M - 1)) * size_t(a.K);
+    if constexpr (F16W) {
+        for (int k = k0 + 8 * cl; k < k1; k += 32) {
+            const uint4 wq = ld16_nt(wr + 2 * size_t(k));
+            const uint4 xq = ld16(xr + k);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, xq), __builtin_bit_cast(f16x8v, wq),
+                                                         acc, 0, 0, 0);
+        }
+    } else {
+        for (int k = k0 + 4 * cl; k < k1; k += 16) {
+            const uint4 wq = ld16_nt(wr + 4 * size_t(k));
+            const uint2 xq = ld8(xr + k);
+            const float xv[4] = {fp16_bits_to_f32(xq.x & 0xFFFFu), fp16_bits_to_f32(xq.x >> 16),
+                                 fp16_bits_to_f32(xq.y & 0xFFFFu), fp16_bits_to_f32(xq.y >> 16)};
+            const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], __builtin_bit_cast(float, wv[i]), acc, 0, 0, 0);
+        }
+    }
+    return acc;
+}
+
+// One F32 / F16 task for M >= 2: workgroup (bx, by) owns rows 16 bx ..
+// +15 and, per wave w, tokens 64 by + 16 w .. +15, over all of K.
+template <bool F16W>
+__global__ __launch_bounds__(256) void float_tile_kernel(MatGroup grp, Q8KView x) {
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
+    const int n0 = bx * 16, m0 = (int(blockIdx.y) * 4 + int(threadIdx.x >> 6)) * 16;
+    if (m0 >= a.M || scan_stopped(a.scan)) return;  // the same in every lane of the wave
+    f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc = float_tile<F16W>(a, n0, m0, 0, a.K, x.h, acc);
+    const int n = n0 + nl;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int tok = m0 + 4 * cl + r;
+        if (tok < a.M && n < a.N) {
+            float v = acc[r];
+            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+            a.y[size_t(tok) * a.ldy + n] = v;
+        }
+    }
+}
+
+// The part kernel's shape for an F32 / F16 task (one 16-row tile, all 16 TT
+// tokens, wave kp = the kp-th quarter of K): the four quarters' sums meet in
+// LDS and are added in quarter order, as the k-quant parts are.
+template <bool F16W, int TT>
+__device__ __attribute__((always_inline)) inline void part_float_wg(const MatArgs &a, int bx, const Q8KView &x) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    if (scan_stopped(a.scan)) return;
+    const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
+    const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = bx * 16;
+    constexpr int KQ = F16W ? 32 : 16;  // values per k step of a lane group
+    const int steps = a.K / KQ;
+    const int k0 = (kp * steps / 4) * KQ, k1 = ((kp + 1) * steps / 4) * KQ;
+    float *terms = reinterpret_cast<float *>(lds);  // [part][token tile][r][lane]
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        acc = float_tile<F16W>(a, n0, 16 * t, k0, k1, x.h, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) terms[((kp * TT + t) * 4 + r) * 64 + lane] = acc[r];
+    }
+    lds_barrier();
+    const int n = n0 + nl;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+        float v = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) v = v + terms[((p * TT + t) * 4 + kp) * 64 + lane];
+        const int tok = 16 * t + 4 * cl + kp;
+        if (tok < a.M && n < a.N) {
+            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+            a.y[size_t(tok) * a.ldy + n] = v;
+        }
+    }
+}
+
+// ================================================ several formats at once
+// A task group whose types differ (E:7954-7959, E:8110-8114) in one launch
+// for 2 <= M <= 64 and K <= 3072: every workgroup is one 16-row tile of its
+// task and runs that format's part-kernel body (the k-quants folded from
+// two token tiles, as a single-format launch does). ra[f] holds format f's
+// LDS offsets (f = kMixQ4K ..); the launch's LDS is the largest of them.
+constexpr int kMixQ4K = 0, kMixQ5K = 1, kMixQ6K = 2, kMixF32 = 3, kMixF16 = 4, kMixFormats = 5;
+struct MixArgs {
+    ResArgs ra[kMixFormats];
+};
+__host__ __device__ inline int mix_format(uint32_t type) {
+    return type == kQ4_K ? kMixQ4K : type == kQ5_K ? kMixQ5K : type == kQ6_K ? kMixQ6K : type == kF32 ? kMixF32 : kMixF16;
+}
+
+template <int TT>
+__global__ __launch_bounds__(256) void part_mixed_kernel(MatGroup grp, Q8KView x, MixArgs mx) {
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    using Q4 = std::conditional_t<(TT > 1), MQ4KS, MQ4K>;
+    using Q5 = std::conditional_t<(TT > 1), MQ5KS, MQ5K>;
+    switch (a.type) {
+        case kQ4_K: part_wg<Q4, TT, 3>(a, bx, x, mx.ra[kMixQ4K]); break;
+        case kQ5_K: part_wg<Q5, TT, 3>(a, bx, x, mx.ra[kMixQ5K]); break;
+        case kQ6_K: part_wg<MQ6KS, TT, 3>(a, bx, x, mx.ra[kMixQ6K]); break;
+        case kF32: part_float_wg<false, TT>(a, bx, x); break;
+        case kF16: part_float_wg<true, TT>(a, bx, x); break;
+        default: break;
+    }
+}
+
 int mfma_cu_count();
 
 // Resident-tile launch if the tiles, codes and scales fit one CU's LDS;
@@ -1123,21 +1263,29 @@ static hipError_t launch_res_r(const MatArgs *tasks, int n, const Q8KView &x, in
 // (several tiles per workgroup in sequence, one wave per SIMD, measured
 // slower than the chunked tile kernel: Q4_K 9728 x 2560, M = 64, 21.9
 // against 17.6 us).
+// LDS offsets of the part-kernel body of format F for (M, K)
+template <class F, int TT>
+static ResArgs part_args(int M, int K) {
+    using C = PartCfg<F, TT, 3>;
+    using P = typename C::P;
+    const int nb = K / 256;
+    ResArgs ra{};
+    ra.off_d = 4 * P::NI * 1024;
+    ra.off_t = ra.off_d + (M * nb + 63) / 64 * 256 + nb * 64 * 4;
+    ra.lds = ra.off_t + C::TERMS;
+    return ra;
+}
+
 template <class F, int TT>
 static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
     constexpr int NBK = 3;
-    using C = PartCfg<F, TT, NBK>;
-    using P = typename C::P;
     const MatArgs &a = tasks[0];
     const int nb = a.K / 256;
     int tiles = 0;
     for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
     if (nb > 4 * NBK || !x.qt || (TT > 2 && tiles > mfma_cu_count())) return hipErrorNotSupported;
-    ResArgs ra{};
+    ResArgs ra = part_args<F, TT>(a.M, a.K);
     ra.tiles = tiles;
-    ra.off_d = 4 * P::NI * 1024;
-    ra.off_t = ra.off_d + (a.M * nb + 63) / 64 * 256 + nb * 64 * 4;
-    ra.lds = ra.off_t + C::TERMS;
     if (ra.lds > 160 * 1024) return hipErrorNotSupported;
     MatGroup g{};
     g.n = n;
@@ -1235,6 +1383,67 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     }
 }
 
+template <int TT>
+static hipError_t launch_part_mixed_t(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    const int M = tasks[0].M, K = tasks[0].K;
+    using Q4 = std::conditional_t<(TT > 1), MQ4KS, MQ4K>;
+    using Q5 = std::conditional_t<(TT > 1), MQ5KS, MQ5K>;
+    MixArgs mx{};
+    mx.ra[kMixQ4K] = part_args<Q4, TT>(M, K);
+    mx.ra[kMixQ5K] = part_args<Q5, TT>(M, K);
+    mx.ra[kMixQ6K] = part_args<MQ6KS, TT>(M, K);
+    mx.ra[kMixF32].lds = mx.ra[kMixF16].lds = 4 * TT * 1024;
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    int lds = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
+        lds = max(lds, mx.ra[mix_format(tasks[i].type)].lds);
+    }
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    hipLaunchKernelGGL((part_mixed_kernel<TT>), dim3(unsigned(g.wg0[n])), dim3(256), size_t(lds), s, g, x, mx);
+    return hipGetLastError();
+}
+
+// Several types in one launch (k-quants, F32, F16; 2 <= M <= 64, K <= 3072,
+// K % 256 == 0, no Q8_0); hipErrorNotSupported (nothing launched) otherwise.
+// Past 32 tokens a workgroup needs a CU to itself, so the tiles must not
+// outnumber the CUs.
+hipError_t launch_mfma_mixed(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
+    const int M = tasks[0].M, K = tasks[0].K;
+    if (M < 2 || M > 64 || K > 3072 || K % 256 || !x.qt || !x.h) return hipErrorNotSupported;
+    int tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        if (tasks[i].type == kQ8_0) return hipErrorNotSupported;
+        tiles += (tasks[i].N + 15) / 16;
+    }
+    if (M <= 16) return launch_part_mixed_t<1>(tasks, n, x, s);
+    if (M <= 32) return launch_part_mixed_t<2>(tasks, n, x, s);
+    if (tiles > mfma_cu_count()) return hipErrorNotSupported;
+    if (M <= 48) return launch_part_mixed_t<3>(tasks, n, x, s);
+    return launch_part_mixed_t<4>(tasks, n, x, s);
+}
+
+// F32 / F16 tasks of one type, M >= 2 (any K with K % 32 == 0 for F16,
+// K % 16 == 0 for F32)
+static hipError_t launch_float(uint32_t type, const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    if (!x.h) return hipErrorInvalidValue;
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
+    }
+    const dim3 grid(unsigned(g.wg0[n]), unsigned((tasks[0].M + 63) / 64));
+    if (type == kF16) hipLaunchKernelGGL((float_tile_kernel<true>), grid, dim3(256), 0, s, g, x);
+    else hipLaunchKernelGGL((float_tile_kernel<false>), grid, dim3(256), 0, s, g, x);
+    return hipGetLastError();
+}
+
 int mfma_cu_count() {
     static int cus[64] = {};
     int dev = 0;
@@ -1254,6 +1463,8 @@ hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView
         case kQ5_K: return launch_tile<MQ5K>(tasks, n, xk, s);
         case kQ6_K: return launch_tile<MQ6KS>(tasks, n, xk, s);
         case kQ8_0: return launch_tile<MQ80>(tasks, n, x0, s);
+        case kF32:
+        case kF16: return launch_float(type, tasks, n, xk, s);
         default: return hipErrorInvalidValue;
     }
 }

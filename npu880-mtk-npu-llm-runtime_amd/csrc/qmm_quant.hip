@@ -10,11 +10,34 @@
 
 namespace qmm {
 
+// Sections of a Q8_K activation buffer as the producers write them.
+struct Q8KOut {
+    int8_t *qs;
+    float *d;
+    int32_t *bs;
+    int8_t *qt;
+    uint16_t *h;
+};
+__host__ inline Q8KOut q8k_out(void *buf, int M, int K) {
+    const Q8KLayout L(M, K);
+    uint8_t *b = static_cast<uint8_t *>(buf);
+    return {reinterpret_cast<int8_t *>(b), reinterpret_cast<float *>(b + L.d_off),
+            reinterpret_cast<int32_t *>(b + L.bs_off), reinterpret_cast<int8_t *>(b + L.tile_off),
+            reinterpret_cast<uint16_t *>(b + L.h_off)};
+}
+
 // Quantize one fp16-rounded 256-value block held 4 values per lane and
 // store it as Q8_K block `blk` (flattened over [M][K/256]).
-// The codes also go to the tiles section qt (nb blocks per row).
+// The codes also go to the tiles section (nb blocks per row), the fp16
+// values to the h section.
 __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
-                                       size_t blk, int8_t *qs, float *d, int32_t *bs, int8_t *qt, int nb) {
+                                       size_t blk, const Q8KOut &o, int nb) {
+    int8_t *qs = o.qs, *qt = o.qt;
+    float *d = o.d;
+    int32_t *bs = o.bs;
+    const uint32_t hlo = uint32_t(f32_to_fp16_bits(h0)) | (uint32_t(f32_to_fp16_bits(h1)) << 16);
+    const uint32_t hhi = uint32_t(f32_to_fp16_bits(h2)) | (uint32_t(f32_to_fp16_bits(h3)) << 16);
+    reinterpret_cast<uint2 *>(o.h + blk * 256)[lane] = make_uint2(hlo, hhi);
     float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
     a = wave_max(a);  // E:941-946
     int sum;
@@ -29,16 +52,13 @@ __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, i
 
 // x [M][K] fp32, flattened 256-blocks; one wave per block.
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x,
-                                                           size_t nblk, int8_t *__restrict__ qs,
-                                                           float *__restrict__ d,
-                                                           int32_t *__restrict__ bs,
-                                                           int8_t *__restrict__ qt, int nb) {
+                                                           size_t nblk, Q8KOut o, int nb) {
     const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (blk >= nblk) return;
     const int lane = threadIdx.x & 63;
     const float4 v = reinterpret_cast<const float4 *>(x + blk * 256)[lane];
     store_q8k_block(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z),
-                    round_to_fp16(v.w), lane, blk, qs, d, bs, qt, nb);
+                    round_to_fp16(v.w), lane, blk, o, nb);
 }
 
 // Q8_0: 32-value blocks, 8 lanes each, 8 blocks per wave (flattened).
@@ -62,28 +82,31 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     if (sub == 0) d[blk] = q8_scale(a);
 }
 
-// swiglu_chunk_worker (E:4349-4357) on fp32 gate/up: h = (g / (1 + expf(-g))) * u,
-// then the same fp16 round + Q8_K quantizer per 256-value block.
+// swiglu_chunk_worker (E:4349-4357): gate and up are the dispatcher's fp16
+// outputs in the reference, so each fp32 input is rounded to fp16 first
+// (E:4352-4353); h = (g / (1 + expf(-g))) * u in fp32, then the same fp16
+// round + Q8_K quantizer per 256-value block.
+__device__ inline float silu_mul(float g, float u) {
+    g = round_to_fp16(g);
+    u = round_to_fp16(u);
+    return (g / (1.0f + expf(-g))) * u;  // E:4355
+}
 __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict__ gate,
                                                          const float *__restrict__ up,
-                                                         size_t nblk, float *__restrict__ h,
-                                                         int8_t *__restrict__ qs,
-                                                         float *__restrict__ d,
-                                                         int32_t *__restrict__ bs,
-                                                         int8_t *__restrict__ qt, int nb) {
+                                                         size_t nblk, float *__restrict__ h, Q8KOut o, int nb) {
     const size_t blk = size_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (blk >= nblk) return;
     const int lane = threadIdx.x & 63;
     const float4 g = reinterpret_cast<const float4 *>(gate + blk * 256)[lane];
     const float4 u = reinterpret_cast<const float4 *>(up + blk * 256)[lane];
     float4 r;
-    r.x = (g.x / (1.0f + expf(-g.x))) * u.x;
-    r.y = (g.y / (1.0f + expf(-g.y))) * u.y;
-    r.z = (g.z / (1.0f + expf(-g.z))) * u.z;
-    r.w = (g.w / (1.0f + expf(-g.w))) * u.w;
+    r.x = silu_mul(g.x, u.x);
+    r.y = silu_mul(g.y, u.y);
+    r.z = silu_mul(g.z, u.z);
+    r.w = silu_mul(g.w, u.w);
     if (h) reinterpret_cast<float4 *>(h + blk * 256)[lane] = r;
     store_q8k_block(round_to_fp16(r.x), round_to_fp16(r.y), round_to_fp16(r.z),
-                    round_to_fp16(r.w), lane, blk, qs, d, bs, qt, nb);
+                    round_to_fp16(r.w), lane, blk, o, nb);
 }
 
 // rmsnorm_fp16_rows_fast (E:4264-4314) + its Q8_K (E:4303-4305): one
@@ -96,10 +119,7 @@ __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict
 template <int NJ>
 __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restrict__ x,
                                                           const float *__restrict__ gamma, int K,
-                                                          float *__restrict__ y, int8_t *__restrict__ qs,
-                                                          float *__restrict__ d,
-                                                          int32_t *__restrict__ bs,
-                                                          int8_t *__restrict__ qt) {
+                                                          float *__restrict__ y, Q8KOut o) {
     __shared__ float part[4];
     const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
     const size_t m = blockIdx.x;
@@ -136,7 +156,7 @@ __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restric
         r.z = round_to_fp16(h[j].z * inv_rms * round_to_fp16(g.z));
         r.w = round_to_fp16(h[j].w * inv_rms * round_to_fp16(g.w));
         if (y) reinterpret_cast<float4 *>(y + m * size_t(K))[q] = r;
-        store_q8k_block(r.x, r.y, r.z, r.w, lane, m * nbk + size_t(4 * j + wid), qs, d, bs, qt, int(nbk));
+        store_q8k_block(r.x, r.y, r.z, r.w, lane, m * nbk + size_t(4 * j + wid), o, int(nbk));
     }
 }
 
@@ -150,6 +170,16 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
     const size_t gi = size_t(blockIdx.x) * 256 + threadIdx.x;
     if (gi >= ngroups) return;
     uint16_t *y = dst + gi * 32;
+    if (type == kF16) {  // E:3857-3860: a copy
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(w) + gi * 32;
+        for (int i = 0; i < 32; ++i) y[i] = src[i];
+        return;
+    }
+    if (type == kF32) {  // E:3876-3879: (__fp16) of each value
+        const float *src = reinterpret_cast<const float *>(w) + gi * 32;
+        for (int i = 0; i < 32; ++i) y[i] = f32_to_fp16_bits(src[i]);
+        return;
+    }
     if (type == kQ8_0) {
         const uint8_t *blk = w + gi * 34;
         const float dd = fp16_bits_to_f32(uint32_t(blk[0]) | (uint32_t(blk[1]) << 8));
@@ -206,14 +236,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
 }
 
 hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s) {
-    const Q8KLayout L(M, K);
-    uint8_t *base = static_cast<uint8_t *>(out);
     const size_t nblk = size_t(M) * size_t(K / 256);
     const unsigned grid = unsigned((nblk + 3) / 4);
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk,
-                       reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
-                       reinterpret_cast<int32_t *>(base + L.bs_off), reinterpret_cast<int8_t *>(base + L.tile_off),
-                       K / 256);
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk, q8k_out(out, M, K), K / 256);
     return hipGetLastError();
 }
 
@@ -230,28 +255,19 @@ hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStre
 
 hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                              void *out, hipStream_t s) {
-    const Q8KLayout L(M, N);
-    uint8_t *base = static_cast<uint8_t *>(out);
     const size_t nblk = size_t(M) * size_t(N / 256);
     const unsigned grid = unsigned((nblk + 3) / 4);
-    hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(grid), dim3(256), 0, s, gate, up, nblk, h,
-                       reinterpret_cast<int8_t *>(base), reinterpret_cast<float *>(base + L.d_off),
-                       reinterpret_cast<int32_t *>(base + L.bs_off), reinterpret_cast<int8_t *>(base + L.tile_off),
+    hipLaunchKernelGGL(swiglu_q8k_kernel, dim3(grid), dim3(256), 0, s, gate, up, nblk, h, q8k_out(out, M, N),
                        N / 256);
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_q8k(const float *x, const float *gamma, int M, int K, float *y,
                               void *out, hipStream_t s) {
-    const Q8KLayout L(M, K);
-    uint8_t *base = static_cast<uint8_t *>(out);
-    int8_t *qs = reinterpret_cast<int8_t *>(base);
-    float *d = reinterpret_cast<float *>(base + L.d_off);
-    int32_t *bs = reinterpret_cast<int32_t *>(base + L.bs_off);
-    int8_t *qt = reinterpret_cast<int8_t *>(base + L.tile_off);
+    const Q8KOut o = q8k_out(out, M, K);
     const int nj = (K / 4 + 255) / 256;  // float4s per thread
 #define QMM_RMS(NJ) \
-    hipLaunchKernelGGL(rmsnorm_q8k_kernel<NJ>, dim3(unsigned(M)), dim3(256), 0, s, x, gamma, K, y, qs, d, bs, qt)
+    hipLaunchKernelGGL(rmsnorm_q8k_kernel<NJ>, dim3(unsigned(M)), dim3(256), 0, s, x, gamma, K, y, o)
     if (nj <= 3) QMM_RMS(3);
     else if (nj <= 4) QMM_RMS(4);
     else if (nj <= 10) QMM_RMS(10);

@@ -24,10 +24,12 @@ LIB_PATH = os.path.join(HERE, "libqmm_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "qmm_hip.h")
 
 QMM_OK, QMM_EINVAL, QMM_ETYPE, QMM_ESHAPE, QMM_EHIP, QMM_ENOMEM, QMM_EALIGN = range(7)
+TYPE_F32, TYPE_F16 = 0, 1
 TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 8, 12, 13, 14
-TYPE_NAMES = {TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K", TYPE_Q6_K: "Q6_K"}
-BLOCK_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
-BLOCK_VALUES = {TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
+TYPE_NAMES = {TYPE_F32: "F32", TYPE_F16: "F16", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K",
+              TYPE_Q6_K: "Q6_K"}
+BLOCK_BYTES = {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
+BLOCK_VALUES = {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
 
 _p = C.c_void_p
 
@@ -40,6 +42,12 @@ class QmmError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"qmm status {status}: {message}")
         self.status = status
+
+
+class LmScanParams(C.Structure):
+    """qmm_lm_scan_params (the chunked vocabulary scan, E:11107-11262)."""
+    _fields_ = [("chunk_rows", C.c_int), ("thresholds", C.POINTER(C.c_float)), ("n_thresholds", C.c_int),
+                ("first_checkpoint", C.c_int), ("prune_margin", C.c_float)]
 
 
 class _Task(C.Structure):
@@ -67,6 +75,7 @@ _SIGNATURES = [
     ("qmm_q8k_d_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_bsum_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_tile_offset", C.c_size_t, [C.c_int, C.c_int]),
+    ("qmm_q8k_h_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_d_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_malloc", C.c_int, [_p, C.c_size_t, C.POINTER(_p)]),
@@ -88,8 +97,10 @@ _SIGNATURES = [
     ("qmm_gguf_upload", C.c_int, [_p, _p, C.c_char_p, _p, _p]),
     ("qmm_lm_head_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int, C.c_uint32,
                                      _p, _p, _p]),
-    ("qmm_eval_rows_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, _p, C.c_int,
+    ("qmm_eval_rows_argmax", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_int64, C.c_uint32, _p, C.c_int,
                                        _p, _p, _p]),
+    ("qmm_lm_head_scan", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int,
+                                   C.POINTER(LmScanParams), _p, C.c_int, _p, _p, _p, _p]),
     ("qmm_dequantize_f16", C.c_int, [_p, _p, C.c_uint32, C.c_int64, C.c_int64, _p]),
     ("qmm_gemm_multi_dispatch", C.c_int, [_p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_gemm_multi_dispatch_prequantized", C.c_int,
@@ -97,7 +108,7 @@ _SIGNATURES = [
     ("qmm_graph_begin", C.c_int, [_p]),
     ("qmm_graph_end", C.c_int, [_p, C.POINTER(_p)]),
     ("qmm_graph_launch", C.c_int, [_p, _p]),
-    ("qmm_graph_destroy", C.c_int, [_p]),
+    ("qmm_graph_destroy", C.c_int, [_p, _p]),
     ("qmm_timer_begin", C.c_int, [_p]),
     ("qmm_timer_end", C.c_int, [_p, C.POINTER(C.c_float)]),
 ]
@@ -374,11 +385,22 @@ class Context:
         self._call("qmm_lm_head_argmax", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_rows)),
                    type_id, rows, row_base, _p(_addr(logits_out)), _p(_addr(best_val)), _p(_addr(best_id)))
 
-    def eval_rows_argmax(self, q8k, q80, M: int, K: int, w_tensor, type_id: int, row_ids, n_ids: int,
-                         vals_out, best_val, best_id):
+    def eval_rows_argmax(self, q8k, q80, M: int, K: int, w_tensor, tensor_rows: int, type_id: int, row_ids,
+                         n_ids: int, vals_out, best_val, best_id):
         self._call("qmm_eval_rows_argmax", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_tensor)),
-                   type_id, _p(_addr(row_ids)), n_ids, _p(_addr(vals_out)), _p(_addr(best_val)),
+                   tensor_rows, type_id, _p(_addr(row_ids)), n_ids, _p(_addr(vals_out)), _p(_addr(best_val)),
                    _p(_addr(best_id)))
+
+    def lm_head_scan(self, q8k, q80, M: int, K: int, w_lm, type_id: int, vocab_rows: int, chunk_rows: int,
+                     thresholds=None, first_checkpoint: int = 0, prune_margin: float = 1e-3, pre_ids=None,
+                     n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None):
+        """qmm_lm_head_scan: the chunked vocabulary scan with early exit and pruning."""
+        thr = None if thresholds is None else (C.c_float * len(thresholds))(*[float(t) for t in thresholds])
+        prm = LmScanParams(chunk_rows, thr if thr is not None else None, 0 if thr is None else len(thresholds),
+                           first_checkpoint, prune_margin)
+        self._call("qmm_lm_head_scan", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_lm)), type_id,
+                   vocab_rows, C.byref(prm), _p(_addr(pre_ids)), n_pre, _p(_addr(draft_ids)), _p(_addr(best_val)),
+                   _p(_addr(best_id)), _p(_addr(scan_state)))
 
     def swiglu_q8k(self, gate, up, M: int, N: int, h_out, out):
         self._call("qmm_swiglu_q8k", self._h, _p(_addr(gate)), _p(_addr(up)), M, N,
@@ -423,7 +445,7 @@ class Context:
         self._call("qmm_graph_launch", self._h, _p(g))
 
     def graph_destroy(self, g: int):
-        self.lib.qmm_graph_destroy(_p(g))
+        self._call("qmm_graph_destroy", self._h, _p(g))
 
     def timer_begin(self):
         self._call("qmm_timer_begin", self._h)
@@ -448,13 +470,21 @@ class Context:
         t = self.d2h(buf, np.int8, (T * 16 * K,), offset=int(self.lib.qmm_q8k_tile_offset(M, K)))
         return q8k_untile(t, M, K)
 
-    def write_q8k(self, buf, d, qs, bs):
+    def write_q8k(self, buf, d, qs, bs, x16=None):
+        """All sections of a device Q8_K buffer; x16 = the fp16 values (bits
+        [M][K]) for the h section, zeros if None."""
         M, K = qs.shape
         lib = self.lib
         self.h2d(buf, np.ascontiguousarray(qs, np.int8))
         self.h2d(buf, np.ascontiguousarray(d, np.float32), offset=int(lib.qmm_q8k_d_offset(M, K)))
         self.h2d(buf, np.ascontiguousarray(bs, np.int32), offset=int(lib.qmm_q8k_bsum_offset(M, K)))
         self.h2d(buf, q8k_tile(qs), offset=int(lib.qmm_q8k_tile_offset(M, K)))
+        h = np.zeros((M, K), np.uint16) if x16 is None else np.ascontiguousarray(x16, np.uint16).reshape(M, K)
+        self.h2d(buf, h, offset=int(lib.qmm_q8k_h_offset(M, K)))
+
+    def read_q8k_h(self, buf, M: int, K: int) -> np.ndarray:
+        """The h section (fp16 bits [M][K]) of a device Q8_K buffer."""
+        return self.d2h(buf, np.uint16, (M, K), offset=int(self.lib.qmm_q8k_h_offset(M, K)))
 
     def read_q8_0(self, buf, M: int, K: int):
         qs = self.d2h(buf, np.int8, (M, K))

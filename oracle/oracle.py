@@ -25,9 +25,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref.so")
 
+TYPE_F32, TYPE_F16 = 0, 1
 TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 8, 12, 13, 14
-BLOCK_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
-BLOCK_VALUES = {TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
+BLOCK_BYTES = {TYPE_F32: 4, TYPE_F16: 2, TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
+BLOCK_VALUES = {TYPE_F32: 1, TYPE_F16: 1, TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
 
 _p = C.c_void_p
 
@@ -77,16 +78,21 @@ class Oracle:
         L.qo_quantize_q8_0_f32.argtypes = [_p, C.c_int, C.c_int, _p, _p]
         L.qo_dot_row.restype = C.c_float
         L.qo_dot_row.argtypes = [C.c_uint32, _p, C.c_int, _p, _p, _p]
+        L.qo_dot_row_float.restype = C.c_float
+        L.qo_dot_row_float.argtypes = [C.c_uint32, _p, C.c_int, _p]
         L.qo_block_partials.restype = C.c_int
         L.qo_block_partials.argtypes = [C.c_uint32, _p, C.c_int, _p, _p, _p, _p]
         L.qo_gemm_multi.restype = C.c_int
         L.qo_gemm_multi.argtypes = [_p, C.c_int, C.c_int, C.POINTER(_MatrixTask), C.c_int]
         L.qo_gemm_multi_prequantized.restype = C.c_int
-        L.qo_gemm_multi_prequantized.argtypes = [_p, _p, _p, _p, _p, C.c_int, C.c_int,
+        L.qo_gemm_multi_prequantized.argtypes = [_p, _p, _p, _p, _p, _p, C.c_int, C.c_int,
                                                  C.POINTER(_MatrixTask), C.c_int]
         L.qo_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
         L.qo_rmsnorm_q8k_f16.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p, _p]
         L.qo_chunk_argmax.argtypes = [_p, C.c_int, C.c_int, C.c_size_t, C.c_int, _p, C.c_uint32, _p, _p]
+        L.qo_lm_head_scan.restype = C.c_int
+        L.qo_lm_head_scan.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p, C.c_int,
+                                      C.c_int, C.c_float, _p, C.c_int, _p, _p, _p, _p, _p]
 
     # fp16 ----------------------------------------------------------------
     def f32_to_fp16(self, x) -> np.ndarray:
@@ -164,6 +170,12 @@ class Oracle:
         return float(self.lib.qo_dot_row(type_id, _ptr(w_row), K, _ptr(d), _ptr(qs),
                                           None if bs is None else _ptr(bs)))
 
+    def dot_row_float(self, type_id: int, w_row: np.ndarray, K: int, x16) -> float:
+        """An F32 / F16 row against one fp16 activation row (bits)."""
+        w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+        x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+        return float(self.lib.qo_dot_row_float(type_id, _ptr(w_row), K, _ptr(x16)))
+
     def block_partials(self, type_id: int, w_row: np.ndarray, K: int, qs, bsum=None):
         nb = K // BLOCK_VALUES[type_id]
         S = np.zeros(nb, np.int32)
@@ -181,7 +193,8 @@ class Oracle:
         ``tasks``: list of dicts with keys ``w`` (uint8 packed rows), ``type``,
         ``rows`` and optional ``residual`` (float32 [M, rows]). Returns one
         float32 [M, rows] array per task. ``prequantized`` = (q8k triple or
-        None, q80 pair or None) skips the quantizer.
+        None, q80 pair or None) skips the quantizer; F32 / F16 tasks then read
+        x rounded to fp16 (the input the engine still passes, E:4206).
         """
         x = np.ascontiguousarray(x, dtype=np.float32)
         if x.ndim == 1:
@@ -205,7 +218,8 @@ class Oracle:
         else:
             q8k, q80 = prequantized
             ptrs = []
-            for a in (q8k or (None, None, None)) + (q80 or (None, None)):
+            x16 = self.f32_to_fp16(x)
+            for a in (q8k or (None, None, None)) + (q80 or (None, None)) + (x16,):
                 if a is None:
                     ptrs.append(None)
                 else:
@@ -269,6 +283,28 @@ class Oracle:
         bv, bi = self.chunk_argmax(vals, best_val, best_id, False, ids, 0)
         return vals, bv, bi
 
+    def lm_head_scan(self, q8k, w, type_id: int, vocab_rows: int, K: int, chunk_rows: int, thresholds=None,
+                     first_checkpoint: int = 0, margin: float = 1e-3, pre_ids=None, draft_ids=None):
+        """The chunked vocabulary scan on Q8_K rows q8k = (d, qs, bsum):
+        (best_val, best_id, chunks_read, active, stopped)."""
+        d, qs, bs = (np.ascontiguousarray(a) for a in q8k)
+        M = qs.shape[0]
+        w = np.ascontiguousarray(w, np.uint8)
+        thr = None if thresholds is None else np.ascontiguousarray(thresholds, np.float32)
+        pre = None if pre_ids is None else np.ascontiguousarray(pre_ids, np.uint32)
+        dr = None if draft_ids is None else np.ascontiguousarray(draft_ids, np.uint32)
+        bv = np.empty(M, np.float32)
+        bi = np.empty(M, np.uint32)
+        act, stp = C.c_int(), C.c_int()
+        n = self.lib.qo_lm_head_scan(type_id, _ptr(w), vocab_rows, K, M, _ptr(d), _ptr(qs), _ptr(bs), chunk_rows,
+                                     None if thr is None else _ptr(thr), 0 if thr is None else thr.size,
+                                     first_checkpoint, margin, None if pre is None else _ptr(pre),
+                                     0 if pre is None else pre.size, None if dr is None else _ptr(dr), _ptr(bv),
+                                     _ptr(bi), C.byref(act), C.byref(stp))
+        if n < 0:
+            raise ValueError("oracle rejected the scan")
+        return bv, bi, n, act.value, stp.value
+
     def rmsnorm_q8k_f16(self, x16: np.ndarray, gamma16: np.ndarray):
         """rmsnorm_fp16_rows_fast on fp16 bits: (y16 [M][K], (d, qs, bsum32))."""
         x16 = np.ascontiguousarray(x16, dtype=np.uint16)
@@ -310,6 +346,10 @@ class Reference:
         L.ref_capacity_m.restype = C.c_int
         L.ref_dot_rows.restype = C.c_int
         L.ref_dot_rows.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p]
+        L.ref_dot_rows_float.restype = C.c_int
+        L.ref_dot_rows_float.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p]
+        L.ref_dequant_contiguous.restype = C.c_int
+        L.ref_dequant_contiguous.argtypes = [C.c_uint32, _p, C.c_size_t, _p]
         L.ref_swiglu_q8k.restype = C.c_int
         L.ref_swiglu_q8k.argtypes = [_p, _p, C.c_int, C.c_int, _p, _p, _p]
         L.ref_gguf_parse.restype = C.c_int
@@ -376,6 +416,25 @@ class Reference:
                                    1 if batch_kernel else 0, _ptr(out))
         if rc != 0:
             raise ValueError("outside the reference's static capacity")
+        return out
+
+    def dot_rows_float(self, type_id: int, w_row: np.ndarray, K: int, x16) -> np.ndarray:
+        """sdot_row_f32_batch / _f16_batch: one row against M fp16 rows [M, K]."""
+        x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+        if x16.ndim == 1:
+            x16 = x16[None, :]
+        M = x16.shape[0]
+        w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+        out = np.empty(M, np.float32)
+        if self.lib.ref_dot_rows_float(type_id, _ptr(w_row), M, K, _ptr(x16), _ptr(out)) != 0:
+            raise ValueError("outside the reference's static capacity")
+        return out
+
+    def dequant_contiguous(self, type_id: int, w: np.ndarray, n_elems: int) -> np.ndarray:
+        """dequant_contiguous_fast -> fp16 bits (any supported type, incl. F32 / F16)."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        out = np.zeros(n_elems, np.uint16)
+        self.lib.ref_dequant_contiguous(type_id, _ptr(w), n_elems, _ptr(out))
         return out
 
     def swiglu_q8k(self, gate16: np.ndarray, up16: np.ndarray):

@@ -228,13 +228,28 @@ void qo_dequant_block_q5_k(const uint8_t *blk, uint16_t *dst) {
     }
 }
 
-/* dequant_contiguous_fast, E:3856-3902 (single-threaded here). */
+/* dequant_contiguous_fast, E:3856-3902 (single-threaded here): F16 rows are
+ * copied (E:3857-3860), F32 values cast to fp16 (E:3876-3879). */
 int qo_dequant_rows(uint32_t type, const uint8_t *src, int64_t rows, int64_t cols,
                     uint16_t *dst) {
+    if (type == QO_TYPE_F16 || type == QO_TYPE_F32) {
+        if (cols <= 0 || rows < 0) return -1;
+        const size_t n = (size_t)rows * (size_t)cols;
+        if (type == QO_TYPE_F16) {
+            memcpy(dst, src, n * 2);
+        } else {
+            for (size_t i = 0; i < n; ++i) {
+                float f;
+                memcpy(&f, src + 4 * i, 4);
+                dst[i] = qo_f32_to_fp16(f);
+            }
+        }
+        return 0;
+    }
     const int64_t qk = (type == QO_TYPE_Q8_0) ? 32 : 256;
     if (cols <= 0 || rows < 0 || cols % qk) return -1;
     const uint64_t bbytes = qo_row_bytes(type, (uint64_t)qk);
-    if (bbytes == 0 || type == QO_TYPE_F32 || type == QO_TYPE_F16) return -1;
+    if (bbytes == 0) return -1;
     const int64_t units = rows * (cols / qk);
     for (int64_t b = 0; b < units; ++b) {
         const uint8_t *blk = src + (size_t)b * bbytes;
@@ -483,6 +498,22 @@ float qo_dot_row(uint32_t type, const uint8_t *w_row, int K, const float *dx,
     return acc;
 }
 
+/* sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440) for one activation
+ * row: acc += w[i] * (float)x[i] in row order, x the fp16 input. */
+float qo_dot_row_float(uint32_t type, const uint8_t *w_row, int K, const uint16_t *x16) {
+    float acc = 0.0f;
+    if (type == QO_TYPE_F32) {
+        for (int i = 0; i < K; ++i) {
+            float w;
+            memcpy(&w, w_row + 4 * (size_t)i, 4);
+            acc += w * qo_fp16_to_f32(x16[i]);
+        }
+    } else {
+        for (int i = 0; i < K; ++i) acc += qo_fp16_to_f32(rd16(w_row + 2 * (size_t)i)) * qo_fp16_to_f32(x16[i]);
+    }
+    return acc;
+}
+
 int qo_block_partials(uint32_t type, const uint8_t *w_row, int K, const int8_t *qs,
                       const int32_t *bsum32, int32_t *S, int32_t *Mb) {
     if (type == QO_TYPE_Q4_K || type == QO_TYPE_Q5_K) {
@@ -522,10 +553,12 @@ int qo_block_partials(uint32_t type, const uint8_t *w_row, int K, const int8_t *
 static int is_kquant(uint32_t t) {
     return t == QO_TYPE_Q4_K || t == QO_TYPE_Q5_K || t == QO_TYPE_Q6_K;
 }
+static int is_float(uint32_t t) { return t == QO_TYPE_F32 || t == QO_TYPE_F16; }
 
-/* exec_sdot_job_work_stealing's row loop (E:3582-3613), fp32 store. */
+/* exec_sdot_job_work_stealing's row loop (E:3582-3613), fp32 store; F32 /
+ * F16 rows read the fp16 input x16 [M][K] (E:3597-3601). */
 static void run_tasks(const float *q8k_d, const int8_t *q8k_qs, const int32_t *q8k_bsum,
-                      const float *q80_d, const int8_t *q80_qs, int M, int K,
+                      const float *q80_d, const int8_t *q80_qs, const uint16_t *x16, int M, int K,
                       const qo_matrix_task *tasks, int n_tasks, int total_rows) {
     const int nb256 = K / 256, nb32 = K / 32;
 #pragma omp parallel for schedule(dynamic, 64)
@@ -537,7 +570,9 @@ static void run_tasks(const float *q8k_d, const int8_t *q8k_qs, const int32_t *q
         const uint8_t *w_row = T->w_base + (size_t)lr * T->row_bytes;
         for (int m = 0; m < M; ++m) {
             float s;
-            if (T->type == QO_TYPE_Q8_0)
+            if (is_float(T->type))
+                s = qo_dot_row_float(T->type, w_row, K, x16 + (size_t)m * K);
+            else if (T->type == QO_TYPE_Q8_0)
                 s = qo_dot_row(T->type, w_row, K, q80_d + (size_t)m * nb32,
                                q80_qs + (size_t)m * K, NULL);
             else
@@ -550,10 +585,10 @@ static void run_tasks(const float *q8k_d, const int8_t *q8k_qs, const int32_t *q
 }
 
 static int check_tasks(int M, int K, qo_matrix_task *tasks, int n_tasks, int *need_q8k,
-                       int *need_q80, int *total_rows) {
+                       int *need_q80, int *need_x16, int *total_rows) {
     if (M <= 0 || K <= 0 || n_tasks <= 0 || !tasks) return -1;
     int tr = 0;
-    *need_q8k = *need_q80 = 0;
+    *need_q8k = *need_q80 = *need_x16 = 0;
     for (int t = 0; t < n_tasks; ++t) {
         if (tasks[t].cols != K) return -1;
         if (is_kquant(tasks[t].type)) {
@@ -562,6 +597,8 @@ static int check_tasks(int M, int K, qo_matrix_task *tasks, int n_tasks, int *ne
         } else if (tasks[t].type == QO_TYPE_Q8_0) {
             if (K % 32) return -1;
             *need_q80 = 1;
+        } else if (is_float(tasks[t].type)) {
+            *need_x16 = 1;
         } else {
             return -1;
         }
@@ -575,11 +612,16 @@ static int check_tasks(int M, int K, qo_matrix_task *tasks, int n_tasks, int *ne
 #include <stdlib.h>
 
 int qo_gemm_multi(const float *x, int M, int K, qo_matrix_task *tasks, int n_tasks) {
-    int need_q8k, need_q80, total_rows;
-    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &total_rows)) return -1;
+    int need_q8k, need_q80, need_x16, total_rows;
+    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &need_x16, &total_rows)) return -1;
     float *kd = NULL, *zd = NULL;
     int8_t *kq = NULL, *zq = NULL;
     int32_t *ks = NULL;
+    uint16_t *x16 = NULL;
+    if (need_x16) { /* the fp16 input itself, E:4206 */
+        x16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)M * K);
+        qo_f32_to_fp16_array(x, x16, (size_t)M * K);
+    }
     if (need_q8k) {
         kd = (float *)malloc(sizeof(float) * (size_t)M * (K / 256));
         kq = (int8_t *)malloc((size_t)M * K);
@@ -591,26 +633,29 @@ int qo_gemm_multi(const float *x, int M, int K, qo_matrix_task *tasks, int n_tas
         zq = (int8_t *)malloc((size_t)M * K);
         qo_quantize_q8_0_f32(x, M, K, zd, zq);
     }
-    run_tasks(kd, kq, ks, zd, zq, M, K, tasks, n_tasks, total_rows);
-    free(kd); free(kq); free(ks); free(zd); free(zq);
+    run_tasks(kd, kq, ks, zd, zq, x16, M, K, tasks, n_tasks, total_rows);
+    free(kd); free(kq); free(ks); free(zd); free(zq); free(x16);
     return 0;
 }
 
 int qo_gemm_multi_prequantized(const float *q8k_d, const int8_t *q8k_qs,
                                const int32_t *q8k_bsum, const float *q80_d,
-                               const int8_t *q80_qs, int M, int K,
+                               const int8_t *q80_qs, const uint16_t *x16, int M, int K,
                                qo_matrix_task *tasks, int n_tasks) {
-    int need_q8k, need_q80, total_rows;
-    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &total_rows)) return -1;
+    int need_q8k, need_q80, need_x16, total_rows;
+    if (check_tasks(M, K, tasks, n_tasks, &need_q8k, &need_q80, &need_x16, &total_rows)) return -1;
     if (need_q8k && (!q8k_d || !q8k_qs || !q8k_bsum)) return -1;
     if (need_q80 && (!q80_d || !q80_qs)) return -1;
-    run_tasks(q8k_d, q8k_qs, q8k_bsum, q80_d, q80_qs, M, K, tasks, n_tasks, total_rows);
+    if (need_x16 && !x16) return -1;
+    run_tasks(q8k_d, q8k_qs, q8k_bsum, q80_d, q80_qs, x16, M, K, tasks, n_tasks, total_rows);
     return 0;
 }
 
 /* ------------------------------------------------------------- swiglu -- */
 
-/* swiglu_chunk_worker scalar branch, E:4349-4356, then E:4357 requant. */
+/* swiglu_chunk_worker scalar branch, E:4349-4356, then E:4357 requant. Gate
+ * and up are fp16 in the reference (the dispatcher's outputs), so each fp32
+ * input is rounded to fp16 first (E:4352-4353). */
 void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                    float *d, int8_t *qs, int32_t *bsum32) {
     float hb[256];
@@ -619,8 +664,8 @@ void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
         for (int b = 0; b < nb; ++b) {
             const size_t off = (size_t)m * N + (size_t)b * 256;
             for (int i = 0; i < 256; ++i) {
-                const float g = gate[off + i];
-                const float u = up[off + i];
+                const float g = qo_fp16_to_f32(qo_f32_to_fp16(gate[off + i]));
+                const float u = qo_fp16_to_f32(qo_f32_to_fp16(up[off + i]));
                 hb[i] = (g / (1.0f + expf(-g))) * u;
             }
             if (h) memcpy(h + off, hb, sizeof(hb));
@@ -678,4 +723,87 @@ void qo_chunk_argmax(const float *logits, int M, int rows, size_t ldl, int round
         best_val[m] = bv;
         best_id[m] = bi;
     }
+}
+
+/* run_final_norm_and_lm_head_batch_sdot after its RMSNorm (E:11138-11256),
+ * without the script-specific extended rows: seed (-1e30, 0); the
+ * pre-evaluated rows (E:11143-11146) and each position's draft candidate
+ * (E:11147-11153) in fp32; then the chunks: fp16-rounded logits, strict >,
+ * positions < active only (E:11169-11183); the pruning (E:11203-11209); the
+ * checkpoint test (E:11244-11256). Q8_K rows for the K-quants, Q8_0 rows for
+ * Q8_0. Returns the number of chunks read; *active_out / *stopped_out get
+ * the final active count and whether a checkpoint ended the scan. */
+int qo_lm_head_scan(uint32_t type, const uint8_t *w, int vocab_rows, int K, int M, const float *xd,
+                    const int8_t *xqs, const int32_t *xbs, int chunk_rows, const float *thresholds,
+                    int n_thresholds, int first_checkpoint, float margin, const uint32_t *pre_ids, int n_pre,
+                    const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int *active_out,
+                    int *stopped_out) {
+    const size_t rb = (size_t)qo_row_bytes(type, (uint64_t)K);
+    const int nd = (type == QO_TYPE_Q8_0) ? K / 32 : K / 256;
+    float cand[4096];
+    if (M > 4096 || rb == 0) return -1;
+#define QO_DOT(row, p)                                                                                    \
+    qo_dot_row(type, w + (size_t)(row) * rb, K, xd + (size_t)(p) * nd, xqs + (size_t)(p) * K,          \
+               xbs ? xbs + (size_t)(p) * (K / 32) : NULL)
+    for (int p = 0; p < M; ++p) {
+        best_val[p] = -1e30f;
+        best_id[p] = 0;
+    }
+    for (int p = 0; p < M; ++p) {
+        for (int i = 0; i < n_pre; ++i) {
+            const uint32_t id = pre_ids[i];
+            const float v = id < (uint32_t)vocab_rows ? QO_DOT(id, p) : -1e30f;
+            if (v > best_val[p]) {
+                best_val[p] = v;
+                best_id[p] = id;
+            }
+        }
+        if (p + 1 < M && draft_ids) {
+            const uint32_t cid = draft_ids[p + 1];
+            const float vc = cid < (uint32_t)vocab_rows ? QO_DOT(cid, p) : -1e30f;
+            cand[p] = vc;
+            if (vc > best_val[p]) {
+                best_val[p] = vc;
+                best_id[p] = cid;
+            }
+        } else {
+            cand[p] = -1e30f;
+        }
+    }
+    int active = M, stopped = 0, c = 0;
+    const int nchunks = (vocab_rows + chunk_rows - 1) / chunk_rows;
+    for (c = 0; c < nchunks; ++c) {
+        const int r0 = c * chunk_rows;
+        const int rows = (r0 + chunk_rows > vocab_rows) ? vocab_rows - r0 : chunk_rows;
+        for (int p = 0; p < active; ++p)
+            for (int r = 0; r < rows; ++r) {
+                const float v = qo_fp16_to_f32(qo_f32_to_fp16(QO_DOT(r0 + r, p)));
+                if (v > best_val[p]) {
+                    best_val[p] = v;
+                    best_id[p] = (uint32_t)(r0 + r);
+                }
+            }
+        for (int p = 0; p + 1 < active; ++p) {
+            if (draft_ids && best_id[p] != draft_ids[p + 1] && best_val[p] > cand[p] + margin) {
+                active = p + 1;
+                break;
+            }
+        }
+        const float thresh = (c < n_thresholds) ? thresholds[c] : -1e30f;
+        int all_above = 1;
+        for (int p = 0; p < active; ++p)
+            if (best_val[p] < thresh) {
+                all_above = 0;
+                break;
+            }
+        if (n_thresholds > 0 && c >= first_checkpoint && all_above) {
+            stopped = 1;
+            ++c;
+            break;
+        }
+    }
+#undef QO_DOT
+    *active_out = active;
+    *stopped_out = stopped;
+    return c;
 }

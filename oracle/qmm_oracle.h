@@ -80,6 +80,11 @@ void qo_quantize_q8_0_f32(const float *x, int M, int K, float *d, int8_t *qs);
 float qo_dot_row(uint32_t type, const uint8_t *w_row, int K, const float *dx,
                  const int8_t *qs, const int32_t *bsum32);
 
+/* sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440): one F32 / F16
+ * weight row against one fp16 activation row x16 (bits), summed in row
+ * order. */
+float qo_dot_row_float(uint32_t type, const uint8_t *w_row, int K, const uint16_t *x16);
+
 /* Per-block exact integer partials of a K-quant row dot:
  *   Q4_K/Q5_K: S[b] = sum_j sc_j * dot_j, Mb[b] = sum_j m_j * bsum32_j
  *   Q6_K:      S[b] = sum_s sc_s * dot_s, Mb[b] = 0
@@ -111,15 +116,17 @@ typedef struct {
  * (OpenMP); each output is computed by one thread in reference order. */
 int qo_gemm_multi(const float *x, int M, int K, qo_matrix_task *tasks, int n_tasks);
 /* Same with caller-provided quantized activations (the prequantized path,
- * E:4186, E:4207-4208). q80_d / q80_qs may be NULL when no Q8_0 task. */
+ * E:4186, E:4207-4208). q80_d / q80_qs may be NULL when no Q8_0 task; x16
+ * (fp16 bits [M][K], the input the engine still passes, E:4206) may be NULL
+ * when no F32 / F16 task. */
 int qo_gemm_multi_prequantized(const float *q8k_d, const int8_t *q8k_qs,
                                const int32_t *q8k_bsum, const float *q80_d,
-                               const int8_t *q80_qs, int M, int K,
+                               const int8_t *q80_qs, const uint16_t *x16, int M, int K,
                                qo_matrix_task *tasks, int n_tasks);
 
-/* swiglu_chunk_worker (E:4326-4359) in the fp32 contract:
- * h = (g / (1 + expf(-g))) * u in fp32, then the fp32->fp16->Q8_K quantizer
- * per 256-value block. gate/up/h are [M][N]; h may be NULL. */
+/* swiglu_chunk_worker (E:4326-4359) in the fp32 contract: g and u rounded
+ * to fp16, h = (g / (1 + expf(-g))) * u in fp32, then the fp32->fp16->Q8_K
+ * quantizer per 256-value block. gate/up/h are [M][N]; h may be NULL. */
 void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                    float *d, int8_t *qs, int32_t *bsum32);
 
@@ -127,6 +134,18 @@ void qo_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
  * order, fp16-rounded values when round16, strict >; best_* updated in place. */
 void qo_chunk_argmax(const float *logits, int M, int rows, size_t ldl, int round16, const uint32_t *ids,
                      uint32_t row_base, float *best_val, uint32_t *best_id);
+
+/* run_final_norm_and_lm_head_batch_sdot's scan after its RMSNorm
+ * (E:11138-11256), script-specific rows left out: pre-evaluated rows and
+ * draft candidates (fp32), chunks of fp16-rounded logits (strict >), the
+ * speculative pruning and the checkpoint thresholds. x* are the Q8_K (or,
+ * for Q8_0 weights, Q8_0) activation arrays of M rows; xbs may be NULL for
+ * Q8_0. Returns the chunks read (-1 on bad arguments). */
+int qo_lm_head_scan(uint32_t type, const uint8_t *w, int vocab_rows, int K, int M, const float *xd,
+                    const int8_t *xqs, const int32_t *xbs, int chunk_rows, const float *thresholds,
+                    int n_thresholds, int first_checkpoint, float margin, const uint32_t *pre_ids, int n_pre,
+                    const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int *active_out,
+                    int *stopped_out);
 
 /* rmsnorm_fp16_rows_fast (E:4264-4314), scalar branch, on fp16 bits:
  * y [M][K] fp16 bits, then the Q8_K of each y row. K % 256 == 0. */

@@ -132,6 +132,35 @@ int ref_dot_rows(uint32_t type, const uint8_t *w_row, int M, int K, const float 
     return rc;
 }
 
+/* sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440): one F32 / F16
+ * weight row against M fp16 activation rows x16 [M][K] (the dispatcher's
+ * x_fp16, E:4206), the row the dispatcher selects at E:3597-3601. */
+int ref_dot_rows_float(uint32_t type, const uint8_t *w_row, int M, int K, const uint16_t *x16,
+                       float *out) {
+    if (M < 1 || M > SDOT_MAX_BATCH) return -1;
+    if (type != GGML_TYPE_F32 && type != GGML_TYPE_F16) return -1;
+    QuantizedBatchInput *Q = (QuantizedBatchInput *)calloc(1, sizeof(QuantizedBatchInput));
+    if (!Q) return -1;
+    Q->M = M;
+    Q->K = K;
+    Q->x_fp16 = (const __fp16 *)x16;
+    if (type == GGML_TYPE_F32) sdot_row_f32_batch(w_row, Q, M, K, out);
+    else sdot_row_f16_batch(w_row, Q, M, K, out);
+    free(Q);
+    return 0;
+}
+
+/* dequant_contiguous_fast (E:3856-3902) over n_elems values, on the calling
+ * thread: the turbo flag selects the serial branch (E:3867), since this
+ * harness starts no worker pool. */
+int ref_dequant_contiguous(uint32_t type, const uint8_t *src, size_t n_elems, uint16_t *dst) {
+    const int saved = Pool.turbo_active;
+    Pool.turbo_active = 1;
+    dequant_contiguous_fast(src, (__fp16 *)dst, type, n_elems);
+    Pool.turbo_active = saved;
+    return 0;
+}
+
 /* swiglu_chunk_worker (E:4326-4359) on fp16 gate/up [M][N]: gate is
  * overwritten with fp16(silu(g)*u) and the per-256 Q8_K requant (written by
  * the reference into g_sdot_input.q8k) is copied out. */

@@ -21,7 +21,8 @@ def test_header_declares_the_boundary():
     names = _declared_functions()
     for must in ("qmm_init", "qmm_gemm_multi_dispatch", "qmm_gemm_multi_dispatch_prequantized",
                  "qmm_quantize_q8k", "qmm_quantize_q8_0", "qmm_dequantize_f16", "qmm_swiglu_q8k",
-                 "qmm_weight_upload", "qmm_row_bytes"):
+                 "qmm_weight_upload", "qmm_row_bytes", "qmm_lm_head_scan", "qmm_eval_rows_argmax",
+                 "qmm_q8k_h_offset"):
         assert must in names
     assert len(names) >= 30
 
@@ -42,14 +43,19 @@ def test_row_bytes_and_layout_sizes():
     assert lib.qmm_row_bytes(8, 2560) == 2720
     assert lib.qmm_row_bytes(14, 9728) == 7980
     assert lib.qmm_row_bytes(12, 300) == 0  # not a multiple of 256
-    assert lib.qmm_row_bytes(1, 2560) == 0  # f16 is not on this path
+    assert lib.qmm_row_bytes(0, 2560) == 10240  # F32 rows (E:366)
+    assert lib.qmm_row_bytes(1, 2560) == 5120   # F16 rows (E:367)
+    assert lib.qmm_row_bytes(1, 40) == 0        # F32 / F16 K must be a multiple of 32
+    assert lib.qmm_row_bytes(2, 2560) == 0      # Q4_0: not on this path
     M, K = 3, 2560
     d_off, bs_off, total = lib.qmm_q8k_d_offset(M, K), lib.qmm_q8k_bsum_offset(M, K), lib.qmm_q8k_bytes(M, K)
     assert d_off >= M * K and d_off % 256 == 0
     assert bs_off >= d_off + 4 * M * K // 256 and bs_off % 256 == 0
     tile_off = lib.qmm_q8k_tile_offset(M, K)
     assert tile_off >= bs_off + 4 * M * K // 32 and tile_off % 256 == 0
-    assert total >= tile_off + 16 * K  # one 16-token tile for M = 3
+    h_off = lib.qmm_q8k_h_offset(M, K)
+    assert h_off >= tile_off + 16 * K and h_off % 256 == 0  # one 16-token tile for M = 3
+    assert total >= h_off + 2 * M * K
     assert lib.qmm_q8_0_d_offset(M, K) >= M * K and lib.qmm_q8_0_bytes(M, K) >= M * K + 4 * M * K // 32
     assert lib.qmm_q8k_bytes(0, K) == 0
 

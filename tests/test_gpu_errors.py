@@ -43,7 +43,7 @@ def test_valid_call_is_ok(ctx, bufs):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(type=1), qmm_hip.QMM_ETYPE),
+    (dict(type=2), qmm_hip.QMM_ETYPE),  # Q4_0: not on this path
     (dict(type=99), qmm_hip.QMM_ETYPE),
     (dict(cols=256), qmm_hip.QMM_ESHAPE),
     (dict(row_bytes=100), qmm_hip.QMM_ESHAPE),

@@ -66,7 +66,7 @@ def test_eval_rows(ctx, oracle, M):
     vb = ctx.malloc(M * len(ids) * 4)
     bv = ctx.upload(np.full(M, -1e30, np.float32))
     bi = ctx.upload(np.zeros(M, np.uint32))
-    ctx.eval_rows_argmax(qb, None, M, K, wb, TYPE_Q6_K, idb, len(ids), vb, bv, bi)
+    ctx.eval_rows_argmax(qb, None, M, K, wb, N, TYPE_Q6_K, idb, len(ids), vb, bv, bi)
     ctx.sync()
     vals, ev, ei = oracle.eval_rows_argmax(q, w, TYPE_Q6_K, K, ids, np.full(M, -1e30, np.float32),
                                            np.zeros(M, np.uint32))
@@ -118,7 +118,7 @@ def test_eval_rows_many(ctx, oracle):
     idb = ctx.upload(ids)
     bv = ctx.upload(np.full(1, -1e30, np.float32))
     bi = ctx.upload(np.zeros(1, np.uint32))
-    ctx.eval_rows_argmax(qb, None, 1, K, wb, TYPE_Q6_K, idb, len(ids), None, bv, bi)
+    ctx.eval_rows_argmax(qb, None, 1, K, wb, N, TYPE_Q6_K, idb, len(ids), None, bv, bi)
     ctx.sync()
     _, ev, ei = oracle.eval_rows_argmax(q, w, TYPE_Q6_K, K, ids, np.full(1, -1e30, np.float32),
                                         np.zeros(1, np.uint32))
@@ -151,3 +151,126 @@ def test_lm_head_nan_row(ctx, oracle):
     assert np.array_equal(got_i, ebi), (got_i, ebi)
     for b in (wb, bv, bi, qb):
         ctx.free(b)
+
+
+def test_eval_rows_past_the_tensor(ctx, oracle):
+    """Ids at or past tensor_rows are never read and count as -1e30 (E:11150):
+    the tensor is uploaded with 16 more rows than tensor_rows says, so the
+    ids past the bound still lie inside the allocation."""
+    N, K, M = 3000, 2560, 2
+    say("eval rows past the tensor")
+    w, q, qb = _setup(ctx, oracle, TYPE_Q6_K, N + 16, K, M, seed=770)
+    ids = np.array([5, N + 3, 17, N, N + 15, 9], np.uint32)
+    wb = ctx.weight_upload(w, TYPE_Q6_K, N + 16, K)
+    idb = ctx.upload(ids)
+    vb = ctx.malloc(M * len(ids) * 4)
+    for seed_v, label in ((-1e30, "seed -1e30"), (-np.inf, "seed -inf")):
+        bv = ctx.upload(np.full(M, seed_v, np.float32))
+        bi = ctx.upload(np.full(M, 123, np.uint32))
+        ctx.eval_rows_argmax(qb, None, M, K, wb, N, TYPE_Q6_K, idb, len(ids), vb, bv, bi)
+        ctx.sync()
+        vals = ctx.d2h(vb, np.float32, (M, len(ids)))
+        inb = [i for i, r in enumerate(ids) if r < N]
+        exp_vals, ev, ei = oracle.eval_rows_argmax(q, w, TYPE_Q6_K, K, ids[inb], np.full(M, seed_v, np.float32),
+                                                   np.full(M, 123, np.uint32))
+        assert np.array_equal(vals[:, inb].view(np.uint32), exp_vals.view(np.uint32)), label
+        assert np.all(vals[:, [1, 3, 4]] == np.float32(-1e30)), label
+        got_v, got_i = ctx.d2h(bv, np.float32, (M,)), ctx.d2h(bi, np.uint32, (M,))
+        assert np.array_equal(got_v.view(np.uint32), ev.view(np.uint32)), label
+        assert np.array_equal(got_i, ei), label
+        ctx.free(bv)
+        ctx.free(bi)
+    for b in (wb, idb, vb, qb):
+        ctx.free(b)
+
+
+# ------------------------------------------------- the chunked vocabulary scan
+import lm_plant  # noqa: E402
+
+V, CH = 20000, 4096  # 5 chunks
+
+
+def _scan(ctx, oracle, M, seed, plan, thresholds, first_checkpoint=0, pre=None, draft=None):
+    K = 2560
+    w = lm_plant.base_tensor(V + 16, K, seed)
+    x = synth.activations(M, K, seed=seed + 1)
+    q = oracle.quantize_q8k(x)
+    lm_plant.plant(w, oracle, q, plan, K)
+    qb = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.write_q8k(qb, *q, x16=oracle.f32_to_fp16(x))
+    wb = ctx.weight_upload(w, TYPE_Q6_K, V + 16, K)
+    bv, bi = ctx.malloc(M * 4), ctx.malloc(M * 4)
+    st = ctx.upload(np.full(4, -7, np.int32))
+    preb = ctx.upload(np.asarray(pre, np.uint32)) if pre is not None else None
+    drb = ctx.upload(np.asarray(draft, np.uint32)) if draft is not None else None
+    ctx.lm_head_scan(qb, None, M, K, wb, TYPE_Q6_K, V, CH, thresholds=thresholds, first_checkpoint=first_checkpoint,
+                     pre_ids=preb, n_pre=0 if pre is None else len(pre), draft_ids=drb, best_val=bv, best_id=bi,
+                     scan_state=st)
+    ctx.sync()
+    got = (ctx.d2h(bv, np.float32, (M,)), ctx.d2h(bi, np.uint32, (M,)), ctx.d2h(st, np.int32, (4,)))
+    exp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, thresholds, first_checkpoint, 1e-3, pre, draft)
+    for b in (qb, wb, bv, bi, st, preb, drb):
+        if b is not None:
+            ctx.free(b)
+    return got, exp
+
+
+def _same(got, exp, want_chunks, want_active, want_stopped):
+    (gv, gi, st), (ev, ei, n, act, stp) = got, exp
+    assert (n, act, stp) == (want_chunks, want_active, want_stopped)  # the plan's outcome, on the oracle
+    assert np.array_equal(gv.view(np.uint32), ev.view(np.uint32)), (gv, ev)
+    assert np.array_equal(gi, ei), (gi, ei)
+    assert list(st) == [n, act, stp, 0], st
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_scan_early_exit(ctx, oracle, M):
+    say(f"lm scan early exit M={M}")
+    T = lm_plant.CHUNK_THRESH
+    # every token above 19.5 in chunk 0: one chunk read
+    plan0 = [(5 + 11 * p, p, 25.0) for p in range(M)]
+    _same(*_scan(ctx, oracle, M, 910 + M, plan0, T), 1, M, 1)
+    # 14 in chunk 2 for every token: three chunks
+    plan2 = [(2 * CH + 77 + p, p, 14.0) for p in range(M)]
+    _same(*_scan(ctx, oracle, M, 920 + M, plan2, T), 3, M, 1)
+    # checkpoints from chunk 3 only: four chunks
+    _same(*_scan(ctx, oracle, M, 930 + M, plan0, T, first_checkpoint=3), 4, M, 1)
+    # no thresholds: all five chunks (the last one partial)
+    _same(*_scan(ctx, oracle, M, 940 + M, plan0, None), 5, M, 0)
+
+
+def test_scan_one_token_short_of_the_threshold(ctx, oracle):
+    """Two tokens above 19.5 in chunk 0, the third only at 17: not all above,
+    so chunk 0 does not end the scan; chunk 1's 16 does."""
+    say("lm scan one token short")
+    plan = [(5, 0, 25.0), (16, 1, 25.0), (27, 2, 17.0)]
+    _same(*_scan(ctx, oracle, 3, 950, plan, lm_plant.CHUNK_THRESH), 2, 3, 1)
+
+
+@pytest.mark.parametrize("M", [3, 4])
+def test_scan_candidates_and_pruning(ctx, oracle, M):
+    say(f"lm scan pruning M={M}")
+    draft = [0, 100, 200, 300][:M]
+    # token 0: its candidate (100) at 5, row 1500 (chunk 0) at 8: the active batch ends at 1 after chunk 0;
+    # the other tokens' chunk-1 rows at 12 are never seen
+    plan = [(100, 0, 5.0), (1500, 0, 8.0)] + [(CH + 10 * p, p, 12.0) for p in range(1, M)]
+    got, exp = _scan(ctx, oracle, M, 960 + M, plan, None, draft=draft)
+    _same(got, exp, 5, 1, 0)
+    assert int(got[1][0]) == 1500
+    # pre-evaluated end-of-text rows (fp32), and a candidate past the vocabulary (never read)
+    draft2 = [0, V + 7] + [400 + p for p in range(2, M)]
+    plan2 = [(V - 4, 0, 30.0), (CH + 10, 1, 12.0)]
+    got, exp = _scan(ctx, oracle, M, 970 + M, plan2, lm_plant.CHUNK_THRESH, pre=[V - 2, V - 4], draft=draft2)
+    assert int(got[1][0]) == V - 4
+    (ev, ei, n, act, stp) = exp
+    _same(got, exp, n, act, stp)
+
+
+def test_scan_stopped_chunks_read_no_weights(ctx, oracle):
+    """After a stop, the later chunks' launches return before touching their
+    rows: rows of chunks 1..4 that would hold every maximum change nothing."""
+    say("lm scan stop skips chunks")
+    plan = [(5, 0, 25.0), (CH + 1, 0, 60.0), (3 * CH + 2, 0, 70.0)]
+    got, exp = _scan(ctx, oracle, 1, 980, plan, lm_plant.CHUNK_THRESH)
+    _same(got, exp, 1, 1, 1)
+    assert int(got[1][0]) == 5

@@ -122,4 +122,34 @@ def test_gemm_multi_rejects_bad_tasks(oracle):
     with pytest.raises(ValueError):
         oracle.gemm_multi(x[:, :300], [dict(w=w, type=TYPE_Q4_K, rows=2)])
     with pytest.raises(ValueError):
-        oracle.gemm_multi(x, [dict(w=w, type=1, rows=2)])
+        oracle.gemm_multi(x, [dict(w=w, type=2, rows=2)])  # Q4_0 is not on this path
+
+
+def test_float_rows_closed_forms(oracle):
+    """F32 / F16 rows (E:3410-3440): unit weights sum the inputs exactly while
+    the partial sums stay integers below 2^24; the sum is in row order —
+    2^24 followed by ones stays 2^24 (each + 1 is a tie to even), where any
+    other order of the ones first would give 2^24 + 2k."""
+    K = 2560
+    x16 = np.ones(K, np.float16).view(np.uint16)
+    ones32 = np.ones(K, np.float32).view(np.uint8)
+    ones16 = np.ones(K, np.float16).view(np.uint8)
+    assert oracle.dot_row_float(0, ones32, K, x16) == K
+    assert oracle.dot_row_float(1, ones16, K, x16) == K
+    w = np.ones(K, np.float32)
+    w[0] = 2.0 ** 24
+    assert oracle.dot_row_float(0, w.view(np.uint8), K, x16) == 2.0 ** 24
+    w[0], w[-1] = 1.0, 2.0 ** 24
+    # ones first: the exact integer 2559, then one rounding of 2^24 + 2559
+    assert oracle.dot_row_float(0, w.view(np.uint8), K, x16) == np.float32(2.0 ** 24 + K - 1)
+
+
+@pytest.mark.parametrize("type_id", [0, 1])
+def test_float_rows_vs_fp64(oracle, type_id):
+    g = np.random.default_rng(11 + type_id)
+    K = 2048
+    x = g.standard_normal(K).astype(np.float16)
+    w = (g.standard_normal(K) * 0.1).astype(np.float32 if type_id == 0 else np.float16)
+    exact = float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+    got = oracle.dot_row_float(type_id, w.view(np.uint8), K, x.view(np.uint16))
+    assert abs(got - exact) <= K * 2.0 ** -23 * float(np.abs(w.astype(np.float64) * x).sum())

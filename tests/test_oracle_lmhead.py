@@ -58,3 +58,74 @@ def test_indexed_rows_report_ids(oracle):
     ids = np.array([50, 7, 9, 3], np.uint32)
     v, i = oracle.chunk_argmax(lg, np.array([-1e30], np.float32), np.zeros(1, np.uint32), False, ids, 0)
     assert v[0] == 3.0 and i[0] == 7
+
+
+# ---------------------------------------------------------------------------
+# The chunked vocabulary scan (E:11138-11256): outcomes fixed by planted
+# logits. Random rows give logits below 1; planted rows give chosen ones.
+import lm_plant  # noqa: E402
+import synth  # noqa: E402
+from oracle import TYPE_Q6_K  # noqa: E402
+
+V, CH, K = 20000, 4096, 2560  # 5 chunks, the last 3616 rows
+
+
+def _scan_setup(oracle, M, seed):
+    w = lm_plant.base_tensor(V + 16, K, seed)  # 16 rows past the vocabulary, never scanned
+    q = oracle.quantize_q8k(synth.activations(M, K, seed=seed + 1))
+    return w, q
+
+
+def test_scan_random_logits_stay_small(oracle):
+    w, q = _scan_setup(oracle, 1, 900)
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH)
+    assert abs(bv[0]) < 2.0 and n == 5 and stp == 0 and act == 1
+
+
+def test_scan_exits_at_the_first_met_threshold(oracle):
+    w, q = _scan_setup(oracle, 1, 901)
+    # 14 in chunk 2: below 19.5 and 16 (chunks 0, 1), above 13.5 (chunk 2)
+    (v,) = lm_plant.plant(w, oracle, q, [(2 * CH + 77, 0, 14.0)], K)
+    assert 13.5 < v < 16.0
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH)
+    assert (n, stp, int(bi[0])) == (3, 1, 2 * CH + 77)
+    assert bv[0] == np.float32(np.float16(v))  # chunk logits compare as fp16
+    # a chunk-0 row above 19.5 ends the scan after one chunk
+    lm_plant.plant(w, oracle, q, [(5, 0, 25.0)], K)
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH)
+    assert (n, stp, int(bi[0])) == (1, 1, 5)
+    # with the first checkpoint at chunk 3 (all chunks required up to it), chunk 3's 11.5 ends it
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH, first_checkpoint=3)
+    assert (n, stp, int(bi[0])) == (4, 1, 5)
+    # no thresholds: every chunk is read
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, None)
+    assert (n, stp, int(bi[0])) == (5, 0, 5)
+
+
+def test_scan_pre_rows_and_candidates(oracle):
+    M = 3
+    w, q = _scan_setup(oracle, M, 902)
+    eos = [V - 2, V - 4]
+    draft = np.array([0, 600, V + 7], np.uint32)  # token 1's candidate is past the vocabulary
+    (ve, vc) = lm_plant.plant(w, oracle, q, [(V - 4, 0, 30.0), (600, 0, 3.0)], K)
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, None, pre_ids=eos, draft_ids=draft)
+    # token 0: the second pre row (fp32 value) wins and no chunk beats it
+    assert int(bi[0]) == V - 4 and bv[0] == np.float32(ve)
+    # token 0's best is not its candidate (600) and beats it: the active batch ends at 1
+    assert act == 1 and n == 5
+
+
+def test_scan_pruning_freezes_later_positions(oracle):
+    M = 4
+    w, q = _scan_setup(oracle, M, 903)
+    draft = np.array([0, 100, 200, 300], np.uint32)
+    # token 0: its candidate 100 has logit 5, row 1500 (chunk 0) has 8 -> prune to 1 after chunk 0;
+    # tokens 1..3: rows in chunk 1 with 12 — never seen, since they are no longer active
+    plan = [(100, 0, 5.0), (1500, 0, 8.0), (CH + 10, 1, 12.0), (CH + 20, 2, 12.0), (CH + 30, 3, 12.0)]
+    lm_plant.plant(w, oracle, q, plan, K)
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, None, draft_ids=draft)
+    assert act == 1 and int(bi[0]) == 1500
+    assert all(bv[p] < 2.0 for p in (1, 2, 3))
+    # without draft ids nothing is pruned and the chunk-1 rows win
+    bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, None)
+    assert act == M and [int(i) for i in bi[1:]] == [CH + 10, CH + 20, CH + 30]

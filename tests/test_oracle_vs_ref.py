@@ -89,3 +89,45 @@ def test_swiglu_requant_matches_reference(oracle, ref):
     # both use the host libm expf; the reference stores h as fp16 (E:4355)
     assert np.array_equal(oracle.f32_to_fp16(h), h16)
     assert np.array_equal(d, d2) and np.array_equal(qs, qs2) and np.array_equal(bs, bs2)
+
+
+@pytest.mark.parametrize("type_id", [0, 1])
+@pytest.mark.parametrize("K", [32, 2560])
+def test_float_rows_match_reference(oracle, ref, type_id, K):
+    """sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440): bit for bit."""
+    g = np.random.default_rng(K + type_id)
+    x16 = (g.standard_normal((3, K)) * 2).astype(np.float16).view(np.uint16)
+    for r in range(3):
+        if type_id == 0:
+            row = (g.standard_normal(K) * 0.05).astype(np.float32).view(np.uint8)
+        else:
+            row = (g.standard_normal(K) * 0.05).astype(np.float16).view(np.uint8)
+        got = np.array([oracle.dot_row_float(type_id, row, K, x16[m]) for m in range(3)], np.float32)
+        exp = ref.dot_rows_float(type_id, row, K, x16)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("type_id", [0, 1])
+def test_float_dequant_matches_reference(oracle, ref, type_id):
+    """dequant_contiguous_fast of F32 / F16 rows (E:3857-3860, E:3876-3879)."""
+    g = np.random.default_rng(3 + type_id)
+    v = g.standard_normal(600) * 300
+    v[:6] = [65519.0, 65520.0, 1e-8, -6e-8, 0.0, -0.0]
+    with np.errstate(over="ignore"):  # 65520 and above round to inf in fp16
+        w = (v.astype(np.float32) if type_id == 0 else v.astype(np.float16)).view(np.uint8)
+    got = oracle.dequant_rows(type_id, w, 20, 30)
+    exp = ref.dequant_contiguous(type_id, w, 600)
+    assert np.array_equal(got.reshape(-1), exp)
+
+
+def test_swiglu_fp32_inputs_match_reference(oracle, ref):
+    """fp32 gate / up that are not fp16 values: the oracle rounds them to fp16
+    first, as the reference's gate / up are the dispatcher's fp16 outputs."""
+    g = np.random.default_rng(6)
+    gate = (g.standard_normal((2, 512)) * 3).astype(np.float32) + np.float32(1e-4)
+    up = g.standard_normal((2, 512)).astype(np.float32) * np.float32(1.0001)
+    assert not np.array_equal(gate.astype(np.float16).astype(np.float32), gate)
+    h16, (d, qs, bs) = ref.swiglu_q8k(oracle.f32_to_fp16(gate), oracle.f32_to_fp16(up))
+    h, (d2, qs2, bs2) = oracle.swiglu_q8k(gate, up)
+    assert np.array_equal(oracle.f32_to_fp16(h), h16)
+    assert np.array_equal(d, d2) and np.array_equal(qs, qs2) and np.array_equal(bs, bs2)
