@@ -231,6 +231,20 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K,
 int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80,
                                          int M, int K, qmm_matrix_task *tasks, int n_tasks);
 
+/* qmm_gemm_multi_dispatch that allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Results equal qmm_gemm_multi_dispatch's. At M >= 2 the quantized input
+ * goes to a device array of qmm_noalloc_scratch_bytes() (32 MiB) that each
+ * GPU holds from qmm_init to the end of the process; a call whose quantized
+ * input is larger (qmm_q8k_bytes(M, K) for K-quant / F32 / F16 tasks, plus
+ * qmm_q8_0_bytes(M, K) for Q8_0 tasks) fails with QMM_ESHAPE. All calls on
+ * one GPU share that array, which keeps the last call's contents: calls that
+ * overlap on one GPU (several contexts or streams at once) race. */
+int qmm_gemm_multi_dispatch_noalloc(qmm_context *ctx, const float *x, int M, int K,
+                                    qmm_matrix_task *tasks, int n_tasks);
+size_t qmm_noalloc_scratch_bytes(void);
+
 /* ---------------------------------------------------- graphs and timing */
 /* Capture the context stream's work into a HIP graph (hipStreamBeginCapture
  * / hipGraphInstantiate) and replay it; for launch-bound loops. */

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -20,8 +21,25 @@
 #include "../../include/qmm_hip.h"
 #include "qmm_device.h"
 
+// Device scratch of qmm_gemm_multi_dispatch_noalloc: the quantized input
+// of one call (its Q8_K section, then its Q8_0 section). Every GPU the
+// library runs on holds its own copy until the process ends. In host code
+// `scratch` names a host-side stand-in, never device memory: kernels and
+// copies get the device address that hipGetSymbolAddress returns for the
+// current device (scratch_on, filled at qmm_init).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_on[kMaxDevices] = {};  // the array's address on each device, once looked up
+}  // namespace
+
 struct qmm_context {
     int device = 0;
+    void *scratch = nullptr;  // this device's copy of `scratch` (nullptr: lookup failed)
+    std::string scratch_err;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     void *act = nullptr;  // Q8_K + Q8_0 activation buffers of the dispatcher
@@ -418,6 +436,23 @@ int qmm_init(int device, qmm_context **out_ctx) {
         delete ctx;
         return QMM_EHIP;
     }
+    // the device address of `scratch`, looked up once per device with that
+    // device current; a failed lookup disables only the no-allocation entry
+    if (device < kMaxDevices) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch_on[device]) {
+            void *ptr = nullptr;
+            e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e == hipSuccess && ptr) g_scratch_on[device] = ptr;
+            else {
+                (void)hipGetLastError();
+                ctx->scratch_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+            }
+        }
+        ctx->scratch = g_scratch_on[device];
+    } else {
+        ctx->scratch_err = "device index beyond the scratch table";
+    }
     ctx->stream = ctx->own_stream;
     *out_ctx = ctx;
     return QMM_OK;
@@ -627,6 +662,40 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
         return hip_fail(ctx, e, "quantize_q8_0 launch");
     return run_tasks(ctx, nullptr, q8k, q80, M, K, tasks, n_tasks);
 }
+
+int qmm_gemm_multi_dispatch_noalloc(qmm_context *ctx, const float *x, int M, int K, qmm_matrix_task *tasks,
+                                    int n_tasks) {
+    if (!ctx) return QMM_EINVAL;
+    if (!x) return fail(ctx, QMM_EINVAL, "null x");
+    bool need_q8k, need_q80;
+    int rc = check_tasks(ctx, M, K, tasks, n_tasks, &need_q8k, &need_q80);
+    if (rc) return rc;
+    if (!aligned(x, 16)) return fail(ctx, QMM_EALIGN, "x must be 16-B aligned");
+    if (M == 1) {  // the batch-1 kernels quantize x themselves: no scratch
+        if ((rc = use_device(ctx))) return rc;
+        return run_tasks(ctx, x, nullptr, nullptr, M, K, tasks, n_tasks);
+    }
+    const size_t k_bytes = need_q8k ? qmm::Q8KLayout(M, K).total : 0;
+    const size_t z_bytes = need_q80 ? qmm::Q80Layout(M, K).total : 0;
+    if (k_bytes + z_bytes > kScratchBytes)
+        return fail(ctx, QMM_ESHAPE,
+                    "the quantized input of M x K = " + std::to_string(M) + " x " + std::to_string(K) + " needs " +
+                        std::to_string(k_bytes + z_bytes) + " bytes, more than the " + std::to_string(kScratchBytes) +
+                        "-byte device scratch of the no-allocation dispatch");
+    if (!ctx->scratch) return fail(ctx, QMM_EHIP, "no device scratch: " + ctx->scratch_err);
+    if ((rc = use_device(ctx))) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->scratch);
+    void *q8k = need_q8k ? base : nullptr;
+    void *q80 = need_q80 ? base + k_bytes : nullptr;  // (k_bytes is a multiple of 256)
+    hipError_t e;
+    if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "quantize_q8k launch");
+    if (need_q80 && (e = qmm::launch_quantize_q8_0(x, M, K, q80, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "quantize_q8_0 launch");
+    return run_tasks(ctx, nullptr, q8k, q80, M, K, tasks, n_tasks);
+}
+
+size_t qmm_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80, int M,
                                          int K, qmm_matrix_task *tasks, int n_tasks) {
