@@ -254,6 +254,13 @@ int qmm_graph_launch(qmm_context *ctx, void *graph_exec);
 /* Waits for the context's stream, then destroys the graph; buffers the
  * context replaced while graphs were alive are freed with the last one. */
 int qmm_graph_destroy(qmm_context *ctx, void *graph_exec);
+/* The HBM read floor (measurement only; no counterpart in the reference):
+ * stream `bytes` from src (16-B aligned) with 16-B non-temporal loads over
+ * `workgroups` workgroups of 4 waves, each wave holding loads_per_wave
+ * (1, 2, 4 or 8) 1-KB loads in flight; one folded word per workgroup goes
+ * to sink[workgroups]. */
+int qmm_stream_read(qmm_context *ctx, const void *src, size_t bytes, int workgroups, int loads_per_wave,
+                    uint32_t *sink);
 /* HIP events on the context stream: begin records, end records and waits,
  * returning the elapsed milliseconds. */
 int qmm_timer_begin(qmm_context *ctx);

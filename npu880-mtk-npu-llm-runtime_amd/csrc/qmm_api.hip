@@ -822,6 +822,18 @@ int qmm_graph_end(qmm_context *ctx, void **graph_exec) {
     return QMM_OK;
 }
 
+int qmm_stream_read(qmm_context *ctx, const void *src, size_t bytes, int workgroups, int loads_per_wave,
+                    uint32_t *sink) {
+    if (!ctx) return QMM_EINVAL;
+    if (!src || !sink || bytes == 0 || workgroups <= 0 || workgroups > (1 << 20))
+        return fail(ctx, QMM_EINVAL, "bad stream_read arguments");
+    if (!aligned(src, 16) || !aligned(sink, 4)) return fail(ctx, QMM_EALIGN, "src must be 16-B aligned");
+    int rc = use_device(ctx);
+    if (rc) return rc;
+    const hipError_t e = qmm::launch_stream_read(src, bytes, workgroups, loads_per_wave, sink, ctx->stream);
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "stream_read launch");
+}
+
 int qmm_graph_launch(qmm_context *ctx, void *graph_exec) {
     if (!ctx || !graph_exec) return fail(ctx, QMM_EINVAL, "bad graph_launch arguments");
     hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), ctx->stream);

@@ -152,6 +152,9 @@ hipError_t launch_argmax_partials(float *logits, int M, int rows, size_t ldl, vo
 int argmax_slices(int rows);
 hipError_t launch_dequant_f16(const uint8_t *w, uint32_t type, int64_t rows, int64_t cols,
                               uint16_t *dst, hipStream_t s);
+// the streaming-read floor (qmm_stream.hip): loads_per_wave in {1, 2, 4, 8}
+hipError_t launch_stream_read(const void *src, size_t bytes, int workgroups, int loads_per_wave, uint32_t *sink,
+                              hipStream_t s);
 // M = 1 GEMV. x32 != nullptr: fp32 activations quantized inside the kernel;
 // otherwise xk / x0 hold the prequantized row.
 hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,

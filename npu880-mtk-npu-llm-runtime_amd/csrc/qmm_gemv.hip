@@ -636,8 +636,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(std::conditional_t<GRP, MatGr
 // ------------------------------------------------------- F32 / F16 rows
 // sdot_row_f32_batch / sdot_row_f16_batch (E:3410-3440) on the fp16 input
 // (x32 rounded to fp16, or the h section of a Q8_K buffer): wave w of
-// workgroup bx takes rows (4 bx + w) R .. + R; a lane takes the 16-B pieces
-// lane, lane + 64, ... of a row, forms each product w * x in fp32 and adds
+// workgroup bx takes rows (4 bx + w) R .. + R. A lane takes the 16-B pieces
+// lane, lane + 64, ... of a row: the wave loads its pieces of the input once
+// (NP per lane at a time: all of K = 2560), then streams its rows two at a
+// time, every load of both rows issued before any product. Each lane adds
 // its products in order, and the wave adds the 64 lane sums by a fixed
 // butterfly. The sums' order is not the reference's row order: these
 // outputs meet the stated tolerance, not bit equality.
@@ -647,10 +649,8 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 template <bool F16W, bool FUSED>
-__device__ inline void float_piece(const uint8_t *wr, const float *x32, const uint16_t *xh, int p, float &acc) {
-    constexpr int V = F16W ? 8 : 4;  // values per 16-B piece of the row
-    const uint4 wq = ld16_nt(wr + 16 * p);
-    float xv[V], wv[V];
+__device__ inline void float_x_piece(const float *x32, const uint16_t *xh, int p, float (&xv)[F16W ? 8 : 4]) {
+    constexpr int V = F16W ? 8 : 4;
     if constexpr (FUSED) {
 #pragma unroll
         for (int h = 0; h < V / 4; ++h) {
@@ -675,51 +675,77 @@ __device__ inline void float_piece(const uint8_t *wr, const float *x32, const ui
             xv[2 * i + 1] = fp16_bits_to_f32(hw[i] >> 16);
         }
     }
+}
+template <bool F16W>
+__device__ inline float float_piece_dot(const uint4 &wq, const float (&xv)[F16W ? 8 : 4], float acc) {
     const uint32_t ww[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         if constexpr (F16W) {
-            wv[2 * i] = fp16_bits_to_f32(ww[i] & 0xFFFFu);
-            wv[2 * i + 1] = fp16_bits_to_f32(ww[i] >> 16);
+            const float p0 = fp16_bits_to_f32(ww[i] & 0xFFFFu) * xv[2 * i];  // E:3436 (products rounded, then added)
+            acc = acc + p0;
+            const float p1 = fp16_bits_to_f32(ww[i] >> 16) * xv[2 * i + 1];
+            acc = acc + p1;
         } else {
-            wv[i] = __builtin_bit_cast(float, ww[i]);
+            const float p0 = __builtin_bit_cast(float, ww[i]) * xv[i];  // E:3420
+            acc = acc + p0;
         }
     }
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const float pr = wv[i] * xv[i];  // E:3420 / E:3436 (products rounded, then added)
-        acc = acc + pr;
-    }
+    return acc;
 }
 template <bool F16W, int R, bool FUSED>
 __device__ __attribute__((always_inline)) inline void gemv_float_wg(const MatArgs &a, int bx, const float *x32,
                                                                     const uint16_t *xh) {
     constexpr int V = F16W ? 8 : 4;
+    constexpr int NP = F16W ? 5 : 10;  // pieces per lane held at once (K = 2560)
     if (scan_stopped(a.scan)) return;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int npc = a.K / V;
-    for (int i = 0; i < R; ++i) {
-        const int row = (bx * 4 + wid) * R + i;
-        if (row >= a.N) break;  // the same in every lane of the wave
-        const uint8_t *wr = a.w + size_t(row) * a.row_bytes;
-        float acc = 0.0f;
-        int p = lane;
-        for (; p + 192 < npc; p += 256) {
-            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;  // (pieces in order: summed in order below)
-            float_piece<F16W, FUSED>(wr, x32, xh, p, a0);
-            float_piece<F16W, FUSED>(wr, x32, xh, p + 64, a1);
-            float_piece<F16W, FUSED>(wr, x32, xh, p + 128, a2);
-            float_piece<F16W, FUSED>(wr, x32, xh, p + 192, a3);
-            acc = acc + a0;
-            acc = acc + a1;
-            acc = acc + a2;
-            acc = acc + a3;
+    const int npc = a.K / V;            // pieces per row
+    const int row0 = (bx * 4 + wid) * R;
+    const int nrows = max(0, min(R, a.N - row0));
+    if (nrows == 0) return;  // the same in every lane of the wave
+    float acc[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[j] = 0.0f;
+    for (int b0 = 0; b0 < npc; b0 += 64 * NP) {
+        float xv[NP][V];
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int p = b0 + lane + 64 * i;
+            if (p < npc) float_x_piece<F16W, FUSED>(x32, xh, p, xv[i]);
         }
-        for (; p < npc; p += 64) float_piece<F16W, FUSED>(wr, x32, xh, p, acc);
-        acc = wave_sum(acc);
+#pragma unroll
+        for (int j = 0; j < R; j += 2) {
+            if (j >= nrows) break;  // the same in every lane of the wave
+            const bool two = j + 1 < nrows;
+            const uint8_t *w0 = a.w + size_t(row0 + j) * a.row_bytes;
+            const uint8_t *w1 = a.w + size_t(row0 + (two ? j + 1 : j)) * a.row_bytes;
+            uint4 q0[NP], q1[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = b0 + lane + 64 * i;
+                if (p < npc) {
+                    q0[i] = ld16_nt(w0 + 16 * size_t(p));
+                    q1[i] = ld16_nt(w1 + 16 * size_t(p));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = b0 + lane + 64 * i;
+                if (p < npc) {
+                    acc[j] = float_piece_dot<F16W>(q0[i], xv[i], acc[j]);
+                    if (j + 1 < R) acc[j + 1] = float_piece_dot<F16W>(q1[i], xv[i], acc[j + 1]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        if (j >= nrows) break;
+        const float v = wave_sum(acc[j]);
         if (lane == 0) {
-            if (a.res) acc = acc + a.res[row];
-            a.y[row] = acc;
+            const int row = row0 + j;
+            a.y[row] = a.res ? v + a.res[row] : v;
         }
     }
 }

@@ -1112,17 +1112,13 @@ __device__ inline f32x4v float_tile(const MatArgs &a, int n0, int m0, int k0, in
     const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
     const uint8_t *wr = a.w + size_t(min(n0 + nl, a.N - 1)) * a.row_bytes;
     const uint16_t *xr = xh + size_t(min(m0 + nl, a.M - 1)) * size_t(a.K);
-    if constexpr (F16W) {
-        for (int k = k0 + 8 * cl; k < k1; k += 32) {
-            const uint4 wq = ld16_nt(wr + 2 * size_t(k));
-            const uint4 xq = ld16(xr + k);
+    constexpr int KQ = F16W ? 32 : 16;  // k per step of the 4 lane groups
+    constexpr int U = 8;                // steps whose loads are issued together
+    auto step = [&](const uint4 &wq, const uint4 &xq) __attribute__((always_inline)) {
+        if constexpr (F16W) {
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8v, xq), __builtin_bit_cast(f16x8v, wq),
                                                          acc, 0, 0, 0);
-        }
-    } else {
-        for (int k = k0 + 4 * cl; k < k1; k += 16) {
-            const uint4 wq = ld16_nt(wr + 4 * size_t(k));
-            const uint2 xq = ld8(xr + k);
+        } else {
             const float xv[4] = {fp16_bits_to_f32(xq.x & 0xFFFFu), fp16_bits_to_f32(xq.x >> 16),
                                  fp16_bits_to_f32(xq.y & 0xFFFFu), fp16_bits_to_f32(xq.y >> 16)};
             const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
@@ -1130,51 +1126,54 @@ __device__ inline f32x4v float_tile(const MatArgs &a, int n0, int m0, int k0, in
             for (int i = 0; i < 4; ++i)
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], __builtin_bit_cast(float, wv[i]), acc, 0, 0, 0);
         }
+    };
+    auto load = [&](int k, uint4 &wq, uint4 &xq) __attribute__((always_inline)) {
+        if constexpr (F16W) {
+            wq = ld16_nt(wr + 2 * size_t(k + 8 * cl));
+            xq = ld16(xr + k + 8 * cl);
+        } else {
+            wq = ld16_nt(wr + 4 * size_t(k + 4 * cl));
+            const uint2 h = ld8(xr + k + 4 * cl);
+            xq = make_uint4(h.x, h.y, 0u, 0u);
+        }
+    };
+    int k = k0;
+    for (; k + U * KQ <= k1; k += U * KQ) {
+        uint4 wq[U], xq[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load(k + u * KQ, wq[u], xq[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) step(wq[u], xq[u]);
+    }
+    for (; k < k1; k += KQ) {
+        uint4 wq, xq;
+        load(k, wq, xq);
+        step(wq, xq);
     }
     return acc;
 }
 
-// One F32 / F16 task for M >= 2: workgroup (bx, by) owns rows 16 bx ..
-// +15 and, per wave w, tokens 64 by + 16 w .. +15, over all of K.
-template <bool F16W>
-__global__ __launch_bounds__(256) void float_tile_kernel(MatGroup grp, Q8KView x) {
-    int bx = 0;
-    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
-    const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
-    const int n0 = bx * 16, m0 = (int(blockIdx.y) * 4 + int(threadIdx.x >> 6)) * 16;
-    if (m0 >= a.M || scan_stopped(a.scan)) return;  // the same in every lane of the wave
-    f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = float_tile<F16W>(a, n0, m0, 0, a.K, x.h, acc);
-    const int n = n0 + nl;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int tok = m0 + 4 * cl + r;
-        if (tok < a.M && n < a.N) {
-            float v = acc[r];
-            if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
-            a.y[size_t(tok) * a.ldy + n] = v;
-        }
-    }
-}
-
-// The part kernel's shape for an F32 / F16 task (one 16-row tile, all 16 TT
-// tokens, wave kp = the kp-th quarter of K): the four quarters' sums meet in
-// LDS and are added in quarter order, as the k-quant parts are.
+// An F32 / F16 task in the part kernel's shape: one 16-row tile and the
+// 16 TT tokens from m0, wave kp taking the kp-th quarter of K; the four
+// quarters' sums meet in LDS and are added in quarter order, as the k-quant
+// parts are. Token tiles past M are skipped.
 template <bool F16W, int TT>
-__device__ __attribute__((always_inline)) inline void part_float_wg(const MatArgs &a, int bx, const Q8KView &x) {
+__device__ __attribute__((always_inline)) inline void part_float_wg(const MatArgs &a, int bx, const Q8KView &x,
+                                                                    int m0 = 0) {
     extern __shared__ __align__(16) uint8_t lds[];
     if (scan_stopped(a.scan)) return;
     const int lane = threadIdx.x & 63, nl = lane & 15, cl = lane >> 4;
     const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = bx * 16;
-    constexpr int KQ = F16W ? 32 : 16;  // values per k step of a lane group
+    constexpr int KQ = F16W ? 32 : 16;  // values per k step of the 4 lane groups
     const int steps = a.K / KQ;
     const int k0 = (kp * steps / 4) * KQ, k1 = ((kp + 1) * steps / 4) * KQ;
     float *terms = reinterpret_cast<float *>(lds);  // [part][token tile][r][lane]
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
+        if (m0 + 16 * t >= a.M) break;  // the same in every lane
         f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        acc = float_tile<F16W>(a, n0, 16 * t, k0, k1, x.h, acc);
+        acc = float_tile<F16W>(a, n0, m0 + 16 * t, k0, k1, x.h, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r) terms[((kp * TT + t) * 4 + r) * 64 + lane] = acc[r];
     }
@@ -1182,15 +1181,25 @@ __device__ __attribute__((always_inline)) inline void part_float_wg(const MatArg
     const int n = n0 + nl;
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
+        if (m0 + 16 * t >= a.M) break;
         float v = 0.0f;
 #pragma unroll
         for (int p = 0; p < 4; ++p) v = v + terms[((p * TT + t) * 4 + kp) * 64 + lane];
-        const int tok = 16 * t + 4 * cl + kp;
+        const int tok = m0 + 16 * t + 4 * cl + kp;
         if (tok < a.M && n < a.N) {
             if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
             a.y[size_t(tok) * a.ldy + n] = v;
         }
     }
+}
+
+// One F32 / F16 task (or several of one type) for M >= 2: workgroup (bx, by)
+// owns rows 16 bx .. +15 and tokens 64 by .. +63 over all of K.
+template <bool F16W>
+__global__ __launch_bounds__(256) void float_tile_kernel(MatGroup grp, Q8KView x) {
+    int bx = 0;
+    const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
+    part_float_wg<F16W, 4>(a, bx, x, int(blockIdx.y) * 64);
 }
 
 // ================================================ several formats at once
@@ -1439,8 +1448,9 @@ static hipError_t launch_float(uint32_t type, const MatArgs *tasks, int n, const
         g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
     }
     const dim3 grid(unsigned(g.wg0[n]), unsigned((tasks[0].M + 63) / 64));
-    if (type == kF16) hipLaunchKernelGGL((float_tile_kernel<true>), grid, dim3(256), 0, s, g, x);
-    else hipLaunchKernelGGL((float_tile_kernel<false>), grid, dim3(256), 0, s, g, x);
+    const size_t lds = 4 * 4 * 1024;  // the four parts' sums of 4 token tiles
+    if (type == kF16) hipLaunchKernelGGL((float_tile_kernel<true>), grid, dim3(256), lds, s, g, x);
+    else hipLaunchKernelGGL((float_tile_kernel<false>), grid, dim3(256), lds, s, g, x);
     return hipGetLastError();
 }
 

@@ -111,6 +111,7 @@ _SIGNATURES = [
     ("qmm_graph_end", C.c_int, [_p, C.POINTER(_p)]),
     ("qmm_graph_launch", C.c_int, [_p, _p]),
     ("qmm_graph_destroy", C.c_int, [_p, _p]),
+    ("qmm_stream_read", C.c_int, [_p, _p, C.c_size_t, C.c_int, C.c_int, _p]),
     ("qmm_timer_begin", C.c_int, [_p]),
     ("qmm_timer_end", C.c_int, [_p, C.POINTER(C.c_float)]),
 ]
@@ -452,6 +453,9 @@ class Context:
 
     def graph_launch(self, g: int):
         self._call("qmm_graph_launch", self._h, _p(g))
+
+    def stream_read(self, src, nbytes: int, workgroups: int, loads_per_wave: int, sink):
+        self._call("qmm_stream_read", self._h, _p(_addr(src)), nbytes, workgroups, loads_per_wave, _p(_addr(sink)))
 
     def graph_destroy(self, g: int):
         self._call("qmm_graph_destroy", self._h, _p(g))

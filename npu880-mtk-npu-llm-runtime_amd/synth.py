@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
+TYPE_F32, TYPE_F16 = 0, 1
 TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 8, 12, 13, 14
 BLOCK_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
 BLOCK_VALUES = {TYPE_Q8_0: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256, TYPE_Q6_K: 256}
@@ -62,7 +63,48 @@ def activations(M: int, K: int, seed: int) -> np.ndarray:
 
 
 def row_bytes(type_id: int, cols: int) -> int:
+    if type_id in (TYPE_F32, TYPE_F16):
+        return cols * (4 if type_id == TYPE_F32 else 2)
     return (cols // BLOCK_VALUES[type_id]) * BLOCK_BYTES[type_id]
+
+
+def float_rows(type_id: int, rows: int, cols: int, seed: int) -> np.ndarray:
+    """F32 / F16 weight rows ~N(0, 0.05^2) as bytes [rows * row_bytes]."""
+    v = rng(seed).standard_normal((rows, cols), dtype=np.float32) * np.float32(0.05)
+    return (v if type_id == TYPE_F32 else v.astype(np.float16)).view(np.uint8).reshape(-1)
+
+
+def q6k_row_following(x: np.ndarray, target: float) -> np.ndarray:
+    """One Q6_K row (K = x.size) whose codes follow x — per block
+    q - 32 = round(31 x / max|x|), every scale 16 — with the fp16 d that puts
+    its fp32 dot with x near `target` (the dot with x's Q8_K codes differs by
+    the quantization error, about 1 %)."""
+    K = x.size
+    xb = x.astype(np.float64).reshape(K // 256, 256)
+    q = np.clip(np.rint(31.0 * xb / np.maximum(np.abs(xb).max(axis=1, keepdims=True), 1e-12)), -32, 31)
+    d = float(np.float16(target / (16.0 * float(np.sum(q * xb)))))
+    codes = (q + 32).astype(np.uint8)  # [block][256], value k = 128 half + 32 i + l
+    out = np.zeros((K // 256, 210), np.uint8)
+    c = codes.reshape(-1, 2, 4, 32)  # block, half, i, l
+    for h in range(2):
+        out[:, 64 * h:64 * h + 32] = (c[:, h, 0] & 15) | ((c[:, h, 2] & 15) << 4)
+        out[:, 64 * h + 32:64 * h + 64] = (c[:, h, 1] & 15) | ((c[:, h, 3] & 15) << 4)
+        out[:, 128 + 32 * h:160 + 32 * h] = ((c[:, h, 0] >> 4) | ((c[:, h, 1] >> 4) << 2) | ((c[:, h, 2] >> 4) << 4)
+                                             | ((c[:, h, 3] >> 4) << 6))
+    out[:, 192:208] = 16
+    out[:, 208:210] = np.array([d], np.float16).view(np.uint8)
+    return out.reshape(-1)
+
+
+def lm_head_small_logits(rows: int, cols: int, seed: int) -> np.ndarray:
+    """A Q6_K vocabulary tensor of random rows with fp16 d ~U[0.5e-5, 1.5e-5]:
+    every random logit of an N(0, 1) input stays below about 1."""
+    w = weights(TYPE_Q6_K, rows, cols, seed=seed).copy()
+    nb = rows * (cols // 256)
+    blk = w.reshape(nb, 210)
+    d = rng(seed + 1).uniform(0.5e-5, 1.5e-5, nb).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return w
 
 
 # The benchmark workloads: (type, rows N, cols K) per tensor.

@@ -357,7 +357,8 @@ class Reference:
         L.ref_rmsnorm_q8k.restype = C.c_int
         L.ref_rmsnorm_q8k.argtypes = [_p, _p, _p, C.c_int, C.c_int, _p, _p, _p]
         L.ref_bench_gemv.restype = C.c_double
-        L.ref_bench_gemv.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, C.c_int, C.c_int]
+        L.ref_bench_gemv.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, _p, _p, C.c_int, C.c_int, C.c_int,
+                                     C.c_size_t]
         self.max_k = L.ref_capacity_k()
         self.max_m = L.ref_capacity_m()
 
@@ -487,11 +488,14 @@ class Reference:
         return y, (d, qs, bs)
 
     def bench_gemv(self, type_id: int, w: np.ndarray, N: int, K: int, x16: np.ndarray,
-                   threads: int, iters: int):
+                   threads: int, iters: int, replicas: int = 1):
+        """Wall seconds of `iters` GEMVs; w holds `replicas` copies of the
+        tensor back to back, pass i reads copy i mod replicas."""
         w = np.ascontiguousarray(w, dtype=np.uint8)
         x16 = np.ascontiguousarray(x16, dtype=np.uint16)
         y = np.empty(N, np.float32)
-        t = self.lib.ref_bench_gemv(type_id, _ptr(w), N, K, _ptr(x16), _ptr(y), threads, iters)
+        stride = w.size // replicas
+        t = self.lib.ref_bench_gemv(type_id, _ptr(w), N, K, _ptr(x16), _ptr(y), threads, iters, replicas, stride)
         if t < 0:
             raise ValueError("bench_gemv rejected its arguments")
         return t, y

@@ -237,7 +237,10 @@ int ref_gguf_parse(const uint8_t *buf, size_t size, uint64_t *alignment, uint64_
  * quantize_row_fp16_to_q8_k of x once, then eval_single_lm_row_dot per
  * weight row — with rows split over `threads` pthreads in grains of
  * SDOT_ROW_GRAIN rows (the reference's row grain, E:866). Runs `iters`
- * passes and returns the wall time in seconds (CLOCK_MONOTONIC).
+ * passes, pass i on weight replica i mod replicas (replicas copies of the
+ * tensor, `stride` bytes apart, so that the weights stream from DRAM rather
+ * than the last-level cache), and returns the wall time in seconds
+ * (CLOCK_MONOTONIC).
  * ------------------------------------------------------------------------- */
 typedef struct {
     const uint8_t *w;
@@ -263,8 +266,8 @@ static void *bench_worker(void *arg) {
 }
 
 double ref_bench_gemv(uint32_t type, const uint8_t *w, int N, int K, const uint16_t *x_f16,
-                      float *y, int threads, int iters) {
-    if (threads < 1 || threads > 256 || K > SDOT_MAX_K || K % 256) return -1.0;
+                      float *y, int threads, int iters, int replicas, size_t stride) {
+    if (threads < 1 || threads > 256 || K > SDOT_MAX_K || K % 256 || replicas < 1) return -1.0;
     if (type != GGML_TYPE_Q4_K && type != GGML_TYPE_Q5_K && type != GGML_TYPE_Q6_K) return -1.0;
     QuantizedBatchInput *Q = (QuantizedBatchInput *)calloc(1, sizeof(QuantizedBatchInput));
     if (!Q) return -1.0;
@@ -276,7 +279,8 @@ double ref_bench_gemv(uint32_t type, const uint8_t *w, int N, int K, const uint1
         Q->M = 1;
         Q->K = K;
         int cursor = 0;
-        BenchShared s = {w, type, ggml_row_bytes(type, (size_t)K), N, K, Q, y, &cursor};
+        BenchShared s = {w + (size_t)(it % replicas) * stride, type, ggml_row_bytes(type, (size_t)K), N, K, Q, y,
+                         &cursor};
         for (int t = 1; t < threads; ++t) pthread_create(&tid[t], NULL, bench_worker, &s);
         bench_worker(&s);
         for (int t = 1; t < threads; ++t) pthread_join(tid[t], NULL);
