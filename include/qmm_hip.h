@@ -111,13 +111,19 @@ size_t qmm_row_bytes(uint32_t type, int64_t cols);
  * At qmm_q8k_h_offset: the fp16 values the codes were quantized from,
  * [M][K] (the reference keeps them as x_fp16 beside its quantized input,
  * E:879-886, and dots its F32 / F16 rows with them, E:3410-3440).
+ * At qmm_q8k_bh_offset: the sums of 16 codes (the reference's bsums, E:870;
+ * exact in fp16) as fp16 in matrix-core operand order (no counterpart; read
+ * by the prefill kernels): for token tile t and block j, 512 B at
+ * (t * K/256 + j) * 512 whose 8-B slot 16c + n holds token 16t + n's sums of
+ * 16-value groups 4c..4c+3.
  * Every producer (qmm_quantize_q8k, qmm_swiglu_q8k, qmm_rmsnorm_q8k)
- * writes all five sections. */
+ * writes all six sections. */
 size_t qmm_q8k_bytes(int M, int K);
 size_t qmm_q8k_d_offset(int M, int K);
 size_t qmm_q8k_bsum_offset(int M, int K);
 size_t qmm_q8k_tile_offset(int M, int K);
 size_t qmm_q8k_h_offset(int M, int K);
+size_t qmm_q8k_bh_offset(int M, int K);
 /* Q8_0 activations (BlockQ8_0_Fast E:874-877): qs int8[M][K] at 0,
  * d f32[M][K/32] at qmm_q8_0_d_offset. */
 size_t qmm_q8_0_bytes(int M, int K);

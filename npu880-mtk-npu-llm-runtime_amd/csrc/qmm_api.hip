@@ -180,14 +180,14 @@ int check_tasks(qmm_context *ctx, int M, int K, qmm_matrix_task *tasks, int n_ta
 // Kernel views of prequantized activation buffers (a null buffer gives a
 // null view).
 void act_views(const void *q8k, const void *q80, int M, int K, qmm::Q8KView &xk, qmm::Q80View &x0) {
-    xk = {nullptr, nullptr, nullptr, nullptr, nullptr};
+    xk = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     x0 = {nullptr, nullptr};
     if (q8k) {
         const qmm::Q8KLayout L(M, K);
         const uint8_t *b = static_cast<const uint8_t *>(q8k);
         xk = {reinterpret_cast<const int8_t *>(b), reinterpret_cast<const float *>(b + L.d_off),
               reinterpret_cast<const int32_t *>(b + L.bs_off), reinterpret_cast<const int8_t *>(b + L.tile_off),
-              reinterpret_cast<const uint16_t *>(b + L.h_off)};
+              reinterpret_cast<const uint16_t *>(b + L.h_off), reinterpret_cast<const uint16_t *>(b + L.bh_off)};
     }
     if (q80) {
         const qmm::Q80Layout L(M, K);
@@ -414,6 +414,7 @@ size_t qmm_q8k_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout
 size_t qmm_q8k_bsum_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).bs_off : 0; }
 size_t qmm_q8k_tile_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).tile_off : 0; }
 size_t qmm_q8k_h_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).h_off : 0; }
+size_t qmm_q8k_bh_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q8KLayout(M, K).bh_off : 0; }
 size_t qmm_q8_0_bytes(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).total : 0; }
 size_t qmm_q8_0_d_offset(int M, int K) { return (M > 0 && K > 0) ? qmm::Q80Layout(M, K).d_off : 0; }
 

@@ -20,7 +20,7 @@ constexpr uint32_t kQ6_K = 14;
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Q8_K activation buffer layout (all sections 256-B aligned):
-//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32] | tiles | h fp16[M][K]
+//   qs int8[M][K] | d f32[M][K/256] | bsum32 i32[M][K/32] | tiles | h fp16[M][K] | bh
 // tiles: the codes again, in the order of an MFMA operand: for token tile t
 // (tokens 16t .. 16t + 15), 256-value block j and 64-value chunk h, 1 KB at
 // ((t * K/256 + j) * 4 + h) * 1024 whose 16-B slot 16c + n (c < 4, n < 16)
@@ -29,15 +29,21 @@ __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~size_
 // h: the fp16 values the codes were quantized from (the reference keeps them
 // beside its quantized input as x_fp16, E:879-886; its F32 / F16 rows are
 // dotted with them, E:3410-3440).
+// bh: the sums of 16 codes (the reference's bsums, E:870, |sum| <= 2032, so
+// exact in fp16) as fp16, in the order of a 16x16x16 fp16 MFMA operand: for
+// token tile t and block j, 512 B at (t * K/256 + j) * 512 whose 8-B slot
+// 16c + n holds token 16t + n's sums of groups 4c .. 4c + 3.
 struct Q8KLayout {
-    size_t d_off, bs_off, tile_off, h_off, total;
+    size_t d_off, bs_off, tile_off, h_off, bh_off, total;
     __host__ __device__ Q8KLayout(int M, int K) {
         const size_t mk = size_t(M) * size_t(K);
+        const size_t mt = size_t((M + 15) / 16) * 16;
         d_off = align256(mk);
         bs_off = align256(d_off + 4 * size_t(M) * size_t(K / 256));
         tile_off = align256(bs_off + 4 * size_t(M) * size_t(K / 32));
-        h_off = align256(tile_off + size_t((M + 15) / 16) * 16 * size_t(K));
-        total = align256(h_off + 2 * mk);
+        h_off = align256(tile_off + mt * size_t(K));
+        bh_off = align256(h_off + 2 * mk);
+        total = align256(bh_off + mt * size_t(K / 8));
     }
 };
 // byte offset in the tiles section of the 4 codes of token m at values
@@ -46,6 +52,10 @@ __host__ __device__ inline size_t q8k_tile_pos(int m, int j, int i, int nb) {
     const int h = i >> 4, kk = 4 * (i & 15);
     const int c = (kk & 31) >> 3, byte = (kk & 7) + ((kk & 32) >> 2);
     return ((size_t(m >> 4) * size_t(nb) + size_t(j)) * 4 + size_t(h)) * 1024 + size_t(16 * (16 * c + (m & 15)) + byte);
+}
+// byte offset in the bh section of token m's sum of group g (< 16) of block j
+__host__ __device__ inline size_t q8k_bh_pos(int m, int j, int g, int nb) {
+    return (size_t(m >> 4) * size_t(nb) + size_t(j)) * 512 + size_t(8 * (16 * (g >> 2) + (m & 15)) + 2 * (g & 3));
 }
 // Q8_0 activation buffer layout: qs int8[M][K] | d f32[M][K/32]
 struct Q80Layout {
@@ -63,6 +73,7 @@ struct Q8KView {
     const int32_t *bs;  // [M][K/32]
     const int8_t *qt;   // the tiles section
     const uint16_t *h;  // fp16 values [M][K]
+    const uint16_t *bh; // fp16 sums of 16 codes, MFMA operand order
 };
 struct Q80View {
     const int8_t *qs;  // [M][K]
@@ -411,6 +422,15 @@ __device__ inline void dma16(const v4i32 &r, uint32_t voff, uint32_t lds) {
 __device__ inline void dma4(const v4i32 &r, uint32_t voff, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds"
                  : : "v"(voff), "s"(lds), "s"(r) : "memory", "m0");
+}
+// the same with a uniform byte offset soff added to every lane's voff
+__device__ inline void dma16s(const v4i32 &r, uint32_t voff, uint32_t soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r), "s"(soff) : "memory", "m0");
+}
+__device__ inline void dma4s(const v4i32 &r, uint32_t voff, uint32_t soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, %3 offen lds"
+                 : : "v"(voff), "s"(lds), "s"(r), "s"(soff) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 // s_waitcnt vmcnt(N) (lgkmcnt and expcnt not waited on)

@@ -17,19 +17,21 @@ struct Q8KOut {
     int32_t *bs;
     int8_t *qt;
     uint16_t *h;
+    uint8_t *bh;
 };
 __host__ inline Q8KOut q8k_out(void *buf, int M, int K) {
     const Q8KLayout L(M, K);
     uint8_t *b = static_cast<uint8_t *>(buf);
     return {reinterpret_cast<int8_t *>(b), reinterpret_cast<float *>(b + L.d_off),
             reinterpret_cast<int32_t *>(b + L.bs_off), reinterpret_cast<int8_t *>(b + L.tile_off),
-            reinterpret_cast<uint16_t *>(b + L.h_off)};
+            reinterpret_cast<uint16_t *>(b + L.h_off), b + L.bh_off};
 }
 
 // Quantize one fp16-rounded 256-value block held 4 values per lane and
 // store it as Q8_K block `blk` (flattened over [M][K/256]).
 // The codes also go to the tiles section (nb blocks per row), the fp16
-// values to the h section.
+// values to the h section, the sums of 16 codes (exact in fp16) to the bh
+// section.
 __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
                                        size_t blk, const Q8KOut &o, int nb) {
     int8_t *qs = o.qs, *qt = o.qt;
@@ -45,7 +47,10 @@ __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, i
     reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
     const int m = int(blk / size_t(nb)), j = int(blk - size_t(m) * size_t(nb));
     *reinterpret_cast<uint32_t *>(qt + q8k_tile_pos(m, j, lane, nb)) = packed;
-    sum = group8_sum(sum);  // bsum32 over 32 values = 8 lanes
+    sum = group4_sum(sum);  // over 16 values = 4 lanes
+    if ((lane & 3) == 0)
+        *reinterpret_cast<uint16_t *>(o.bh + q8k_bh_pos(m, j, lane >> 2, nb)) = f32_to_fp16_bits((float)sum);
+    sum += dpp_half_mirror(sum);  // bsum32 over 32 values = 8 lanes
     if ((lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
     if (lane == 0) d[blk] = q8_scale(a);  // E:953
 }

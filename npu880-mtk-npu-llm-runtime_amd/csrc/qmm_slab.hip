@@ -1,0 +1,370 @@
+// qmm_slab.hip — prefill GEMM (M > 64 tokens) over GGUF-packed k-quant rows
+// (Q4_K, Q5_K, Q6_K) with int8 MFMA, gfx950.
+//
+// Workgroup = 4 waves on a slab of R = 16 RW PR weight rows x T = 16 TW PT
+// tokens; wave (pr, pt) owns RW row tiles x TW token tiles of 16 x 16. The K
+// loop walks one 256-value block at a time through PD LDS stages, each filled by direct buffer -> LDS
+// transfers (buffer_load ... lds): the slab's packed weight rows, the
+// tokens' codes from the tiles section of the activation buffer (already in
+// MFMA operand order), their fp16 sums of 16 codes (bh section) and their
+// block scales. A wave unpacks each of its row tiles once per step into
+// registers (the unit scales folded into two int8 B operands, as the small-M
+// kernels do) and reuses it for all TW token tiles, so the unpacking is paid
+// once per 16 TW tokens.
+//
+// Per 16 x 16 tile and block: S = 8 D1 + D2 (Q4_K) or 256 D1 + D2 (Q5_K,
+// Q6_K) from two v_mfma_i32_16x16x64_i8 chains over the block's four 64-value
+// chunks; the Q4_K / Q5_K min term Mb = sum_u m_u bsum32_u from one
+// v_mfma_f32_16x16x16_f16 of the 16 sums of 16 codes (|sum| <= 2032) against
+// the mins (<= 63), both exact in fp16, every product and partial sum an
+// integer below 2^24, so the fp32 result is Mb exactly, in any summation
+// order. The per-block fp32 update is the reference's expression, blocks in
+// order, so every output equals the reference's fp32 sum bit for bit:
+//   Q4_K / Q5_K: acc += dx * (d * (float)S - dmin * (float)Mb)   (E:11026, E:11063)
+//   Q6_K:        acc += (d * dx) * (float)S                      (E:11101)
+//
+// Workgroups are numbered so that the ones sharing a row slab run together on
+// one XCD (workgroup b runs on XCD b mod 8): that XCD's L2 then serves the
+// slab's weights to every token group after the first read from HBM.
+#include "qmm_kformats.h"
+
+namespace qmm {
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <class F, int RW_, int TW_, int PR_, int PD_>
+struct SlabCfg {
+    static constexpr int RW = RW_, TW = TW_, PR = PR_, PT = 4 / PR_, PD = PD_;
+    static_assert(PR * PT == 4, "4 waves");
+    static constexpr bool MIN = F::kMin;
+    static constexpr int R = 16 * RW * PR;  // weight rows per workgroup
+    static constexpr int T = 16 * TW * PT;  // tokens per workgroup
+    static constexpr int SB = F::BB;  // weight bytes per row and step
+    // rows of Q4_K / Q5_K start 16-B aligned (the launcher checks):
+    // a step's bytes are whole 16-B units; Q6_K's 210-B blocks take the 16-B
+    // aligned span around them (at most 14 B of lead-in, 4 B read past).
+    static constexpr bool ALIGNED = SB % 16 == 0;
+    static constexpr int WCR = (ALIGNED ? SB / 16 : (SB + 30) / 16) | 1;  // 16-B units per row, odd
+    static constexpr int NWI = (R * WCR + 63) / 64;       // weight transfers (1 KB each)
+    static constexpr int NAI = (T / 16) * 4;              // code transfers (4 KB per token tile)
+    static constexpr int NBI = MIN ? (T / 16 * 32 + 63) / 64 : 0;  // bh transfers (512 B per token tile)
+    static constexpr int NDI = (T + 63) / 64;                        // scales (4-B transfers)
+    static constexpr int NWW = (NWI + 3) / 4, NAW = NAI / 4, NBW = (NBI + 3) / 4, NDW = (NDI + 3) / 4;
+    static constexpr int L = NWW + NAW + NBW + NDW;       // transfers per wave and step
+    static constexpr int OFF_A = NWI * 1024;
+    static constexpr int OFF_B = OFF_A + NAI * 1024;
+    static constexpr int OFF_D = OFF_B + NBI * 1024;
+    static constexpr int STAGE = OFF_D + NDI * 256;
+    static constexpr int OFF_DUMP = PD * STAGE, LDS = OFF_DUMP + 1024;
+    static_assert(NAI % 4 == 0, "token tiles per workgroup: a multiple of 4 code transfers");
+    static_assert((PD - 2) * L <= 63, "vmcnt range");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// B operands of one row tile for one block
+struct SlabB {
+    uint4 b1[4], b2[4];
+    half4v mh;  // mins of the lane's groups (Q4_K / Q5_K)
+    float d, dmin;
+};
+
+// the 4 mins (as fp16) a lane supplies for groups 4c .. 4c + 3: units 2c, 2c,
+// 2c + 1, 2c + 1 (mw: the 8 mins four to a dword)
+__device__ inline half4v mins_f16(const uint32_t (&mw)[2], int c) {
+    // (a mask select: an index would put mw in scratch memory)
+    const uint32_t sel = 0u - uint32_t((c >> 1) & 1);
+    const uint32_t w = (mw[0] & ~sel) | (mw[1] & sel);
+    const int b0 = 2 * (c & 1);
+    const half2v bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    // 0x6400 | m is the fp16 value 1024 + m (m < 64): subtract 1024, exactly
+    const half2v lo = __builtin_bit_cast(half2v, __builtin_bit_cast(uint32_t, byte_pair(w, b0)) | 0x64006400u) - bias;
+    const half2v hi =
+        __builtin_bit_cast(half2v, __builtin_bit_cast(uint32_t, byte_pair(w, b0 + 1)) | 0x64006400u) - bias;
+    return half4v{lo.x, lo.y, hi.x, hi.y};
+}
+
+template <class F>
+__device__ inline void slab_unpack(const uint8_t *blk, int c, SlabB &o) {
+    if constexpr (std::is_same_v<F, MQ6KS>) {
+        const MQ6KS::W w = MQ6KS::load_lds(blk, c);
+        SplitB sb;
+        split_b(w, c, sb);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            o.b1[h] = sb.b1[h];
+            o.b2[h] = sb.b2[h];
+        }
+        o.d = fp16_bits_to_f32(w.d);
+        o.dmin = 0.0f;
+    } else {  // Q4_K / Q5_K folded
+        const typename F::W w = F::load_lds(blk, c);
+        uint32_t scp[2], mp[2];
+        scales_k4_packed(w.h.y, w.h.z, w.h.w, scp, mp);
+        SplitB sb;
+        split_b(w, scp, mp, sb);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            o.b1[h] = sb.b1[h];
+            o.b2[h] = sb.b2[h];
+        }
+        o.mh = mins_f16(mp, c);
+        o.d = fp16_bits_to_f32(w.h.x & 0xFFFFu);
+        o.dmin = fp16_bits_to_f32(w.h.x >> 16);
+    }
+}
+
+template <class C, class F>
+__global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<F>::T x, int ntg) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int RW = C::RW, TW = C::TW;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nl = lane & 15, cl = lane >> 4;
+    const int pt = wid % C::PT, pr = wid / C::PT;
+
+    // workgroup -> (row slab, token group): consecutive slots of one XCD
+    // take the token groups of one slab
+    const int G = grp.wg0[grp.n] * ntg;
+    const int per = (G + 7) / 8;
+    const int lin = int(blockIdx.x % 8u) * per + int(blockIdx.x / 8u);
+    if (lin >= G) return;
+    const int rg = lin / ntg, tg = lin - rg * ntg;
+    int bx;
+    const MatArgs a = grp.t[group_task(grp, rg, bx)];
+    if (scan_stopped(a.scan)) return;
+    const int n0 = bx * C::R, m0 = tg * C::T;
+    const int K = a.K;
+    const int nsteps = K / 256;
+    const int nbk = K / 256;  // blocks per activation row
+
+    // descriptors: the slab's rows (from the 16-B boundary at or below the
+    // first), the codes, sums and scales of the tokens
+    const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
+    const uint32_t bl = uint32_t(wstart & 15);
+    const int rows_valid = min(C::R, a.N - n0);
+    const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
+                              (bl + uint32_t(rows_valid) * uint32_t(a.row_bytes) + 15u) & ~15u);
+    const uint32_t mpad = uint32_t((a.M + 15) & ~15);
+    const v4i32 ra = buf_rsrc(x.qt, mpad * uint32_t(K));
+    v4i32 rb = ra;
+    if constexpr (C::MIN) rb = buf_rsrc(x.bh, mpad * uint32_t(K / 8));
+    const v4i32 rd = buf_rsrc(x.d, uint32_t(a.M) * uint32_t(nbk) * 4u);
+    const uint32_t lds0 = lds_addr(lds);
+
+    // per-lane source offsets of step 0 (lanes past a region's data get
+    // kFar); the step's own offset is a uniform soffset, and a step past the
+    // end adds the region's whole range, so it reads zeros
+    uint32_t wo[C::NWW], wp[C::NWW], ao[C::NAW], bo[C::NBW > 0 ? C::NBW : 1], dof[C::NDW];
+#pragma unroll
+    for (int s = 0; s < C::NWW; ++s) {  // unit pc of row `row`: 16 B from the 16-B boundary at or below its step bytes
+        const int p = (s * 4 + wid) * 64 + lane;
+        const int row = p / C::WCR, pc = p - row * C::WCR;
+        wo[s] = row < C::R ? uint32_t(row) * uint32_t(a.row_bytes) + bl : kFar;
+        wp[s] = 16u * uint32_t(pc);
+        if constexpr (C::ALIGNED) wo[s] = row < C::R ? wo[s] + wp[s] : kFar;  // bl = 0: every step starts 16-B aligned
+    }
+#pragma unroll
+    for (int s = 0; s < C::NAW; ++s) {
+        const int i = s * 4 + wid, tt = i >> 2, h = i & 3;  // token tile, 1-KB quarter
+        const uint32_t tile = uint32_t(m0 / 16 + tt);
+        ao[s] = (tile * uint32_t(nbk)) * 4096u + 1024u * uint32_t(h) + 16u * uint32_t(lane);
+    }
+#pragma unroll
+    for (int s = 0; s < C::NBW; ++s) {
+        const int p = (s * 4 + wid) * 64 + lane, tt = p >> 5, q = p & 31;
+        bo[s] = tt < C::T / 16 ? (uint32_t(m0 / 16 + tt) * uint32_t(nbk)) * 512u + 16u * uint32_t(q) : kFar;
+    }
+#pragma unroll
+    for (int s = 0; s < C::NDW; ++s) {
+        const int p = (s * 4 + wid) * 64 + lane;
+        dof[s] = p < C::T ? uint32_t(m0 + p) * uint32_t(nbk) * 4u : kFar;
+    }
+    const uint32_t wrange = uint32_t(rw.z), arange = uint32_t(ra.z), brange = uint32_t(rb.z), drange = uint32_t(rd.z);
+    // the transfers of step st into stage sg (every wave issues L per step)
+    auto issue = [&](int st, int sg) __attribute__((always_inline)) {
+        const bool live = st < nsteps;
+        const uint32_t base = lds0 + uint32_t(sg * C::STAGE), dump = lds0 + uint32_t(C::OFF_DUMP);
+#pragma unroll
+        for (int s = 0; s < C::NWW; ++s) {
+            const int i = s * 4 + wid;
+            const uint32_t dst = i < C::NWI ? base + uint32_t(i * 1024) : dump;
+            if constexpr (C::ALIGNED) {
+                dma16s(rw, wo[s], live ? uint32_t(st) * uint32_t(C::SB) : wrange, dst);
+            } else {
+                const uint32_t v = ((wo[s] + uint32_t(st) * uint32_t(C::SB)) & ~15u) + wp[s];
+                dma16s(rw, wo[s] != kFar ? v : kFar, live ? 0u : wrange, dst);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < C::NAW; ++s)
+            dma16s(ra, ao[s], live ? uint32_t(st) * 4096u : arange, base + uint32_t(C::OFF_A + (s * 4 + wid) * 1024));
+#pragma unroll
+        for (int s = 0; s < C::NBW; ++s) {
+            const int i = s * 4 + wid;
+            dma16s(rb, bo[s], live ? uint32_t(st) * 512u : brange, i < C::NBI ? base + uint32_t(C::OFF_B + i * 1024) : dump);
+        }
+#pragma unroll
+        for (int s = 0; s < C::NDW; ++s) {
+            const int i = s * 4 + wid;
+            dma4s(rd, dof[s], live ? uint32_t(st) * 4u : drange, i < C::NDI ? base + uint32_t(C::OFF_D + i * 256) : dump);
+        }
+    };
+
+    float acc[RW][TW][4];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[r][t][q] = 0.0f;
+
+#pragma unroll
+    for (int p = 0; p + 1 < C::PD; ++p) issue(p, p);
+    for (int st = 0; st < nsteps; ++st) {
+        const int sg = st % C::PD;
+        wait_vmcnt<(C::PD - 2) * C::L>();  // this wave's transfers of step st have landed
+        __builtin_amdgcn_s_barrier();       // every wave's have; stage (st - 1) is free
+        __builtin_amdgcn_sched_barrier(0);
+        issue(st + C::PD - 1, (st + C::PD - 1) % C::PD);
+        const uint8_t *sbase = lds + sg * C::STAGE;
+        const uint8_t *sa = sbase + C::OFF_A;
+        const float *sd = reinterpret_cast<const float *>(sbase + C::OFF_D);
+        SlabB B[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const int rl = (pr * RW + r) * 16 + nl;  // lane's row in the slab
+            const uint32_t mis = C::ALIGNED ? 0u : (uint32_t(rl) * uint32_t(a.row_bytes) + bl + uint32_t(st) * uint32_t(C::SB)) & 15u;
+            slab_unpack<F>(sbase + rl * (C::WCR * 16) + mis, cl, B[r]);
+        }
+        {
+            // tile u: codes and sums loaded two tiles ahead, dx one ahead; the
+            // MFMAs of tile t + 1 are issued before tile t's fp32 update, so
+            // the matrix core runs while the update's VALU work issues
+            uint4 av[2][4];
+            half4v bh[2];
+            float4 dx[2];
+            int4v D1[2][RW], D2[2][RW];
+            f32x4v Mb[2][RW];
+            auto load_a = [&](int t, int buf) __attribute__((always_inline)) {
+                const int tt = pt * TW + t;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) av[buf][h] = ld16(sa + (tt * 4 + h) * 1024 + 16 * lane);
+                if constexpr (C::MIN) bh[buf] = __builtin_bit_cast(half4v, ld8(sbase + C::OFF_B + tt * 512 + 8 * lane));
+            };
+            auto load_d = [&](int t, int buf) __attribute__((always_inline)) {
+                dx[buf] = *reinterpret_cast<const float4 *>(sd + (pt * TW + t) * 16 + 4 * cl);
+            };
+            auto mm = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+                for (int r = 0; r < RW; ++r) {
+                    int4v d1 = {0, 0, 0, 0}, d2 = {0, 0, 0, 0};
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        d1 = mfma16x16x64(av[buf][h], B[r].b1[h], d1);
+                        d2 = mfma16x16x64(av[buf][h], B[r].b2[h], d2);
+                    }
+                    D1[buf][r] = d1;
+                    D2[buf][r] = d2;
+                    f32x4v m = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (C::MIN) m = __builtin_amdgcn_mfma_f32_16x16x16f16(bh[buf], B[r].mh, m, 0, 0, 0);
+                    Mb[buf][r] = m;
+                }
+            };
+            auto epi = [&](int t, int buf) __attribute__((always_inline)) {
+                const float dxq[4] = {dx[buf].x, dx[buf].y, dx[buf].z, dx[buf].w};
+#pragma unroll
+                for (int r = 0; r < RW; ++r)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int S = (D1[buf][r][q] << F::kShift) + D2[buf][r][q];
+                        if constexpr (C::MIN)
+                            acc[r][t][q] += dxq[q] * (B[r].d * (float)S - B[r].dmin * Mb[buf][r][q]);  // E:11026 / E:11063
+                        else
+                            acc[r][t][q] += (B[r].d * dxq[q]) * (float)S;  // E:11101
+                    }
+            };
+            load_a(0, 0);
+            load_d(0, 0);
+            if (TW > 1) load_a(1, 1);
+            mm(0);
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                if (t + 1 < TW) {
+                    mm((t + 1) & 1);
+                    load_d(t + 1, (t + 1) & 1);
+                }
+                if (t + 2 < TW) load_a(t + 2, t & 1);
+                epi(t, t & 1);
+                if (t + 1 < TW) {
+#pragma unroll
+                    for (int i = 0; i < (C::MIN ? 9 : 8) * RW; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of tile t + 1
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read of tile t + 2
+                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU of tile t's update
+                    }
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();  // the tail's transfers (zeros into a free stage) land before the workgroup ends
+
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int n = n0 + (pr * RW + r) * 16 + nl;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int tok = m0 + (pt * TW + t) * 16 + 4 * cl + q;
+                if (tok >= a.M) continue;
+                float v = acc[r][t][q];
+                if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+                a.y[size_t(tok) * a.ldy + n] = v;
+            }
+    }
+}
+
+template <class C, class F>
+static hipError_t launch_slab_t(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + C::R - 1) / C::R;
+    }
+    const int ntg = (tasks[0].M + C::T - 1) / C::T;
+    const int G = g.wg0[n] * ntg;
+    const unsigned grid = unsigned((G + 7) / 8 * 8);
+    hipLaunchKernelGGL((slab_kernel<C, F>), dim3(grid), dim3(256), size_t(C::LDS), s, g, x, ntg);
+    return hipGetLastError();
+}
+
+// hipErrorNotSupported (nothing launched) where the slab kernel does not
+// apply: K not a multiple of 256, operand sections missing, rows of an
+// aligned format not 16-B aligned, or offsets past the 32-bit buffer range.
+template <class F>
+hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
+    const MatArgs &a = tasks[0];
+    if (a.K % 256 || !x.qt) return hipErrorNotSupported;
+    if constexpr (F::kMin)
+        if (!x.bh) return hipErrorNotSupported;
+    if (size_t((a.M + 15) & ~15) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorNotSupported;
+    constexpr bool aligned = F::BB % 16 == 0;
+    for (int i = 0; i < n; ++i) {
+        if (aligned && ((reinterpret_cast<uintptr_t>(tasks[i].w) | tasks[i].row_bytes) & 15)) return hipErrorNotSupported;
+        if (size_t(tasks[i].N) * tasks[i].row_bytes + 16 >= (size_t(1) << 31)) return hipErrorNotSupported;
+    }
+    // 64 rows x 64 tokens, two workgroups per CU (measured best at M = 512)
+    //                              RW TW PR PD
+    return launch_slab_t<SlabCfg<F, 1, 4, 4, 2>, F>(tasks, n, x, s);
+}
+
+template hipError_t launch_slab<MQ4KS>(const MatArgs *, int, const Q8KView &, hipStream_t);
+template hipError_t launch_slab<MQ5KS>(const MatArgs *, int, const Q8KView &, hipStream_t);
+template hipError_t launch_slab<MQ6KS>(const MatArgs *, int, const Q8KView &, hipStream_t);
+
+}  // namespace qmm

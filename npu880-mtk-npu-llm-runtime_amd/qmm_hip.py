@@ -76,6 +76,7 @@ _SIGNATURES = [
     ("qmm_q8k_bsum_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_tile_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8k_h_offset", C.c_size_t, [C.c_int, C.c_int]),
+    ("qmm_q8k_bh_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_bytes", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_q8_0_d_offset", C.c_size_t, [C.c_int, C.c_int]),
     ("qmm_malloc", C.c_int, [_p, C.c_size_t, C.POINTER(_p)]),
@@ -157,6 +158,18 @@ def q8k_untile(t: np.ndarray, M: int, K: int) -> np.ndarray:
     """Inverse of q8k_tile: the first M tokens' codes in [M][K] order."""
     T, nb = (M + 15) // 16, K // 256
     return np.ascontiguousarray(t.reshape(T, nb, 4, 4, 16, 2, 8).transpose(0, 4, 1, 2, 5, 3, 6)).reshape(T * 16, K)[:M]
+
+
+def q8k_bh(qs: np.ndarray) -> np.ndarray:
+    """Codes [M][K] -> the bh section of a Q8_K buffer (fp16 bits, flat
+    uint16): for token tile t and block j, 256 values whose 4-value slot
+    16c + n holds token 16t + n's sums of 16-value groups 4c..4c+3."""
+    M, K = qs.shape
+    T, nb = (M + 15) // 16, K // 256
+    p = np.zeros((T * 16, K), np.int32)
+    p[:M] = qs
+    s16 = p.reshape(T, 16, nb, 4, 4, 16).sum(axis=5)  # (t, n, j, c, g%4)
+    return np.ascontiguousarray(s16.transpose(0, 2, 3, 1, 4)).astype(np.float16).view(np.uint16).reshape(-1)
 
 
 def q8k_bytes(M: int, K: int) -> int:
@@ -483,6 +496,12 @@ class Context:
         t = self.d2h(buf, np.int8, (T * 16 * K,), offset=int(self.lib.qmm_q8k_tile_offset(M, K)))
         return q8k_untile(t, M, K)
 
+    def read_q8k_bh(self, buf, M: int, K: int) -> np.ndarray:
+        """The bh section of a device Q8_K buffer as fp32 sums [M][K/16]."""
+        T, nb = (M + 15) // 16, K // 256
+        v = self.d2h(buf, np.float16, (T, nb, 4, 16, 4), offset=int(self.lib.qmm_q8k_bh_offset(M, K)))
+        return np.ascontiguousarray(v.transpose(0, 3, 1, 2, 4)).reshape(T * 16, K // 16)[:M].astype(np.float32)
+
     def write_q8k(self, buf, d, qs, bs, x16=None):
         """All sections of a device Q8_K buffer; x16 = the fp16 values (bits
         [M][K]) for the h section, zeros if None."""
@@ -494,6 +513,13 @@ class Context:
         self.h2d(buf, q8k_tile(qs), offset=int(lib.qmm_q8k_tile_offset(M, K)))
         h = np.zeros((M, K), np.uint16) if x16 is None else np.ascontiguousarray(x16, np.uint16).reshape(M, K)
         self.h2d(buf, h, offset=int(lib.qmm_q8k_h_offset(M, K)))
+        self.h2d(buf, q8k_bh(qs), offset=int(lib.qmm_q8k_bh_offset(M, K)))
+
+    def write_q80(self, buf, d, qs):
+        """Both sections of a device Q8_0 buffer from its codes and scales."""
+        M, K = qs.shape
+        self.h2d(buf, np.ascontiguousarray(qs, np.int8))
+        self.h2d(buf, np.ascontiguousarray(d, np.float32), offset=int(self.lib.qmm_q8_0_d_offset(M, K)))
 
     def read_q8k_h(self, buf, M: int, K: int) -> np.ndarray:
         """The h section (fp16 bits [M][K]) of a device Q8_K buffer."""

@@ -55,7 +55,9 @@ def test_row_bytes_and_layout_sizes():
     assert tile_off >= bs_off + 4 * M * K // 32 and tile_off % 256 == 0
     h_off = lib.qmm_q8k_h_offset(M, K)
     assert h_off >= tile_off + 16 * K and h_off % 256 == 0  # one 16-token tile for M = 3
-    assert total >= h_off + 2 * M * K
+    bh_off = lib.qmm_q8k_bh_offset(M, K)
+    assert bh_off >= h_off + 2 * M * K and bh_off % 256 == 0
+    assert total >= bh_off + 16 * K // 8  # fp16 sums of 16 codes for one 16-token tile
     assert lib.qmm_q8_0_d_offset(M, K) >= M * K and lib.qmm_q8_0_bytes(M, K) >= M * K + 4 * M * K // 32
     assert lib.qmm_q8k_bytes(0, K) == 0
 

@@ -129,8 +129,9 @@ def test_tree_verify_q4k(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
 
 
-def test_tree_verify_q5k_qkv(ctx, oracle):
-    _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, 64, seed=2100)
+@pytest.mark.parametrize("M", [8, 16, 32, 64])
+def test_tree_verify_q5k_qkv(ctx, oracle, M):
+    _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, M, seed=2100 + M)
 
 
 def _extreme_weights(type_id, N, K, seed):
@@ -191,6 +192,60 @@ def test_prefill_m512_row_subsets(ctx, oracle, name):
     for r0 in (0, N - 128):
         ref = oracle.gemm_multi(x, [dict(w=w[r0 * rb:(r0 + 128) * rb], type=type_id, rows=128)])[0]
         check_outputs(y[:, r0:r0 + 128], ref, f"prefill {name} rows {r0}..{r0 + 128}")
+
+
+@pytest.mark.parametrize("name", ["qkv", "o", "gate", "down", "q8_0"])
+def test_prefill_m512_every_row_tile(ctx, oracle, name):
+    """Full prefill tensors at M = 512: one row of every 16-row tile (its
+    position in the tile cycling through 0..15), all 512 tokens, against the
+    oracle, so every row slab and token group of the grid is checked."""
+    type_id, N, K = synth.PREFILL_LAYER["tensors"][name]
+    M = 512
+    say(f"prefill strided rows {name} {NAMES[type_id]} N={N} K={K} M={M}")
+    w = synth.weights(type_id, N, K, seed=3100 + N)
+    x = synth.activations(M, K, seed=3101)
+    wb = ctx.weight_upload(w, type_id, N, K)
+    y = ctx.gemm(type_id, wb, N, K, x)
+    ctx.free(wb)
+    rb = synth.row_bytes(type_id, K)
+    rows = np.array([16 * i + (7 * i) % 16 for i in range(N // 16)])
+    sub = w.reshape(N, rb)[rows].reshape(-1)
+    ref = oracle.gemm_multi(x, [dict(w=sub, type=type_id, rows=rows.size)])[0]
+    check_outputs(y[:, rows], ref, f"prefill {name} strided rows")
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
+@pytest.mark.parametrize("N,K,M", [(70, 2560, 65), (201, 1024, 129), (64, 4096, 200), (130, 768, 300)])
+def test_prefill_tails(ctx, oracle, type_id, N, K, M):
+    """The prefill kernel's partial row slabs and token groups (M > 64, N and
+    M not multiples of the workgroup tile), several K."""
+    _run(ctx, oracle, type_id, N, K, M, seed=3200 + N + M + type_id)
+
+
+@pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0])
+def test_prefill_residual(ctx, oracle, type_id):
+    _run(ctx, oracle, type_id, 150, 2560, 140, seed=3300 + type_id, residual=True)
+
+
+def test_prefill_task_group(ctx, oracle):
+    """gate + up (and a third task) of one type in one call at M = 160: one
+    launch over the tasks' concatenated row slabs."""
+    K, M = 2560, 160
+    say(f"prefill task group M={M}")
+    specs = [1000, 333, 64]
+    x = synth.activations(M, K, seed=3400)
+    ws = [synth.weights(TYPE_Q4_K, n, K, seed=3401 + i) for i, n in enumerate(specs)]
+    xb = ctx.upload(x)
+    wbs = [ctx.weight_upload(w, TYPE_Q4_K, n, K) for w, n in zip(ws, specs)]
+    ybs = [ctx.malloc(M * n * 4) for n in specs]
+    tasks = [qmm_hip.MatrixTask(wb, TYPE_Q4_K, n, K, yb, n) for wb, yb, n in zip(wbs, ybs, specs)]
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=TYPE_Q4_K, rows=n) for w, n in zip(ws, specs)])
+    for i, (n, yb) in enumerate(zip(specs, ybs)):
+        check_outputs(ctx.d2h(yb, np.float32, (M, n)), refs[i], f"group task {i}")
+    for b in [xb] + wbs + ybs:
+        ctx.free(b)
 
 
 # ---------------------------------------------------------------- dispatch

@@ -57,8 +57,7 @@ def _run_group(ctx, oracle, specs, M, K, seed, prequantized=False, residual_on=N
         if need_q80:
             z = oracle.quantize_q8_0(x)
             zb = ctx.malloc(ctx.lib.qmm_q8_0_bytes(M, K))
-            ctx.h2d(zb, z[1])
-            ctx.h2d(zb, z[0], offset=int(ctx.lib.qmm_q8_0_d_offset(M, K)))
+            ctx.write_q80(zb, z[0], z[1])
             bufs.append(zb)
         ctx.gemm_multi_dispatch_prequantized(qb, zb, M, K, tasks)
     else:

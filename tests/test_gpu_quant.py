@@ -35,6 +35,10 @@ def test_quantize_q8k_bit_exact(ctx, oracle, M, K):
     assert np.array_equal(ctx.read_q8k_tiles(out, M, K), qs)
     # the h section: the fp16 values the codes came from
     assert np.array_equal(ctx.read_q8k_h(out, M, K), oracle.f32_to_fp16(x))
+    # the bh section: sums of 16 codes (pairs of them are the bsum32 values)
+    bh = ctx.read_q8k_bh(out, M, K)
+    assert np.array_equal(bh, eqs.reshape(M, K // 16, 16).astype(np.int32).sum(axis=2).astype(np.float32))
+    assert np.array_equal(bh.reshape(M, K // 32, 2).sum(axis=2).astype(np.int32), ebs)
     ctx.free(xb)
     ctx.free(out)
 
@@ -75,6 +79,8 @@ def test_swiglu_requant(ctx, oracle):
     assert np.array_equal(d.view(np.uint32), ed.view(np.uint32))
     assert np.array_equal(qs, eqs) and np.array_equal(bs, ebs)
     assert np.array_equal(ctx.read_q8k_tiles(out, M, N), qs)
+    assert np.array_equal(ctx.read_q8k_bh(out, M, N),
+                          qs.reshape(M, N // 16, 16).astype(np.int32).sum(axis=2).astype(np.float32))
     assert np.array_equal(ctx.read_q8k_h(out, M, N), oracle.f32_to_fp16(h))
     for b in (gb, ub, hb, out):
         ctx.free(b)
