@@ -726,7 +726,7 @@ __device__ __attribute__((always_inline)) inline void gemv_float_wg(const MatArg
                 const int p = b0 + lane + 64 * i;
                 if (p < npc) {
                     q0[i] = ld16_nt(w0 + 16 * size_t(p));
-                    q1[i] = ld16_nt(w1 + 16 * size_t(p));
+                    if constexpr (R > 1) q1[i] = ld16_nt(w1 + 16 * size_t(p));
                 }
             }
 #pragma unroll
@@ -734,7 +734,8 @@ __device__ __attribute__((always_inline)) inline void gemv_float_wg(const MatArg
                 const int p = b0 + lane + 64 * i;
                 if (p < npc) {
                     acc[j] = float_piece_dot<F16W>(q0[i], xv[i], acc[j]);
-                    if (j + 1 < R) acc[j + 1] = float_piece_dot<F16W>(q1[i], xv[i], acc[j + 1]);
+                    if constexpr (R > 1)
+                        if (j + 1 < R) acc[j + 1] = float_piece_dot<F16W>(q1[i], xv[i], acc[j + 1]);
                 }
             }
         }
@@ -765,8 +766,10 @@ __global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const flo
         case kQ5_K: gemv_wg<FmtQ5K, R, kGemvU, FUSED, 0>(a, bx, x32, prek, pre0); break;
         case kQ6_K: gemv_wg<FmtQ6K4, R, 3, FUSED, stage_chunks<FmtQ6K4, 3>()>(a, bx, x32, prek, pre0); break;
         case kQ8_0: gemv_wg<FmtQ80, R, kGemvU, FUSED, stage_chunks<FmtQ80, kGemvU>()>(a, bx, x32, prek, pre0); break;
-        case kF32: gemv_float_wg<false, R, FUSED>(a, bx, x32, prek.h); break;
-        case kF16: gemv_float_wg<true, R, FUSED>(a, bx, x32, prek.h); break;
+        // F32 / F16 rows: one row per wave whatever the group's R (their
+        // bytes per row are 4-8x a k-quant's; more workgroups share them)
+        case kF32: gemv_float_wg<false, 1, FUSED>(a, bx, x32, prek.h); break;
+        case kF16: gemv_float_wg<true, 1, FUSED>(a, bx, x32, prek.h); break;
         default: break;
     }
 }
@@ -1057,7 +1060,8 @@ static hipError_t launch_gemv_mixed_r(const MatArgs *tasks, int n, const float *
     size_t lds = 0;
     for (int i = 0; i < n; ++i) {
         g.t[i] = tasks[i];
-        g.wg0[i + 1] = g.wg0[i] + ((tasks[i].N + R - 1) / R + 3) / 4;
+        const int r = (tasks[i].type == kF32 || tasks[i].type == kF16) ? 1 : R;  // rows per wave
+        g.wg0[i + 1] = g.wg0[i] + ((tasks[i].N + r - 1) / r + 3) / 4;
         lds = max(lds, gemv_wg_lds<R>(tasks[i].type, tasks[i].K));
     }
     const dim3 grid(unsigned(g.wg0[n]));
