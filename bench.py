@@ -756,12 +756,18 @@ def pmc_write(dirs):
     print("#     SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_WAVES GRBM_GUI_ACTIVE -d gpurun_out/gpmc1 -o run \\")
     print("#     --output-format csv -- python3 bench.py --pmc-run")
     print("#   rocprofv3 --pmc FETCH_SIZE -d gpurun_out/gpmc2 ... ; rocprofv3 --pmc WRITE_SIZE -d gpurun_out/gpmc3 ...")
+    print("#   rocprofv3 --pmc SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS \\")
+    print("#     SQ_VALU_MFMA_COEXEC_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 -d gpurun_out/gpmc4 ...")
     print(f"# summary: {cmd}")
     print("# derived: mfma_busy_frac = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs * 1024 SIMDs)")
     print("#   (rocprof's MfmaUtil); valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA; int8_ops_executed =")
     print("#   SQ_INSTS_VALU_MFMA_MOPS_I8 * 512; lds_bank_conflict_frac = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE;")
     print("#   hbm_bytes = FETCH_SIZE * 1.9966 + WRITE_SIZE * 1.0 KiB (the factors the same counters read on a")
-    print("#   device copy of known size, profiles/gemv_q4k_fused_9728x2560_pmc.txt)")
+    print("#   device copy of known size, profiles/gemv_q4k_fused_9728x2560_pmc.txt); wave time (SQ_WAVE_CYCLES,")
+    print("#   quad-cycles summed over waves): valu_active_frac = SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES,")
+    print("#   wait_any_frac = SQ_WAIT_ANY / SQ_WAVE_CYCLES (waitcnt / barrier), wait_issue_frac =")
+    print("#   SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (ready instruction not issued); mfma_coexec_frac =")
+    print("#   SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES (MFMA-busy cycles in which a VALU issued)")
     for name, t, N, K, M in PMC_WORKLOADS:
         if name not in acc:
             continue
@@ -771,8 +777,10 @@ def pmc_write(dirs):
         print(f"{name}.kernel: {names[name]}")
         print(f"{name}.shape: {qmm_hip.TYPE_NAMES[t]} {N}x{K} M={M}")
         print(f"{name}.us_under_profiler: {np.mean(dur[name]):.3f}")
-        for k in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_VALU_MFMA_BUSY_CYCLES",
-                  "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAVES", "GRBM_GUI_ACTIVE", "FETCH_SIZE",
+        for k in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_INSTS_VALU_MFMA_MOPS_F16",
+                  "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_LDS_BANK_CONFLICT",
+                  "SQ_LDS_IDX_ACTIVE", "SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+                  "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "FETCH_SIZE",
                   "WRITE_SIZE"):
             if k in c:
                 print(f"{name}.{k}: {c[k]:.6g}")
@@ -783,6 +791,14 @@ def pmc_write(dirs):
                 print(f"{name}.valu_per_mfma: {c['SQ_INSTS_VALU'] / c['SQ_INSTS_MFMA']:.3f}")
         if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("GRBM_GUI_ACTIVE"):
             print(f"{name}.mfma_busy_frac: {c['SQ_VALU_MFMA_BUSY_CYCLES'] / (c['GRBM_GUI_ACTIVE'] / 8 * 1024):.4f}")
+        if c.get("SQ_WAVE_CYCLES"):
+            wc = c["SQ_WAVE_CYCLES"]
+            for k, lab in (("SQ_ACTIVE_INST_VALU", "valu_active_frac"), ("SQ_WAIT_ANY", "wait_any_frac"),
+                           ("SQ_WAIT_INST_ANY", "wait_issue_frac")):
+                if k in c:
+                    print(f"{name}.{lab}: {c[k] / wc:.3f}")
+        if c.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in c:
+            print(f"{name}.mfma_coexec_frac: {c['SQ_VALU_MFMA_COEXEC_CYCLES'] / c['SQ_VALU_MFMA_BUSY_CYCLES']:.3f}")
         if "SQ_INSTS_VALU_MFMA_MOPS_I8" in c:
             ex = c["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
             print(f"{name}.int8_ops_executed: {ex:.6g}")
