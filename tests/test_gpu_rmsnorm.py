@@ -57,3 +57,35 @@ def test_rmsnorm_without_y(ctx, oracle):
     assert np.mean(qs != eqs) < 0.01
     for b in (xb, gb, q):
         ctx.free(b)
+
+
+def test_rmsnorm_block_mismatch_rate(ctx, oracle):
+    """How often the tree-ordered sum of squares changes a Q8_K block against
+    the reference's row-ordered sum, at the workload's width (K = 2560) over
+    512 rows: the fraction of 256-value blocks whose codes or scale differ
+    from the oracle's (the compiled reference's) is printed and bounded."""
+    M, K = 512, 2560
+    say(f"rmsnorm mismatch rate M={M} K={K}")
+    g = np.random.default_rng(2560)
+    x = g.standard_normal((M, K)).astype(np.float32)
+    gamma = g.uniform(0.5, 1.5, K).astype(np.float32)
+    xb, gb = ctx.upload(x), ctx.upload(gamma)
+    q = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.rmsnorm_q8k(xb, gb, M, K, None, q)
+    ctx.sync()
+    d, qs, bs = ctx.read_q8k(q, M, K)
+    _, (rd, rqs, rbs) = oracle.rmsnorm_q8k(x, gamma)
+    nb = K // 256
+    code_diff = (qs.reshape(M, nb, 256) != rqs.reshape(M, nb, 256)).any(axis=2)
+    scale_diff = d.reshape(M, nb).view(np.uint32) != rd.reshape(M, nb).view(np.uint32)
+    blocks = code_diff | scale_diff
+    rows = blocks.any(axis=1)
+    codes = np.count_nonzero(qs != rqs)
+    say(f"rmsnorm K={K}: {np.count_nonzero(blocks)} of {blocks.size} blocks "
+        f"({100 * blocks.mean():.2f} %) and {np.count_nonzero(rows)} of {M} rows differ; "
+        f"{codes} of {qs.size} codes ({100 * codes / qs.size:.4f} %), each by at most "
+        f"{int(np.abs(qs.astype(int) - rqs.astype(int)).max())}")
+    assert np.abs(qs.astype(int) - rqs.astype(int)).max() <= 1
+    assert blocks.mean() < 0.25
+    for b in (xb, gb, q):
+        ctx.free(b)
