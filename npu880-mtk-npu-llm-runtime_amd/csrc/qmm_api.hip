@@ -262,6 +262,19 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
 }
 
 // Checks of a prequantized input for a validated task list.
+// Sections of the dispatcher's own Q8_K buffer that no kernel of an M >= 2
+// call reads: bsum32 (read only by the batch-1 GEMV on prequantized input),
+// the row-major codes above 64 tokens (the tile and slab kernels read the
+// tiles section), the fp16 values without an F32 / F16 task.
+unsigned q8k_skip(int M, const qmm_matrix_task *tasks, int n_tasks) {
+    unsigned skip = qmm::kSkipBs;
+    if (M > 64) skip |= qmm::kSkipQs;
+    bool flt = false;
+    for (int i = 0; i < n_tasks; ++i) flt = flt || is_float(tasks[i].type);
+    if (!flt) skip |= qmm::kSkipH;
+    return skip;
+}
+
 int check_pre(qmm_context *ctx, const void *q8k, const void *q80, bool need_q8k, bool need_q80) {
     if (need_q8k && !q8k) return fail(ctx, QMM_EINVAL, "K-quant or F32/F16 task without Q8_K activations");
     if (need_q80 && !q80) return fail(ctx, QMM_EINVAL, "Q8_0 task without Q8_0 activations");
@@ -657,7 +670,8 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
     void *q8k = need_q8k ? ctx->act : nullptr;
     void *q80 = need_q80 ? static_cast<uint8_t *>(ctx->act) + k_bytes : nullptr;
     hipError_t e;
-    if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream)) != hipSuccess)
+    if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream, q8k_skip(M, tasks, n_tasks))) !=
+                        hipSuccess)
         return hip_fail(ctx, e, "quantize_q8k launch");
     if (need_q80 && (e = qmm::launch_quantize_q8_0(x, M, K, q80, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "quantize_q8_0 launch");
@@ -689,7 +703,8 @@ int qmm_gemm_multi_dispatch_noalloc(qmm_context *ctx, const float *x, int M, int
     void *q8k = need_q8k ? base : nullptr;
     void *q80 = need_q80 ? base + k_bytes : nullptr;  // (k_bytes is a multiple of 256)
     hipError_t e;
-    if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream)) != hipSuccess)
+    if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream, q8k_skip(M, tasks, n_tasks))) !=
+                        hipSuccess)
         return hip_fail(ctx, e, "quantize_q8k launch");
     if (need_q80 && (e = qmm::launch_quantize_q8_0(x, M, K, q80, ctx->stream)) != hipSuccess)
         return hip_fail(ctx, e, "quantize_q8_0 launch");

@@ -127,7 +127,11 @@ __device__ inline int group_task(const MatGroup &g, int bx, int &local) {
 }
 
 // Launchers (return hipSuccess or the launch error).
-hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s);
+// sections a Q8_K producer may leave unwritten (the dispatcher's own buffer,
+// where no kernel of the call reads them): the codes [M][K], the h values,
+// the bsum32 array
+constexpr unsigned kSkipQs = 1, kSkipH = 2, kSkipBs = 4;
+hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s, unsigned skip = 0);
 hipError_t launch_quantize_q8_0(const float *x, int M, int K, void *out, hipStream_t s);
 hipError_t launch_swiglu_q8k(const float *gate, const float *up, int M, int N, float *h,
                              void *out, hipStream_t s);

@@ -31,27 +31,29 @@ __host__ inline Q8KOut q8k_out(void *buf, int M, int K) {
 // store it as Q8_K block `blk` (flattened over [M][K/256]).
 // The codes also go to the tiles section (nb blocks per row), the fp16
 // values to the h section, the sums of 16 codes (exact in fp16) to the bh
-// section.
+// section. A null qs, h or bs pointer leaves that section unwritten.
 __device__ inline void store_q8k_block(float h0, float h1, float h2, float h3, int lane,
                                        size_t blk, const Q8KOut &o, int nb) {
     int8_t *qs = o.qs, *qt = o.qt;
     float *d = o.d;
     int32_t *bs = o.bs;
-    const uint32_t hlo = uint32_t(f32_to_fp16_bits(h0)) | (uint32_t(f32_to_fp16_bits(h1)) << 16);
-    const uint32_t hhi = uint32_t(f32_to_fp16_bits(h2)) | (uint32_t(f32_to_fp16_bits(h3)) << 16);
-    reinterpret_cast<uint2 *>(o.h + blk * 256)[lane] = make_uint2(hlo, hhi);
+    if (o.h) {
+        const uint32_t hlo = uint32_t(f32_to_fp16_bits(h0)) | (uint32_t(f32_to_fp16_bits(h1)) << 16);
+        const uint32_t hhi = uint32_t(f32_to_fp16_bits(h2)) | (uint32_t(f32_to_fp16_bits(h3)) << 16);
+        reinterpret_cast<uint2 *>(o.h + blk * 256)[lane] = make_uint2(hlo, hhi);
+    }
     float a = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
     a = wave_max(a);  // E:941-946
     int sum;
     const uint32_t packed = quant4(h0, h1, h2, h3, a, sum);
-    reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
+    if (qs) reinterpret_cast<uint32_t *>(qs + blk * 256)[lane] = packed;
     const int m = int(blk / size_t(nb)), j = int(blk - size_t(m) * size_t(nb));
     *reinterpret_cast<uint32_t *>(qt + q8k_tile_pos(m, j, lane, nb)) = packed;
     sum = group4_sum(sum);  // over 16 values = 4 lanes
     if ((lane & 3) == 0)
         *reinterpret_cast<uint16_t *>(o.bh + q8k_bh_pos(m, j, lane >> 2, nb)) = f32_to_fp16_bits((float)sum);
     sum += dpp_half_mirror(sum);  // bsum32 over 32 values = 8 lanes
-    if ((lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
+    if (bs && (lane & 7) == 0) bs[blk * 8 + (lane >> 3)] = sum;
     if (lane == 0) d[blk] = q8_scale(a);  // E:953
 }
 
@@ -240,10 +242,14 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict_
     }
 }
 
-hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s) {
+hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStream_t s, unsigned skip) {
     const size_t nblk = size_t(M) * size_t(K / 256);
     const unsigned grid = unsigned((nblk + 3) / 4);
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk, q8k_out(out, M, K), K / 256);
+    Q8KOut o = q8k_out(out, M, K);
+    if (skip & kSkipQs) o.qs = nullptr;
+    if (skip & kSkipH) o.h = nullptr;
+    if (skip & kSkipBs) o.bs = nullptr;
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk, o, K / 256);
     return hipGetLastError();
 }
 
