@@ -325,9 +325,34 @@ int lm_task(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, co
 // or past id_limit are never read and count as -1e30, E:11150); else rows
 // [row_base, row_base + rows) start at w. scr: this call's scratch (laid out
 // by lm_scratch); scan: a scan's state or NULL. Arguments are validated.
+// A batch-1 scan chunk's step not yet applied: the next chunk's launch
+// applies it first (PrevStep), or one scan_final launch does. Its partials
+// and the next chunk's alternate between two buffers.
+struct PendingStep {
+    bool on = false;
+    const void *part = nullptr;
+    int nparts = 0;
+    uint32_t row_base = 0;
+    float thresh = 0.0f;
+    bool checkpoint = false;
+    int c = 0;
+    void *bufs[2] = {nullptr, nullptr};
+};
+
+int launch_pending(qmm_context *ctx, PendingStep &pend, float *best_val, uint32_t *best_id, const qmm::ScanStep &st,
+                   int32_t *scan) {
+    if (!pend.on) return QMM_OK;
+    pend.on = false;
+    const hipError_t e = qmm::launch_scan_final(pend.part, pend.nparts, pend.row_base, best_val, best_id, st.cand,
+                                                st.draft, st.margin, pend.thresh, pend.checkpoint, pend.c, scan,
+                                                ctx->stream);
+    return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "scan step launch");
+}
+
 int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, qmm_matrix_task t,
                   uint32_t row_base, const uint32_t *ids, uint32_t id_limit, float *logits_out, float *best_val,
-                  uint32_t *best_id, uint8_t *scr, int32_t *scan, const qmm::ScanStep *step) {
+                  uint32_t *best_id, uint8_t *scr, int32_t *scan, const qmm::ScanStep *step,
+                  PendingStep *pend = nullptr) {
     const int rows = t.rows;
     const LmScratch L = lm_scratch(M, rows, t.row_bytes, logits_out != nullptr, ids != nullptr);
     float *logits = logits_out ? logits_out : reinterpret_cast<float *>(scr);
@@ -345,7 +370,29 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
     qmm::Q80View x0;
     act_views(q8k, q80, M, K, xk, x0);
     const bool round16 = ids == nullptr;  // chunk scans compare fp16 logits (E:11175), indexed rows fp32
-    if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
+    if (M == 1 && step && pend) {  // a scan chunk: its step waits for the next chunk's launch
+        void *mine = pend->bufs[step->c & 1];
+        qmm::PrevStep pre{};
+        if (pend->on)
+            pre = qmm::PrevStep{pend->part, pend->nparts, pend->row_base, pend->thresh, pend->checkpoint ? 1 : 0,
+                                pend->c, best_val, best_id, scan};
+        int nparts = 0;
+        e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, scan), xk, x0, round16, ids, id_limit, mine, &nparts,
+                                    ctx->stream, pre);
+        if (e == hipSuccess) {
+            pend->on = true;
+            pend->part = mine;
+            pend->nparts = nparts;
+            pend->row_base = row_base;
+            pend->thresh = step->thresh;
+            pend->checkpoint = step->checkpoint;
+            pend->c = step->c;
+            return QMM_OK;
+        }
+        if (e != hipErrorNotSupported) return hip_fail(ctx, e, "GEMV + argmax launch");
+        int rc = launch_pending(ctx, *pend, best_val, best_id, *step, scan);
+        if (rc) return rc;
+    } else if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
         int nparts = 0;
         e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, scan), xk, x0, round16, ids, id_limit, part, &nparts,
                                     ctx->stream);
@@ -765,7 +812,8 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
     // scratch: candidate logits [M] | candidate dots [M][M - 1] | the largest call's area
     const size_t rb = tc.row_bytes;
     const size_t cand_b = align256(size_t(M) * 4), cdot_b = align256(size_t(M) * size_t(std::max(M - 1, 1)) * 4);
-    size_t area = lm_scratch(M, chunk, rb, false, false).total();
+    const size_t part_b = lm_scratch(M, chunk, rb, false, false).part_b;
+    size_t area = lm_scratch(M, chunk, rb, false, false).total() + (M == 1 ? 2 * part_b : 0);
     if (n_pre > 0) area = std::max(area, lm_scratch(M, n_pre, rb, false, true).total());
     if (draft_ids && M >= 2) area = std::max(area, align256(size_t(M - 1) * rb));
     if ((rc = ensure_lm(ctx, cand_b + cdot_b + area))) return rc;
@@ -791,6 +839,10 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
         if (e != hipSuccess) return hip_fail(ctx, e, "candidate launch");
     }
     // the chunks (E:11158-11257): each does nothing once the scan has stopped
+    PendingStep pend;
+    pend.bufs[0] = work + lm_scratch(M, chunk, rb, false, false).total();
+    pend.bufs[1] = static_cast<uint8_t *>(pend.bufs[0]) + part_b;
+    qmm::ScanStep last{};
     for (int c = 0; c < nchunks; ++c) {
         const int r0 = c * params->chunk_rows;
         qmm_matrix_task t = tc;
@@ -804,11 +856,12 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
         step.thresh = c < params->n_thresholds ? params->thresholds[c] : -1e30f;  // E:11245-11246
         step.checkpoint = params->n_thresholds > 0 && c >= params->first_checkpoint;
         step.c = c;
+        last = step;
         if ((rc = lm_argmax_run(ctx, q8k, q80, M, K, t, uint32_t(r0), nullptr, 0u, nullptr, best_val, best_id, work,
-                                scan_state, &step)))
+                                scan_state, &step, M == 1 ? &pend : nullptr)))
             return rc;
     }
-    return QMM_OK;
+    return launch_pending(ctx, pend, best_val, best_id, last, scan_state);
 }
 
 int qmm_graph_begin(qmm_context *ctx) {

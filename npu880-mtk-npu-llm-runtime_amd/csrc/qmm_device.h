@@ -187,14 +187,30 @@ size_t gemv_mixed_lds_bytes(uint32_t type, int K);
 // (<= kMaxArgmaxParts) for launch_argmax_final. hipErrorNotSupported, with
 // nothing launched, where that grid does not apply.
 constexpr int kMaxArgmaxParts = 4096;
+// A batch-1 scan's step after the previous chunk, applied at the start of the
+// next chunk's launch instead of by a launch of its own: that chunk's
+// partials, its first row and its threshold test. Every workgroup reads the
+// partials and reaches the same decision; workgroup 0 writes the state.
+struct PrevStep {
+    const void *part;  // nullptr: none
+    int nparts;
+    uint32_t row_base;
+    float thresh;
+    int checkpoint, c;
+    float *best_val;
+    uint32_t *best_id;
+    int32_t *st;
+};
 struct AmaxOut {
     void *part;
     int round16;
     const uint32_t *ids;  // the rows' ids (NULL: contiguous rows); ids >= id_limit count as -1e30
     uint32_t id_limit;
+    PrevStep pre;
 };
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
-                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s);
+                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
+                              const PrevStep &pre = PrevStep{});
 hipError_t launch_argmax_final(const void *part, int nparts, const uint32_t *ids, uint32_t row_base,
                                float *best_val, uint32_t *best_id, const int32_t *st, hipStream_t s);
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
@@ -305,6 +321,19 @@ __device__ inline Best wave_best(Best b) {
 // a scan that has stopped (uniform: every thread reads the same word)
 __device__ inline bool scan_stopped(const int32_t *st) {
     return st && __builtin_amdgcn_readfirstlane(st[kScanStopped]) != 0;
+}
+__device__ inline int scan_active(const int32_t *st, int M) {
+    return st ? __builtin_amdgcn_readfirstlane(st[kScanActive]) : M;
+}
+// the best of a 256-thread workgroup (sh: 4 entries of LDS)
+__device__ inline Best block_best(Best b, Best *sh) {
+    b = wave_best(b);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) sh[wid] = b;
+    __syncthreads();
+    Best r = sh[0];
+    for (int w = 1; w < 4; ++w) r = better(r, sh[w]);
+    return r;
 }
 
 // ------------------------------------------------------ Q8 quantization

@@ -820,6 +820,20 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
 
     int gw = int(blockIdx.x) * 4 + wid;
     const int stride = int(gridDim.x) * 4;
+    // 0. a scan's step after the previous chunk (the partials are requested
+    // ahead of the activations; the decision precedes every weight request,
+    // so a chunk the step stops reads no weights)
+    Best pb4[4];
+    if constexpr (AMAX) {
+        if (am.pre.part) {
+            const Best *pp = static_cast<const Best *>(am.pre.part);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = int(threadIdx.x) + 256 * i;
+                pb4[i] = e < am.pre.nparts ? pp[e] : Best{-INFINITY, kNone};
+            }
+        }
+    }
     // 1. the activation row, then the first group's bytes
     XPre xp;
     CPre cp;
@@ -827,6 +841,35 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
     }
     else cpre_load<q80>(pq, pd, pb, K, cp);
+    if constexpr (AMAX) {
+        if (am.pre.part) {
+            __shared__ Best psh[4];
+            __shared__ int pstop;
+            Best b = better(better(pb4[0], pb4[1]), better(pb4[2], pb4[3]));  // slices e, e + 256, ... in order
+            b = block_best(b, psh);
+            const PrevStep &q = am.pre;
+            if (threadIdx.x == 0) {
+                // the running best of token 0 (E:11177), then the threshold test (E:11248-11256)
+                float bv = q.best_val[0];
+                uint32_t bi = q.best_id[0];
+                const int act = scan_active(q.st, 1);
+                if (act > 0 && b.i != kNone && b.v > bv) {
+                    bv = b.v;
+                    bi = q.row_base + b.i;
+                }
+                const int stop = q.checkpoint && (act == 0 || !(bv < q.thresh));
+                pstop = stop;
+                if (blockIdx.x == 0) {
+                    q.best_val[0] = bv;
+                    q.best_id[0] = bi;
+                    q.st[kScanChunks] = q.c + 1;
+                    if (stop) q.st[kScanStopped] = 1;
+                }
+            }
+            __syncthreads();
+            if (pstop) return;
+        }
+    }
     // a wave that loads x waits for it before it requests weights (measured:
     // weights first 5.09 us, x first 4.88; all waves held until x is in
     // 5.20): x is the critical path and weight requests slow its arrival
@@ -966,23 +1009,24 @@ static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, cons
 template <class F, int U>
 static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                                        const uint32_t *ids, uint32_t id_limit, void *part, int *nparts,
-                                       hipStream_t s) {
+                                       hipStream_t s, const PrevStep &pre) {
     constexpr int R = kGemvR;
     const int nb = a.K / F::QK, cus = cu_count();
     const int wg0 = ((a.N + R - 1) / R + 3) / 4;
     if (a.N < (IsQ80<F>::v ? 8192 : 4096) || R * nb > (64 / F::G) * U || wg0 < 2 * cus) return hipErrorNotSupported;
     const int wgs = min(3 * cus, wg0 * 5 / 8);
-    if (wgs > kMaxArgmaxParts) return hipErrorNotSupported;
+    if (wgs > kMaxArgmaxParts || (pre.part && pre.nparts > 1024)) return hipErrorNotSupported;
     *nparts = wgs;
     return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
-                                                AmaxOut{part, round16 ? 1 : 0, ids, id_limit});
+                                                AmaxOut{part, round16 ? 1 : 0, ids, id_limit, pre});
 }
 
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
-                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s) {
+                              const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
+                              const PrevStep &pre) {
     switch (type) {
-        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s);
-        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s);
+        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
+        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
         default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
     }
 }

@@ -19,22 +19,8 @@
 
 namespace qmm {
 
-__device__ inline Best block_best(Best b, Best *sh) {
-    b = wave_best(b);
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    if (lane == 0) sh[wid] = b;
-    __syncthreads();
-    Best r = sh[0];
-    for (int w = 1; w < 4; ++w) r = better(r, sh[w]);
-    return r;
-}
-
 // slice s of token m: rows [s * SLICE, (s + 1) * SLICE) of logits[m][.]
 constexpr int kSlice = 1024;
-
-__device__ inline int scan_active(const int32_t *st, int M) {
-    return st ? __builtin_amdgcn_readfirstlane(st[kScanActive]) : M;
-}
 
 // Position i of an indexed list names row ids[i]; a row past the tensor
 // (ids[i] >= id_limit) has the value -1e30 (E:11150), written back to the

@@ -190,7 +190,7 @@ import lm_plant  # noqa: E402
 V, CH = 20000, 4096  # 5 chunks
 
 
-def _scan(ctx, oracle, M, seed, plan, thresholds, first_checkpoint=0, pre=None, draft=None):
+def _scan(ctx, oracle, M, seed, plan, thresholds, first_checkpoint=0, pre=None, draft=None, V=V, CH=CH):
     K = 2560
     w = lm_plant.base_tensor(V + 16, K, seed)
     x = synth.activations(M, K, seed=seed + 1)
@@ -274,3 +274,25 @@ def test_scan_stopped_chunks_read_no_weights(ctx, oracle):
     got, exp = _scan(ctx, oracle, 1, 980, plan, lm_plant.CHUNK_THRESH)
     _same(got, exp, 1, 1, 1)
     assert int(got[1][0]) == 5
+
+
+@pytest.mark.parametrize("case", ["chunk0", "chunk2", "checkpoint3", "all"])
+def test_scan_tall_chunks_batch1(ctx, oracle, case):
+    """Batch-1 chunks tall enough for the persistent GEMV (12288 rows): each
+    chunk's step is applied by the next chunk's launch (or, for the last, by a
+    launch of its own), and a step that stops the scan ends that launch before
+    it requests weights."""
+    V2, CH2 = 60000, 12288  # 5 chunks, the last 10848 rows
+    T = lm_plant.CHUNK_THRESH
+    say(f"lm scan tall chunks {case}")
+    plan0 = [(5, 0, 25.0), (CH2 + 3, 0, 60.0)]  # a larger row in chunk 1 must not be seen after a stop at chunk 0
+    if case == "chunk0":
+        _same(*_scan(ctx, oracle, 1, 990, plan0, T, V=V2, CH=CH2), 1, 1, 1)
+    elif case == "chunk2":
+        _same(*_scan(ctx, oracle, 1, 991, [(2 * CH2 + 77, 0, 14.0)], T, V=V2, CH=CH2), 3, 1, 1)
+    elif case == "checkpoint3":
+        _same(*_scan(ctx, oracle, 1, 992, plan0, T, first_checkpoint=3, V=V2, CH=CH2), 4, 1, 1)
+    else:
+        got, exp = _scan(ctx, oracle, 1, 993, [(4 * CH2 + 9, 0, 40.0)], None, V=V2, CH=CH2)
+        _same(got, exp, 5, 1, 0)
+        assert int(got[1][0]) == 4 * CH2 + 9
