@@ -427,8 +427,11 @@ def bench_mixed(ctx, args):
 
 
 def bench_ffn(ctx, args):
-    """FFN block at batch 1: gate+up Q4_K 9728x2560 on one shared Q8_K input
-    (one dispatch), SiLU(gate)*up -> Q8_K, down Q6_K 2560x9728 (prequantized)."""
+    """FFN block at batch 1: gate+up Q4_K 9728x2560 on one input row,
+    SiLU(gate)*up -> Q8_K, down Q6_K 2560x9728 with its residual —
+    qmm_ffn_block (gate/up with SwiGLU in its epilogue, then the down GEMV
+    on h in fp16: two launches), and beside it the three separate calls
+    (dispatch, swiglu, prequantized dispatch)."""
     H, F = 2560, 9728
     tg, tu, td = synth.FFN["gate"], synth.FFN["up"], synth.FFN["down"]
     block = 2 * F * synth.row_bytes(tg[0], H) + H * synth.row_bytes(td[0], F)
@@ -437,23 +440,30 @@ def bench_ffn(ctx, args):
     wu = Replicated(ctx, tu[0], F, H, R, 72)
     wd = Replicated(ctx, td[0], H, F, R, 73)
     x = ctx.upload(synth.activations(1, H, seed=70))
+    res = ctx.upload(synth.activations(1, H, seed=74))
     g, u, h, y = ctx.malloc(F * 4), ctx.malloc(F * 4), ctx.malloc(F * 4), ctx.malloc(H * 4)
     q = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, F))
     ctx.reserve(1, F)
 
-    def step(i):
+    def block_call(i):
+        ctx.ffn_block(x, None, H, wg.task(i, g), wu.task(i, u), wd.task(i, y, res=res), None)
+
+    def three_calls(i):
         ctx.gemm_multi_dispatch(x, 1, H, [wg.task(i, g), wu.task(i, u)])
         ctx.swiglu_q8k(g, u, 1, F, h, q)
-        ctx.gemm_multi_dispatch_prequantized(q, None, 1, F, [wd.task(i, y)])
+        ctx.gemm_multi_dispatch_prequantized(q, None, 1, F, [wd.task(i, y, res=res)])
 
-    ms, _ = timed(ctx, step, max(50, args.steps // 10), 10, R)
-    alg = block + H * 4 + H * 4  # weights + fp32 x in + fp32 y out (the fused minimum)
+    steps = max(50, args.steps // 10)
+    ms, _ = timed(ctx, block_call, steps, 10, R)
+    ms3, _ = timed(ctx, three_calls, steps, 10, R)
+    alg = block + H * 4 + H * 4 + H * 4  # weights + fp32 x, residual in + fp32 y out (the fused minimum)
     for b in (wg, wu, wd):
         b.free()
-    for b in (x, g, u, h, y, q):
+    for b in (x, res, g, u, h, y, q):
         ctx.free(b)
     out = {"us_per_block": round(ms * 1e3, 3), "algorithmic_bytes": alg, "gbs": round(gbs(alg, ms), 1),
-           "replicas": R, "launches": "gemv(gate+up, one launch), swiglu+Q8_K, gemv(down)"}
+           "replicas": R, "launches": "qmm_ffn_block: gate+up with SwiGLU (one launch), down GEMV on fp16 h",
+           "three_calls_us": round(ms3 * 1e3, 3)}
     log(f"FFN block: {out}")
     return out
 

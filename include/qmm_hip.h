@@ -152,6 +152,22 @@ int qmm_quantize_q8_0(qmm_context *ctx, const float *x, int M, int K, void *q80_
  * Q8_K quantizer per 256 values; gate/up/h are [M][N]. h_out may be NULL. */
 int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, int N,
                    float *h_out, void *q8k_out);
+/* The FFN block of one layer at batch 1 — the sdot path of E:8287-8296 at
+ * M = 1: the {gate, up} task group on the input row (fp32 x, quantized to
+ * Q8_K here, or a prequantized Q8_K row: give exactly one), h = silu(gate) *
+ * up (swiglu_chunk_worker, E:4349-4357) into h_out (fp32 [N], may be NULL),
+ * h's Q8_K, then the down task — its residual included — on that Q8_K.
+ * gate and up: N x K, one type, outputs required (the reference keeps both);
+ * down: cols = N, any type but Q8_0. N % 256 == 0. Results equal the three
+ * steps run as separate calls (qmm_gemm_multi_dispatch, qmm_swiglu_q8k,
+ * qmm_gemm_multi_dispatch_prequantized), bit for bit. Two launches where
+ * they apply — gate/up Q4_K with K <= 3072 (SwiGLU in the gate/up
+ * epilogue), down Q4_K or Q6_K with N <= 12288 on the batch-1 persistent
+ * grid (h quantized in its prologue) — else the three steps as separate
+ * launches. Uses the context's buffers: qmm_reserve(ctx, 1, N) sizes them
+ * for graph capture. */
+int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_matrix_task *gate,
+                  qmm_matrix_task *up, qmm_matrix_task *down, float *h_out);
 /* rmsnorm_fp16_rows_fast (E:4264-4314) with its Q8_K output (E:4303-4305,
  * the producer that sets the prequantized flag, E:4312): per row of x
  * [M][K], y = fp16(x * inv_rms * gamma), inv_rms = 1 / sqrt(mean(x^2) +

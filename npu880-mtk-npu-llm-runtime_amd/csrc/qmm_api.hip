@@ -139,6 +139,11 @@ void free_retired(qmm_context *ctx) {
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// The FFN block's scratch for N intermediate values: h's Q8_K (separate
+// launches) or h in fp16 (one launch), then h itself when the caller does not
+// take it.
+size_t ffn_scratch_bytes(int N) { return align256(qmm::Q8KLayout(1, N).total) + align256(size_t(N) * 4); }
+
 // Validate the task list against (M, K) and assign start_row.
 // need_q8k: a K-quant task, or an F32 / F16 task (they read the fp16
 // section of the Q8_K buffer when M >= 2 or the input is prequantized)
@@ -553,7 +558,8 @@ int qmm_reserve(qmm_context *ctx, int max_M, int max_K) {
     if (!ctx || max_M <= 0 || max_K <= 0) return fail(ctx, QMM_EINVAL, "bad reserve size");
     int rc = use_device(ctx);
     if (rc) return rc;
-    return ensure_act(ctx, qmm::Q8KLayout(max_M, max_K).total + qmm::Q80Layout(max_M, max_K).total);
+    return ensure_act(ctx, std::max(qmm::Q8KLayout(max_M, max_K).total + qmm::Q80Layout(max_M, max_K).total,
+                                    ffn_scratch_bytes(max_K)));
 }
 
 int qmm_device_info(qmm_context *ctx, int *cu_count, size_t *hbm_bytes, char *arch, size_t arch_len) {
@@ -685,6 +691,62 @@ int qmm_rmsnorm_q8k(qmm_context *ctx, const float *x, const float *gamma, int M,
     if (rc) return rc;
     hipError_t e = qmm::launch_rmsnorm_q8k(x, gamma, M, K, y_out, q8k_out, ctx->stream);
     return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "rmsnorm launch");
+}
+
+int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_matrix_task *gate,
+                  qmm_matrix_task *up, qmm_matrix_task *down, float *h_out) {
+    if (!ctx) return QMM_EINVAL;
+    if (!gate || !up || !down) return fail(ctx, QMM_EINVAL, "null task");
+    if ((x == nullptr) == (q8k == nullptr)) return fail(ctx, QMM_EINVAL, "give exactly one of x and q8k");
+    qmm_matrix_task gu[2] = {*gate, *up};
+    bool need_q8k, need_q80;
+    int rc = check_tasks(ctx, 1, K, gu, 2, &need_q8k, &need_q80);
+    if (rc) return rc;
+    const int N = gate->rows;
+    if (N <= 0 || up->rows != N || up->type != gate->type)
+        return fail(ctx, QMM_ESHAPE, "gate and up must have the same positive rows and type");
+    if (N % 256) return fail(ctx, QMM_ESHAPE, "gate/up rows must be a multiple of 256 (h is quantized to Q8_K)");
+    if (x && !aligned(x, 16)) return fail(ctx, QMM_EALIGN, "x must be 16-B aligned");
+    if (q8k && (rc = check_pre(ctx, q8k, nullptr, need_q8k, need_q80))) return rc;
+    if (!aligned(gate->dst, 16) || !aligned(up->dst, 16) || (h_out && !aligned(h_out, 16)))
+        return fail(ctx, QMM_EALIGN, "gate/up outputs and h_out must be 16-B aligned");
+    qmm_matrix_task dn = *down;
+    bool dn_q8k, dn_q80;
+    if ((rc = check_tasks(ctx, 1, N, &dn, 1, &dn_q8k, &dn_q80))) return rc;
+    if (dn_q80) return fail(ctx, QMM_ETYPE, "a Q8_0 down task needs Q8_0 activations; h is quantized to Q8_K");
+    if ((rc = use_device(ctx))) return rc;
+    if ((rc = ensure_act(ctx, ffn_scratch_bytes(N)))) return rc;
+    uint8_t *scr = static_cast<uint8_t *>(ctx->act);
+    void *hq = scr;  // h's Q8_K (separate launches) or h in fp16 (one launch)
+    float *h = h_out ? h_out : reinterpret_cast<float *>(scr + align256(qmm::Q8KLayout(1, N).total));
+    qmm::Q8KView xk;
+    qmm::Q80View x0;
+    act_views(q8k, nullptr, 1, K, xk, x0);
+    // two launches where they apply: gate/up with SwiGLU in its epilogue,
+    // then the down GEMV on h in fp16
+    const qmm::MatArgs da = mat_args(dn, 1, N);
+    uint32_t *hx = static_cast<uint32_t *>(hq);
+    if (gate->type == qmm::kQ4_K && dn.rows > 0 && K % 256 == 0 && K <= 3072 && N <= 12288 &&
+        qmm::launch_gemv_x16(dn.type, da, reinterpret_cast<const uint16_t *>(hx), ctx->stream, false) == hipSuccess) {
+        qmm::FfnArgs a{};
+        a.wg = static_cast<const uint8_t *>(gate->w_base);
+        a.wu = static_cast<const uint8_t *>(up->w_base);
+        a.g = gate->dst;
+        a.u = up->dst;
+        a.h_out = h_out;
+        a.hx = hx;
+        a.K = K;
+        a.F = N;
+        a.rb1 = int(gate->row_bytes);
+        hipError_t e = qmm::launch_ffn_gate_up(a, x, xk, ctx->stream);
+        if (e == hipSuccess) e = qmm::launch_gemv_x16(dn.type, da, reinterpret_cast<const uint16_t *>(hx), ctx->stream);
+        return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "FFN block launch");
+    }
+    // the reference's three steps as separate launches
+    if ((rc = run_tasks(ctx, x, q8k, nullptr, 1, K, gu, 2))) return rc;
+    const hipError_t e = qmm::launch_swiglu_q8k(gate->dst, up->dst, 1, N, h, hq, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "swiglu launch");
+    return run_tasks(ctx, nullptr, hq, nullptr, 1, N, &dn, 1);
 }
 
 int qmm_dequantize_f16(qmm_context *ctx, const void *w_blocks, uint32_t type, int64_t rows,

@@ -220,6 +220,26 @@ hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView
 // K % 256 == 0, or with a Q8_0 task.
 hipError_t launch_mfma_mixed(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s);
 
+// The FFN block's gate/up launch at batch 1 (qmm_ffn.hip): gate and up (F
+// x K, Q4_K) on one input row, with SwiGLU's h written in fp32 (h_out, may
+// be null) and rounded to fp16 (hx) for the down projection's launch
+// (launch_gemv_x16). hipErrorNotSupported (nothing launched) unless K % 256
+// == 0, K <= 3072, F % 256 == 0, 16-B aligned rows.
+struct FfnArgs {
+    const uint8_t *wg, *wu;
+    float *g, *u;      // gate / up outputs (either may be null)
+    float *h_out;      // h (fp32 [F]) or null
+    uint32_t *hx;      // h rounded to fp16, two rows per word ([F / 2])
+    int K, F;
+    int rb1;           // row bytes of gate / up
+};
+hipError_t launch_ffn_gate_up(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s);
+// M = 1 GEMV of one task on an fp16 activation row x16 (16-B aligned, K %
+// 256 == 0, K <= 12288), quantized to Q8_K (or Q8_0) in the kernel: Q4_K /
+// Q6_K on the persistent grid, else hipErrorNotSupported (nothing
+// launched). launch = false: only whether it applies.
+hipError_t launch_gemv_x16(uint32_t type, const MatArgs &a, const uint16_t *x16, hipStream_t s, bool launch = true);
+
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 
 // ------------------------------------------------------------ fp16 helpers
@@ -228,6 +248,15 @@ __device__ inline float fp16_bits_to_f32(uint32_t bits16) {
 }
 // fp32 -> fp16 (round to nearest even, v_cvt_f16_f32) -> fp32
 __device__ inline float round_to_fp16(float x) { return (float)(_Float16)x; }
+// swiglu_chunk_worker (E:4349-4357): gate and up are the dispatcher's fp16
+// outputs in the reference, so each fp32 input is rounded to fp16 first
+// (E:4352-4353); h = (g / (1 + expf(-g))) * u in fp32 (E:4355). The caller
+// rounds h to fp16 before its Q8_K quantizer.
+__device__ inline float silu_mul(float g, float u) {
+    g = round_to_fp16(g);
+    u = round_to_fp16(u);
+    return (g / (1.0f + expf(-g))) * u;  // E:4355
+}
 __device__ inline uint16_t f32_to_fp16_bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }

@@ -1,0 +1,195 @@
+// qmm_ffn.hip — the FFN block of one layer at batch 1 in two launches, gfx950.
+//
+// The reference's CPU path for the block (E:8287-8296) is three steps: the
+// {gate, up} task group on the normed input row, swiglu_fp16_rows_fast (h =
+// silu(gate) * up and h's Q8_K, E:4326-4378), and the down task with its
+// residual on that Q8_K. Here:
+//
+//  1. gate/up (this file): a persistent grid whose waves take groups of two
+//     row pairs — gate rows 2p, 2p + 1 and the same up rows, one contiguous
+//     span of each, staged through LDS — with the lanes, per-block
+//     expression and in-order block sums of the batch-1 GEMV. Each group's
+//     epilogue writes gate and up, h = silu(g) * u, and h rounded to fp16
+//     (the quantizer's input): the SwiGLU step costs no launch of its own.
+//  2. down: the batch-1 persistent GEMV on that fp16 row, which quantizes it
+//     to Q8_K in LDS (the reference's quantizer) while the first weights
+//     are in flight.
+// The launch boundary orders h's writes before its reads. Every output
+// equals the three separate steps' bit for bit: the same block terms,
+// summed in the same order, and the same Q8_K codes of h.
+#include "qmm_gemv_parts.h"
+
+namespace qmm {
+
+namespace {
+
+constexpr int kRP = 2;  // row pairs per gate/up group (4 rows)
+constexpr int kU = 3;   // wave steps of 16 blocks per batch: 48 blocks
+
+__host__ __device__ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// LDS: x codes | per-wave block terms and dump | per-wave stage
+__host__ __device__ inline size_t terms_bytes(int K) {
+    return align_up(size_t(4) * (2 * kRP * (K / 256) + 64) * 4, 16);
+}
+__host__ __device__ inline size_t gate_up_lds_bytes(int K, int nc) {
+    return gemv_act_lds_bytes(false, K) + terms_bytes(K) + size_t(4) * nc * 1024;
+}
+
+__device__ inline void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Row sum of nb block terms in block order (eval_single_lm_row_dot's order).
+__device__ inline float row_sum(const float *cr, int nb) {
+    float acc = 0.0f;
+    int bb = 0;
+    for (; bb + 8 <= nb; bb += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = cr[bb + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += v[i];
+    }
+    for (; bb < nb; ++bb) acc += cr[bb];
+    return acc;
+}
+
+}  // namespace
+
+// FUSED: x32 is quantized here; otherwise prek holds the prequantized input
+// row. NC: 16-B stage loads per lane of a group.
+template <bool FUSED, int NC>
+__global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float *__restrict__ x32, Q8KView prek) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    using FG = FmtQ4K4;
+    constexpr int SLOTS = 64 / FG::G;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int g = lane / FG::G, k = lane % FG::G;
+    const int K = a.K, F = a.F, nb = K / 256;
+    const int ngroups = (F + kRP - 1) / kRP;
+
+    const LdsAct act = gemv_act_view(lds, false, K);
+    const size_t act_b = gemv_act_lds_bytes(false, K);
+    float *contrib = reinterpret_cast<float *>(lds + act_b) + wid * (2 * kRP * nb + 64);
+    float *dump = contrib + 2 * kRP * nb;
+    uint8_t *stage = lds + act_b + terms_bytes(K) + size_t(wid) * NC * 1024;
+
+    // a group's bytes: the gate span, then the up span (both 16-B aligned;
+    // chunk indices clamped so every lane issues its loads)
+    uint4 st[NC];
+    auto stage_load = [&](int gp) __attribute__((always_inline)) {
+        const int rows = min(kRP, F - gp * kRP);
+        const int half = rows * (a.rb1 >> 4);
+        const uint8_t *sg = a.wg + size_t(gp) * kRP * a.rb1;
+        const uint8_t *su = a.wu + size_t(gp) * kRP * a.rb1;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = min(64 * j + lane, 2 * half - 1);
+            st[j] = ld16_nt(c < half ? sg + 16 * c : su + 16 * (c - half));
+        }
+    };
+
+    // 1. the input row, then the first group's bytes; the input into LDS
+    int gw = int(blockIdx.x) * 4 + wid;
+    const int stride = int(gridDim.x) * 4;
+    XPre xp;
+    CPre cp;
+    if constexpr (FUSED) {
+        if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
+    } else {
+        cpre_load<false>(prek.qs, prek.d, prek.bs, K, cp);
+    }
+    if constexpr (FUSED) wait_vmcnt<0>();  // x before the weights (as in the persistent GEMV)
+    __builtin_amdgcn_sched_barrier(0);
+    if (gw < ngroups) stage_load(gw);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FUSED) x_fill<false, false>(xp, x32, K, act);
+    else cpre_fill<false, false>(cp, prek.qs, prek.d, prek.bs, K, act);
+    lds_barrier();
+
+    // 2. groups; each step requests the next group's bytes first
+    const int adv = SLOTS % nb;
+    for (; gw < ngroups; gw += stride) {
+        const int rows = min(kRP, F - gw * kRP);
+        const int nblk = 2 * rows * nb;
+        wave_lds_fence();
+#pragma unroll
+        for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+        wave_lds_fence();
+        if (gw + stride < ngroups) stage_load(gw + stride);
+        int b = g % nb;
+        FG::Raw rs[kU];
+        FG::Act as[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int f = u * SLOTS + g;
+            const bool own = f < nblk;
+            rs[u] = FG::load(stage + (own ? f : 0) * FG::BB, k);
+            as[u] = FG::load_act(act, own ? b : 0, k);
+            b += adv;
+            b = b >= nb ? b - nb : b;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int f = u * SLOTS + g;
+            const float c = FG::compute(rs[u], as[u], k);
+            *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
+        }
+        wave_lds_fence();
+        // lanes 0 .. rows-1: gate rows, rows .. 2 rows-1: the same up rows
+        const float acc = lane < 2 * rows ? row_sum(contrib + lane * nb, nb) : 0.0f;
+        const float upv = __shfl(acc, lane + rows);
+        const float hv = silu_mul(acc, upv);  // (meaningful in the gate lanes)
+        const float hv1 = __shfl(hv, 1);
+        if (lane < 2 * rows) {
+            const bool gate = lane < rows;
+            const int row = gw * kRP + (gate ? lane : lane - rows);
+            float *dst = gate ? a.g : a.u;
+            if (dst) dst[row] = acc;
+            if (gate && a.h_out) a.h_out[row] = hv;
+        }
+        if (lane == 0)  // the group's two h rows in fp16 (F is even: whole pairs)
+            a.hx[gw] = uint32_t(f32_to_fp16_bits(hv)) | (uint32_t(f32_to_fp16_bits(hv1)) << 16);
+    }
+}
+
+namespace {
+
+int cus_of_device() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <bool FUSED, int NC>
+hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
+    const int ngroups = (a.F + kRP - 1) / kRP;
+    const int quads = (ngroups + 3) / 4;
+    // a persistent grid as the batch-1 GEMV's: 5/8 of a workgroup per four
+    // groups, at most three per CU
+    const int cus = cus_of_device();
+    const int wgs = max(1, min(3 * cus, quads * 5 / 8));
+    hipLaunchKernelGGL((ffn_gate_up_kernel<FUSED, NC>), dim3(unsigned(wgs)), dim3(256), gate_up_lds_bytes(a.K, NC), s,
+                       a, x32, xk);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_ffn_gate_up(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
+    if (a.K % 256 || a.K > 3072 || a.F % 256 || a.F <= 0 || a.rb1 % 16 || !a.hx) return hipErrorNotSupported;
+    if (!x32 && (!xk.qs || !xk.d || !xk.bs)) return hipErrorNotSupported;
+    const int need = (2 * kRP * (a.K / 256) * FmtQ4K4::BB + 1023) / 1024;  // 16-B loads per lane
+    if (x32) return need <= 6 ? launch_gate_up_t<true, 6>(a, x32, xk, s) : launch_gate_up_t<true, 7>(a, x32, xk, s);
+    return need <= 6 ? launch_gate_up_t<false, 6>(a, x32, xk, s) : launch_gate_up_t<false, 7>(a, x32, xk, s);
+}
+
+}  // namespace qmm

@@ -89,15 +89,8 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     if (sub == 0) d[blk] = q8_scale(a);
 }
 
-// swiglu_chunk_worker (E:4349-4357): gate and up are the dispatcher's fp16
-// outputs in the reference, so each fp32 input is rounded to fp16 first
-// (E:4352-4353); h = (g / (1 + expf(-g))) * u in fp32, then the same fp16
-// round + Q8_K quantizer per 256-value block.
-__device__ inline float silu_mul(float g, float u) {
-    g = round_to_fp16(g);
-    u = round_to_fp16(u);
-    return (g / (1.0f + expf(-g))) * u;  // E:4355
-}
+// swiglu_chunk_worker (E:4349-4357): h = silu_mul(gate, up) per value, then
+// the fp16 round + Q8_K quantizer per 256-value block.
 __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float *__restrict__ gate,
                                                          const float *__restrict__ up,
                                                          size_t nblk, float *__restrict__ h, Q8KOut o, int nb) {

@@ -89,6 +89,7 @@ _SIGNATURES = [
     ("qmm_quantize_q8_0", C.c_int, [_p, _p, C.c_int, C.c_int, _p]),
     ("qmm_swiglu_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_rmsnorm_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
+    ("qmm_ffn_block", C.c_int, [_p, _p, _p, C.c_int, _p, _p, _p, _p]),
     ("qmm_gguf_open", C.c_int, [C.c_char_p, _p]),
     ("qmm_gguf_close", C.c_int, [_p]),
     ("qmm_gguf_header", C.c_int, [_p, _p, _p, _p, _p]),
@@ -421,6 +422,13 @@ class Context:
     def swiglu_q8k(self, gate, up, M: int, N: int, h_out, out):
         self._call("qmm_swiglu_q8k", self._h, _p(_addr(gate)), _p(_addr(up)), M, N,
                    _p(_addr(h_out)), _p(_addr(out)))
+
+    def ffn_block(self, x, q8k, K: int, gate: MatrixTask, up: MatrixTask, down: MatrixTask, h_out=None):
+        """qmm_ffn_block: give exactly one of x (fp32 [K]) and q8k."""
+        gu = self._tasks(1, K, [gate, up])
+        dn = self._tasks(1, down.cols, [down])
+        self._call("qmm_ffn_block", self._h, _p(_addr(x)), _p(_addr(q8k)), K, C.byref(gu[0]), C.byref(gu[1]),
+                   C.byref(dn[0]), _p(_addr(h_out)))
 
     def dequantize_f16(self, w, type_id: int, rows: int, cols: int, dst):
         self._call("qmm_dequantize_f16", self._h, _p(_addr(w)), type_id, rows, cols, _p(_addr(dst)))
