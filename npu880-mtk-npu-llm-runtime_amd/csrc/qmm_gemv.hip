@@ -11,12 +11,12 @@
 // eval_single_lm_row_dot (E:10986-11105), so the result equals the
 // reference's fp32 sum bit for bit.
 //
-// Weight bytes. Q4_K / Q5_K blocks (144 / 176 B) are 16-B aligned: lanes
-// load their pieces straight from HBM with 16-B loads. Q6_K / Q8_0 blocks
-// (210 / 34 B) are only 2-B aligned: the wave loads the contiguous bytes of
-// U wave steps with 16-B loads into an LDS stage and lanes read their
-// pieces from there (two-byte realignment costs LDS reads, not HBM
-// transactions).
+// Weight bytes. Every format is staged: the wave loads the contiguous bytes
+// of U wave steps with 16-B loads into an LDS stage and lanes read their
+// pieces from there, so each byte moves in a full 16-B transaction whatever
+// the block's alignment (Q4_K / Q5_K blocks of 144 / 176 B are 16-B aligned;
+// Q6_K / Q8_0 blocks of 210 / 34 B only 2-B aligned: two-byte realignment
+// costs LDS reads, not HBM transactions).
 //
 // Activations live in LDS for the whole workgroup. The fp32 input (or the
 // prequantized row) is requested first, then the first batch of weights;
@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const flo
     const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
     switch (a.type) {
         case kQ4_K: gemv_wg<FmtQ4K4, R, 3, FUSED, stage_chunks<FmtQ4K4, 3>()>(a, bx, x32, prek, pre0); break;
-        case kQ5_K: gemv_wg<FmtQ5K, R, kGemvU, FUSED, 0>(a, bx, x32, prek, pre0); break;
+        case kQ5_K: gemv_wg<FmtQ5K4, R, 3, FUSED, stage_chunks<FmtQ5K4, 3>()>(a, bx, x32, prek, pre0); break;
         case kQ6_K: gemv_wg<FmtQ6K4, R, 3, FUSED, stage_chunks<FmtQ6K4, 3>()>(a, bx, x32, prek, pre0); break;
         case kQ8_0: gemv_wg<FmtQ80, R, kGemvU, FUSED, stage_chunks<FmtQ80, kGemvU>()>(a, bx, x32, prek, pre0); break;
         // F32 / F16 rows: one row per wave whatever the group's R (their
@@ -525,7 +525,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
 size_t gemv_lds_bytes(uint32_t type, int K) {
     switch (type) {
         case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K);
-        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, kGemvR, kGemvU>(K);
+        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K4, kGemvR, 3>(K);
         case kQ6_K: return gemv_lds_bytes_t<FmtQ6K4, kGemvR, 3>(K);
         case kQ8_0: return gemv_lds_bytes_t<FmtQ80, kGemvR, kGemvU>(K);
         default: return 0;
@@ -597,6 +597,7 @@ hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk
                               const PrevStep &pre) {
     switch (type) {
         case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
+        case kQ5_K: return launch_gemv_argmax_t<FmtQ5K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
         case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
         default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
     }
@@ -659,7 +660,7 @@ template <int R>
 static size_t gemv_wg_lds(uint32_t type, int K) {
     switch (type) {
         case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, R, 3>(K);
-        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K, R, kGemvU>(K);
+        case kQ5_K: return gemv_lds_bytes_t<FmtQ5K4, R, 3>(K);
         case kQ6_K: return gemv_lds_bytes_t<FmtQ6K4, R, 3>(K);
         case kQ8_0: return gemv_lds_bytes_t<FmtQ80, R, kGemvU>(K);
         default: return 0;
@@ -723,6 +724,7 @@ static hipError_t launch_gemv_x16_t(const MatArgs &a, const uint16_t *x16, hipSt
 hipError_t launch_gemv_x16(uint32_t type, const MatArgs &a, const uint16_t *x16, hipStream_t s, bool launch) {
     switch (type) {
         case kQ4_K: return launch_gemv_x16_t<FmtQ4K4, 3>(a, x16, s, launch);
+        case kQ5_K: return launch_gemv_x16_t<FmtQ5K4, 3>(a, x16, s, launch);
         case kQ6_K: return launch_gemv_x16_t<FmtQ6K4, 3>(a, x16, s, launch);
         default: return hipErrorNotSupported;
     }
@@ -733,7 +735,7 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
     switch (type) {
         case kQ4_K: return launch_gemv_rows<FmtQ4K4, 3>(tasks, n, x32, xk, x0, s);
-        case kQ5_K: return launch_gemv_rows<FmtQ5K, kGemvU>(tasks, n, x32, xk, x0, s);
+        case kQ5_K: return launch_gemv_rows<FmtQ5K4, 3>(tasks, n, x32, xk, x0, s);
         case kQ6_K: return launch_gemv_rows<FmtQ6K4, 3>(tasks, n, x32, xk, x0, s);
         case kQ8_0: return launch_gemv_rows<FmtQ80, kGemvU>(tasks, n, x32, xk, x0, s);
         case kF32:

@@ -22,47 +22,10 @@ __device__ inline float row16_max(float v) {
 }
 
 // ----------------------------------------------------------------- Q4_K
-// Block (144 B): d f16 @0, dmin f16 @2, scales[12] @4, codes[128] @16.
-// Lane k of 8: chunk j = k/2 (64 values), half lh = k%2 -> code bytes
-// [16 + 32j + 16lh, +16): low nibbles = values 64j + 16lh + (0..15)
-// (sub-block 2j), high nibbles = 64j + 32 + 16lh + (0..15) (sub-block 2j+1).
-struct FmtQ4K {
-    static constexpr int G = 8, BB = 144, QK = 256;
-    static constexpr bool kStaged = false;
-    struct Raw { uint4 h, c; };
-    struct Act { uint4 xl, xh; uint2 bs; float dx; };
-    __device__ static Raw load(const uint8_t *blk, int k) {
-        return {ld16_nt(blk), ld16_nt(blk + 16 + 16 * k)};
-    }
-    __device__ static Act load_act(const LdsAct &x, int b, int k) {
-        const int j = k >> 1, lh = k & 1;
-        const int8_t *xb = x.qs + b * 272 + 64 * j + 16 * lh;
-        return {ld16(xb), ld16(xb + 32), ld8(x.bs + b * 8 + 2 * j), x.d[b]};
-    }
-    __device__ static float compute(const Raw &r, const Act &a, int k) {
-        const int j = k >> 1, lh = k & 1;
-        int sc0, m0, sc1, m1;
-        scale_min_k4(2 * j, r.h.y, r.h.z, r.h.w, sc0, m0);
-        scale_min_k4(2 * j + 1, r.h.y, r.h.z, r.h.w, sc1, m1);
-        const uint32_t M4 = 0x0F0F0F0Fu;
-        int dot1 = sdot4(int(r.c.x & M4), int(a.xl.x), 0);
-        dot1 = sdot4(int(r.c.y & M4), int(a.xl.y), dot1);
-        dot1 = sdot4(int(r.c.z & M4), int(a.xl.z), dot1);
-        dot1 = sdot4(int(r.c.w & M4), int(a.xl.w), dot1);
-        int dot2 = sdot4(int((r.c.x >> 4) & M4), int(a.xh.x), 0);
-        dot2 = sdot4(int((r.c.y >> 4) & M4), int(a.xh.y), dot2);
-        dot2 = sdot4(int((r.c.z >> 4) & M4), int(a.xh.z), dot2);
-        dot2 = sdot4(int((r.c.w >> 4) & M4), int(a.xh.w), dot2);
-        int S = __mul24(sc0, dot1) + __mul24(sc1, dot2);
-        int Mb = lh ? 0 : __mul24(m0, int(a.bs.x)) + __mul24(m1, int(a.bs.y));
-        S = group8_sum(S);
-        Mb = group8_sum(Mb);
-        const float d = fp16_bits_to_f32(r.h.x & 0xFFFFu);
-        const float dmin = fp16_bits_to_f32(r.h.x >> 16);
-        return a.dx * (d * (float)S - dmin * (float)Mb);  // E:11026
-    }
-};
-
+// Block (144 B): d f16 @0, dmin f16 @2, scales[12] @4, codes[128] @16: code
+// bytes [16 + 32j, +32) hold values 64j + (0..31) in their low nibbles
+// (sub-block 2j) and 64j + 32 + (0..31) in their high nibbles (sub-block
+// 2j+1).
 // Q4_K, 4 lanes per block (the form the library launches): lane k owns
 // the 64 values of chunk k — code bytes [16 + 32k, +32): low nibbles =
 // sub-block 2k, high nibbles = sub-block 2k+1. The wave's span is staged
@@ -115,42 +78,41 @@ struct FmtQ4K4 {
 
 // ----------------------------------------------------------------- Q5_K
 // Block (176 B): d @0, dmin @2, scales[12] @4, qh[32] @16, ql[128] @48.
-// Lane k: chunk j = k/2, half lh = k%2 -> ql bytes [48 + 32j + 16lh, +16),
-// qh bytes [16 + 16lh, +16); high bit of value 64j + l is bit 2j of qh[l],
-// of value 64j + 32 + l bit 2j+1.
-struct FmtQ5K {
-    static constexpr int G = 8, BB = 176, QK = 256;
-    static constexpr bool kStaged = false;
-    struct Raw { uint4 h, qh, ql; };
-    using Act = FmtQ4K::Act;
-    __device__ static Raw load(const uint8_t *blk, int k) {
-        const int j = k >> 1, lh = k & 1;
-        return {ld16_nt(blk), ld16_nt(blk + 16 + 16 * lh), ld16_nt(blk + 48 + 32 * j + 16 * lh)};
+// Q5_K, 4 lanes per block (the form the library launches): lane k owns the
+// 64 values of chunk k — ql bytes [48 + 32k, +32): low nibbles = sub-block
+// 2k, high nibbles = sub-block 2k+1 — and reads the whole qh[32]: the high
+// bit of value 64k + l is bit 2k of qh[l], of value 64k + 32 + l bit 2k+1.
+// The wave's span is staged through LDS (176-B blocks stay 16-B aligned).
+struct FmtQ5K4 {
+    static constexpr int G = 4, BB = 176, QK = 256;
+    static constexpr bool kStaged = true;
+    struct Raw { uint4 h, qh0, qh1, c0, c1; };
+    using Act = FmtQ4K4::Act;
+    __device__ static Raw load(const uint8_t *blk, int k) {  // blk points into the LDS stage
+        return {ld16(blk), ld16(blk + 16), ld16(blk + 32), ld16(blk + 48 + 32 * k), ld16(blk + 64 + 32 * k)};
     }
-    __device__ static Act load_act(const LdsAct &x, int b, int k) { return FmtQ4K::load_act(x, b, k); }
+    __device__ static Act load_act(const LdsAct &x, int b, int k) { return FmtQ4K4::load_act(x, b, k); }
     __device__ static float compute(const Raw &r, const Act &a, int k) {
-        const int j = k >> 1, lh = k & 1;
-        int sc0, m0, sc1, m1;
-        scale_min_k4(2 * j, r.h.y, r.h.z, r.h.w, sc0, m0);
-        scale_min_k4(2 * j + 1, r.h.y, r.h.z, r.h.w, sc1, m1);
+        uint32_t SC, MM;
+        scale_pair_k4(k, r.h.y, r.h.z, r.h.w, SC, MM);
         const uint32_t M4 = 0x0F0F0F0Fu, M1 = 0x01010101u;
-        const uint32_t s0 = 2 * j, s1 = 2 * j + 1;
-        const uint32_t qlv[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
-        const uint32_t qhv[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-        const uint32_t xl[4] = {a.xl.x, a.xl.y, a.xl.z, a.xl.w};
-        const uint32_t xh[4] = {a.xh.x, a.xh.y, a.xh.z, a.xh.w};
+        const uint32_t s0 = 2 * k, s1 = 2 * k + 1;
+        const uint32_t c[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+        const uint32_t qh[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
+        const uint32_t xl[8] = {a.x0.x, a.x0.y, a.x0.z, a.x0.w, a.x1.x, a.x1.y, a.x1.z, a.x1.w};
+        const uint32_t xh[8] = {a.x2.x, a.x2.y, a.x2.z, a.x2.w, a.x3.x, a.x3.y, a.x3.z, a.x3.w};
         int dot1 = 0, dot2 = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = (qlv[i] & M4) | (((qhv[i] >> s0) & M1) << 4);
-            const uint32_t hi = ((qlv[i] >> 4) & M4) | (((qhv[i] >> s1) & M1) << 4);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = (c[i] & M4) | (((qh[i] >> s0) & M1) << 4);
+            const uint32_t hi = ((c[i] >> 4) & M4) | (((qh[i] >> s1) & M1) << 4);
             dot1 = sdot4(int(lo), int(xl[i]), dot1);
             dot2 = sdot4(int(hi), int(xh[i]), dot2);
         }
-        int S = __mul24(sc0, dot1) + __mul24(sc1, dot2);
-        int Mb = lh ? 0 : __mul24(m0, int(a.bs.x)) + __mul24(m1, int(a.bs.y));
-        S = group8_sum(S);
-        Mb = group8_sum(Mb);
+        int S = __mul24(int(SC & 0xFF), dot1) + __mul24(int(SC >> 8), dot2);
+        int Mb = __mul24(int(MM & 0xFF), int(a.bs.x)) + __mul24(int(MM >> 8), int(a.bs.y));
+        S = group4_sum(S);
+        Mb = group4_sum(Mb);
         const float d = fp16_bits_to_f32(r.h.x & 0xFFFFu);
         const float dmin = fp16_bits_to_f32(r.h.x >> 16);
         return a.dx * (d * (float)S - dmin * (float)Mb);  // E:11063

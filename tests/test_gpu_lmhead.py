@@ -6,7 +6,7 @@ import pytest
 
 import synth
 from gpu_util import check_outputs, say
-from oracle import TYPE_Q4_K, TYPE_Q6_K
+from oracle import TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K
 
 pytestmark = pytest.mark.gpu
 
@@ -77,7 +77,7 @@ def test_eval_rows(ctx, oracle, M):
         ctx.free(b)
 
 
-@pytest.mark.parametrize("type_id", [TYPE_Q6_K, TYPE_Q4_K])
+@pytest.mark.parametrize("type_id", [TYPE_Q6_K, TYPE_Q4_K, TYPE_Q5_K])
 def test_lm_head_tall_chunks(ctx, oracle, type_id):
     """One row, no logits requested, chunks tall enough for the persistent
     GEMV grid. Ties planted inside a chunk and across chunks (the earlier row

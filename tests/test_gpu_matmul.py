@@ -44,7 +44,7 @@ def test_gemv_q6k_lm_head_shape(ctx, oracle):
 
 
 @pytest.mark.parametrize("type_id,N,K,residual", [(TYPE_Q4_K, 60001, 256, True), (TYPE_Q8_0, 50003, 512, False),
-                                                  (TYPE_Q6_K, 49157, 768, True)])
+                                                  (TYPE_Q6_K, 49157, 768, True), (TYPE_Q5_K, 40007, 512, True)])
 def test_gemv_tall_tensors(ctx, oracle, type_id, N, K, residual):
     """Tensors tall enough for the persistent grid (several row groups per
     wave, the next group prefetched), with ragged last groups."""
@@ -52,7 +52,8 @@ def test_gemv_tall_tensors(ctx, oracle, type_id, N, K, residual):
 
 
 @pytest.mark.parametrize("type_id,N,K,residual", [(TYPE_Q4_K, 9727, 2560, True), (TYPE_Q6_K, 8195, 768, False),
-                                                  (TYPE_Q8_0, 8200, 288, True), (TYPE_Q4_K, 8192, 3072, False)])
+                                                  (TYPE_Q8_0, 8200, 288, True), (TYPE_Q4_K, 8192, 3072, False),
+                                                  (TYPE_Q5_K, 8192, 2560, False), (TYPE_Q5_K, 9733, 3072, True)])
 def test_gemv_two_group_grid(ctx, oracle, type_id, N, K, residual):
     """The persistent batch-1 grid where no wave has more than two row groups
     (60 % of the waves have a second, prefetched): ragged last groups, groups
