@@ -287,6 +287,8 @@ __device__ inline int group8_sum(int v) {
 typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 // 16 B load of an address that is 16-B aligned.
 __device__ inline uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
+// cache policy of a buffer load: non-temporal (streaming, read once)
+constexpr int kNonTemporal = 2;
 // streaming (non-temporal) 16 B load: weights are read exactly once
 __device__ inline uint4 ld16_nt(const void *p) {
     const v4u32 v = __builtin_nontemporal_load(reinterpret_cast<const v4u32 *>(p));

@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
     constexpr bool q80 = IsQ80<F>::v;
     if (scan_stopped(a.scan)) return;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int g = lane / G, k = lane % G;
     const int K = a.K, nb = K / F::QK;
     const int ngroups = (a.N + R - 1) / R;
@@ -365,17 +365,24 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     const float *pd = q80 ? pre0.d : prek.d;
     const int32_t *pb = prek.bs;
 
-    // a group's bytes from the 16-B boundary at or below its first byte;
-    // chunk indices clamped so every lane issues its loads
+    // a group's bytes from the 16-B boundary at or below its first byte,
+    // through a descriptor that ends with the group (rounded up to a 16-B
+    // granule: the range check is per dword, and a granule never crosses a
+    // page): lanes past the end read zeros and request no memory. The group
+    // index is wave-uniform, so its address is scalar arithmetic and every
+    // lane's offset is fixed.
     static_assert(NC <= NST, "stage loads beyond the stage");
     uint4 st[NC];
     auto stage_load = [&](int gr) __attribute__((always_inline)) {
         const int rows = max(0, min(R, a.N - gr * R));
         const uint8_t *span = a.w + size_t(rows > 0 ? gr * R : 0) * a.row_bytes;
         const int mis = int(reinterpret_cast<uintptr_t>(span) & 15);
-        const int nchunks = (mis + max(rows * nb, 1) * F::BB + 15) >> 4;
+        const int bytes = (mis + max(rows * nb, 1) * F::BB + 15) & ~15;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(span - mis), short(0), bytes, 0x00020000);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) st[j] = ld16_nt(span - mis + 16 * min(64 * j + lane, nchunks - 1));
+        for (int j = 0; j < NC; ++j)
+            st[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t(16 * (64 * j + lane)), 0, kNonTemporal));
     };
 
     int gw = int(blockIdx.x) * 4 + wid;
