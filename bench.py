@@ -905,7 +905,7 @@ def main():
         "tokens_per_s_equiv": round(value * 1e9 / DECODE_BYTES_PER_TOKEN, 1),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic(TRAFFIC_PROFILE),
-                     "kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, true, 6, false> (fused Q8_K quantizer)",
+                     "kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, true, 6, false, false> (fused Q8_K quantizer)",
                      "us_per_launch": round(ms * 1e3, 3), "algorithmic_bytes": head["step_bytes"],
                      "floor_us_per_launch": floor["us_per_launch"],
                      "frac_of_measured_floor": round(floor["us_per_launch"] / (ms * 1e3), 4)},
