@@ -208,7 +208,7 @@ def bench_headline(ctx, args):
     log(f"GEMV on prequantized Q8_K: {ms_pre * 1e3:.3f} us; one replica (cache-resident): {ms_hot * 1e3:.3f} us")
     floor = bench_stream_floor(ctx, W, args)
     out = dict(ms=ms, wall=wall, step_bytes=step_bytes, parity=parity, R=W.R, wbytes=W.bytes,
-               gemv_prequantized={"kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, false, 6, false> on Q8_K input",
+               gemv_prequantized={"kernel": "gemv_persist_kernel<FmtQ4K4, 4, 3, false, 6, false, false> on Q8_K input",
                                   "us_per_launch": round(ms_pre * 1e3, 3), "algorithmic_bytes": kern_bytes,
                                   "gbs": round(gbs(kern_bytes, ms_pre), 1)},
                cache_resident_us_per_launch=round(ms_hot * 1e3, 3), hbm_read_floor=floor)
