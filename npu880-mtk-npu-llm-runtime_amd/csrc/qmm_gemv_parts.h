@@ -95,8 +95,11 @@ struct FmtQ5K4 {
     __device__ static float compute(const Raw &r, const Act &a, int k) {
         uint32_t SC, MM;
         scale_pair_k4(k, r.h.y, r.h.z, r.h.w, SC, MM);
-        const uint32_t M4 = 0x0F0F0F0Fu, M1 = 0x01010101u;
-        const uint32_t s0 = 2 * k, s1 = 2 * k + 1;
+        const uint32_t M4 = 0x0F0F0F0Fu, B4 = 0x10101010u;
+        // rotating a qh dword right by 2k - 4 (mod 32) puts bit 2k of each
+        // byte at bit 4 and bit 2k + 1 at bit 5; what crosses a byte boundary
+        // lands in bits the masks drop
+        const uint32_t rot = uint32_t(2 * k - 4) & 31u;
         const uint32_t c[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
         const uint32_t qh[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
         const uint32_t xl[8] = {a.x0.x, a.x0.y, a.x0.z, a.x0.w, a.x1.x, a.x1.y, a.x1.z, a.x1.w};
@@ -104,8 +107,9 @@ struct FmtQ5K4 {
         int dot1 = 0, dot2 = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t lo = (c[i] & M4) | (((qh[i] >> s0) & M1) << 4);
-            const uint32_t hi = ((c[i] >> 4) & M4) | (((qh[i] >> s1) & M1) << 4);
+            const uint32_t h = __builtin_amdgcn_alignbit(qh[i], qh[i], rot);
+            const uint32_t lo = (c[i] & M4) | (h & B4);
+            const uint32_t hi = ((c[i] >> 4) & M4) | ((h >> 1) & B4);
             dot1 = sdot4(int(lo), int(xl[i]), dot1);
             dot2 = sdot4(int(hi), int(xh[i]), dot2);
         }
