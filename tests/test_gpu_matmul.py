@@ -115,6 +115,16 @@ def test_mfma_small_m_long_k(ctx, oracle, type_id, K, M):
     _run(ctx, oracle, type_id, 70, K, M, seed=900 + K + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q6_K, 2560, 9728, 64), (TYPE_Q5_K, 300, 4096, 40),
+                                           (TYPE_Q4_K, 333, 9728, 17), (TYPE_Q6_K, 200, 3328, 33),
+                                           (TYPE_Q8_0, 2560, 2560, 48), (TYPE_Q4_K, 1000, 4096, 9),
+                                           (TYPE_Q8_0, 130, 9728, 64)])
+def test_mfma_k_split_tiles(ctx, oracle, type_id, N, K, M):
+    """9..64 tokens over K > 3072 (and Q8_0 at any K): 16 x 16 tiles whose
+    chunks are split over the 4 waves and summed in block order."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1700 + K + M)
+
+
 @pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 6144, 2560, 8), (TYPE_Q6_K, 13000, 1024, 3),
                                            (TYPE_Q5_K, 300, 3072, 16), (TYPE_Q4_K, 4111, 768, 11),
                                            (TYPE_Q6_K, 3000, 2560, 7)])
@@ -125,7 +135,7 @@ def test_resident_tile_layouts(ctx, oracle, type_id, N, K, M):
     _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
 
 
-@pytest.mark.parametrize("M", [8, 16, 32, 64])
+@pytest.mark.parametrize("M", [8, 16, 32, 48, 64])
 def test_tree_verify_q4k(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q4_K, 9728, 2560, M, seed=2000 + M)
 
