@@ -305,7 +305,8 @@ def gemm_line(name, M, N, K, type_id, ms, extra_bytes=0):
 def bench_tree(ctx, args):
     steps = max(50, args.steps // 4)
     out = {}
-    for label, (t, N, K) in (("q4k_9728x2560", synth.TREE_VERIFY["q4k"]), ("q5k_4096x2560", synth.TREE_VERIFY["q5k"])):
+    for label, (t, N, K) in (("q4k_9728x2560", synth.TREE_VERIFY["q4k"]), ("q5k_4096x2560", synth.TREE_VERIFY["q5k"]),
+                             ("q6k_2560x9728", synth.TREE_VERIFY["q6k"])):
         W = Replicated(ctx, t, N, K, 0, seed=10 + t)
         lines = {}
         for M in synth.TREE_VERIFY["M"]:

@@ -111,7 +111,8 @@ def lm_head_small_logits(rows: int, cols: int, seed: int) -> np.ndarray:
 GEMV_Q4K = dict(type=TYPE_Q4_K, N=9728, K=2560)
 GEMV_Q6K_LMHEAD = dict(type=TYPE_Q6_K, N=151936, K=2560)
 FFN = dict(gate=(TYPE_Q4_K, 9728, 2560), up=(TYPE_Q4_K, 9728, 2560), down=(TYPE_Q6_K, 2560, 9728))
-TREE_VERIFY = dict(M=(8, 16, 32, 64), q4k=(TYPE_Q4_K, 9728, 2560), q5k=(TYPE_Q5_K, 4096, 2560))
+TREE_VERIFY = dict(M=(8, 16, 32, 64), q4k=(TYPE_Q4_K, 9728, 2560), q5k=(TYPE_Q5_K, 4096, 2560),
+                   q6k=(TYPE_Q6_K, 2560, 9728))
 PREFILL_LAYER = dict(
     M=512,
     tensors=dict(qkv=(TYPE_Q5_K, 6144, 2560), o=(TYPE_Q4_K, 2560, 4096),
