@@ -26,34 +26,14 @@ namespace {
 constexpr int kRP = 2;  // row pairs per gate/up group (4 rows)
 constexpr int kU = 3;   // wave steps of 16 blocks per batch: 48 blocks
 
-__host__ __device__ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-// LDS: x codes | per-wave block terms and dump | per-wave stage
-__host__ __device__ inline size_t terms_bytes(int K) {
-    return align_up(size_t(4) * (2 * kRP * (K / 256) + 64) * 4, 16);
-}
+// LDS: x codes | per-wave stage
 __host__ __device__ inline size_t gate_up_lds_bytes(int K, int nc) {
-    return gemv_act_lds_bytes(false, K) + terms_bytes(K) + size_t(4) * nc * 1024;
+    return gemv_act_lds_bytes(false, K) + size_t(4) * nc * 1024;
 }
 
 __device__ inline void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-}
-
-// Row sum of nb block terms in block order (eval_single_lm_row_dot's order).
-__device__ inline float row_sum(const float *cr, int nb) {
-    float acc = 0.0f;
-    int bb = 0;
-    for (; bb + 8 <= nb; bb += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = cr[bb + i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc += v[i];
-    }
-    for (; bb < nb; ++bb) acc += cr[bb];
-    return acc;
 }
 
 }  // namespace
@@ -64,7 +44,6 @@ template <bool FUSED, int NC>
 __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float *__restrict__ x32, Q8KView prek) {
     extern __shared__ __align__(16) uint8_t lds[];
     using FG = FmtQ4K4;
-    constexpr int SLOTS = 64 / FG::G;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / FG::G, k = lane % FG::G;
     const int K = a.K, F = a.F, nb = K / 256;
@@ -72,9 +51,7 @@ __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float
 
     const LdsAct act = gemv_act_view(lds, false, K);
     const size_t act_b = gemv_act_lds_bytes(false, K);
-    float *contrib = reinterpret_cast<float *>(lds + act_b) + wid * (2 * kRP * nb + 64);
-    float *dump = contrib + 2 * kRP * nb;
-    uint8_t *stage = lds + act_b + terms_bytes(K) + size_t(wid) * NC * 1024;
+    uint8_t *stage = lds + act_b + size_t(wid) * NC * 1024;
 
     // a group's bytes: the gate span, then the up span (both 16-B aligned;
     // chunk indices clamped so every lane issues its loads)
@@ -109,48 +86,62 @@ __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float
     else cpre_fill<false, false>(cp, prek.qs, prek.d, prek.bs, K, act);
     lds_barrier();
 
-    // 2. groups; each step requests the next group's bytes first
-    const int adv = SLOTS % nb;
+    // 2. groups; each step requests the next group's bytes first. The
+    // group's 4 rows (r = 0, 1: gate rows 2p, 2p + 1; r = 2, 3: the same up
+    // rows) take 4 lane groups each (16 lanes, one DPP row): lane group q of
+    // row r computes the row's blocks q bpg .. q bpg + bpg - 1, and the row
+    // sum runs along the 4 groups in registers, blocks in order
+    // (eval_single_lm_row_dot's accumulation): group q adds its run to the
+    // sum group q - 1 passes it. Slots past the row's blocks add +0.0, which
+    // leaves every sum unchanged (none is -0.0: each starts from +0.0).
+    // Row r's sum ends in lane 16 r + 12.
+    const int bpg = (nb + 3) / 4;  // <= kU (K <= 3072)
+    const int r = g / 4, q = g % 4;
     for (; gw < ngroups; gw += stride) {
         const int rows = min(kRP, F - gw * kRP);
-        const int nblk = 2 * rows * nb;
+        const bool rown = (r & 1) < rows;
+        const int srow = r < kRP ? r : rows + (r - kRP);  // the row's place in the stage
         wave_lds_fence();
 #pragma unroll
         for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
         wave_lds_fence();
         if (gw + stride < ngroups) stage_load(gw + stride);
-        int b = g % nb;
         FG::Raw rs[kU];
         FG::Act as[kU];
+        bool own[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int f = u * SLOTS + g;
-            const bool own = f < nblk;
-            rs[u] = FG::load(stage + (own ? f : 0) * FG::BB, k);
-            as[u] = FG::load_act(act, own ? b : 0, k);
-            b += adv;
-            b = b >= nb ? b - nb : b;
+            const int b = q * bpg + u;
+            own[u] = u < bpg && b < nb && rown;
+            rs[u] = FG::load(stage + (own[u] ? srow * nb + b : 0) * FG::BB, k);
+            as[u] = FG::load_act(act, own[u] ? b : 0, k);
         }
+        float c[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int f = u * SLOTS + g;
-            const float c = FG::compute(rs[u], as[u], k);
-            *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
+            const float v = FG::compute(rs[u], as[u], k);
+            c[u] = own[u] ? v : 0.0f;
         }
-        wave_lds_fence();
-        // lanes 0 .. rows-1: gate rows, rows .. 2 rows-1: the same up rows
-        const float acc = lane < 2 * rows ? row_sum(contrib + lane * nb, nb) : 0.0f;
-        const float upv = __shfl(acc, lane + rows);
-        const float hv = silu_mul(acc, upv);  // (meaningful in the gate lanes)
-        const float hv1 = __shfl(hv, 1);
-        if (lane < 2 * rows) {
-            const bool gate = lane < rows;
-            const int row = gw * kRP + (gate ? lane : lane - rows);
+        float acc = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {  // row_shr:4 gives groups q = 0 a +0.0 start
+            float t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x114, 0xF,
+                                                                            0xF, true));
+#pragma unroll
+            for (int u = 0; u < kU; ++u) t = t + c[u];
+            acc = t;
+        }
+        const float upv = __shfl(acc, lane + 32);  // lane 16 r + 12: up row r - 2 + 2 = r + 2's sum
+        const float hv = silu_mul(acc, upv);       // (meaningful in the gate lanes 12, 28)
+        const float hv1 = __shfl(hv, lane + 16);   // lane 12: gate row 1's h
+        if (q == 3 && k == 0 && rown) {
+            const bool gate = r < kRP;
+            const int row = gw * kRP + (r & 1);
             float *dst = gate ? a.g : a.u;
             if (dst) dst[row] = acc;
             if (gate && a.h_out) a.h_out[row] = hv;
         }
-        if (lane == 0)  // the group's two h rows in fp16 (F is even: whole pairs)
+        if (lane == 12)  // the group's two h rows in fp16 (F is even: whole pairs)
             a.hx[gw] = uint32_t(f32_to_fp16_bits(hv)) | (uint32_t(f32_to_fp16_bits(hv1)) << 16);
     }
 }

@@ -455,8 +455,18 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     lds_barrier();
-    // 3. groups
-    const int adv = SLOTS % nb;
+    // 3. groups. Where a row's block slots fill one 16-lane DPP row (4
+    // lanes per block, R = SLOTS / 4), the row's GPR = 4 lane groups take its
+    // blocks in consecutive runs of bpg = ceil(nb / 4) <= U, and the row sum
+    // (blocks in order, eval_single_lm_row_dot's accumulation) runs along
+    // them in registers: group q adds its run to the sum group q - 1 passes
+    // it, in GPR steps. Slots past the row's blocks add +0.0, which leaves
+    // every sum unchanged (none is -0.0: each starts from +0.0). Otherwise
+    // the block terms meet in LDS and one lane per row sums them.
+    constexpr bool CHAIN = G == 4 && SLOTS == 4 * R;
+    constexpr int GPR = CHAIN ? SLOTS / R : 1;
+    const int bpg = (nb + GPR - 1) / GPR;
+    [[maybe_unused]] const int adv = SLOTS % nb;
     Best wb{-INFINITY, kNone};  // AMAX: the wave's running (max, first row)
     for (; gw < ngroups; gw += stride) {
         const int row0 = gw * R;
@@ -473,39 +483,77 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         // the next group, in flight during the math (none for a wave's last:
         // a clamped duplicate would cost the address units as much as a new one)
         if (gw + stride < ngroups) stage_load(gw + stride);
-        int b = g % nb;
-        typename F::Raw rs[U];
-        typename F::Act as[U];
+        float acc = 0.0f;
+        int orow = lane;  // the row (of the group) this lane's acc belongs to
+        bool wr = lane < nrows;
+        if constexpr (CHAIN) {
+            const int r = g / GPR, q = g % GPR;  // row, its lane group's place in the row
+            typename F::Raw rs[U];
+            typename F::Act as[U];
+            bool own[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const bool own = u * SLOTS + g < nblk;
-            rs[u] = F::load(stage + mis + (u * SLOTS + g) * F::BB, k);
-            as[u] = F::load_act(act, own ? b : 0, k);
-            b += adv;
-            b = b >= nb ? b - nb : b;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int f = u * SLOTS + g;
-            const float c = F::compute(rs[u], as[u], k);
-            *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-        // per row, blocks in order (eval_single_lm_row_dot's accumulation)
-        if (lane < nrows) {
-            float acc = 0.0f;
-            const float *cr = contrib + lane * nb;
-            int bb = 0;
-            for (; bb + 8 <= nb; bb += 8) {
-                float v[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = cr[bb + i];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc += v[i];
+            for (int u = 0; u < U; ++u) {
+                const int b = q * bpg + u;  // the row's blocks in runs of bpg
+                own[u] = u < bpg && b < nb && r < nrows;
+                rs[u] = F::load(stage + mis + (own[u] ? r * nb + b : 0) * F::BB, k);
+                as[u] = F::load_act(act, own[u] ? b : 0, k);
             }
-            for (; bb < nb; ++bb) acc += cr[bb];
-            const int row = row0 + lane;
+            float c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float v = F::compute(rs[u], as[u], k);
+                c[u] = own[u] ? v : 0.0f;
+            }
+            // after step h the groups q <= h hold their sums through their
+            // runs; row_shr:4 gives groups q = 0 a +0.0 start
+            float sacc = 0.0f;
+#pragma unroll
+            for (int h = 0; h < GPR; ++h) {
+                float t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sacc), 0x114,
+                                                                                0xF, 0xF, true));
+#pragma unroll
+                for (int u = 0; u < U; ++u) t = t + c[u];
+                sacc = t;
+            }
+            acc = sacc;
+            orow = r;
+            wr = q == GPR - 1 && k == 0 && r < nrows;
+        } else {
+            int b = g % nb;
+            typename F::Raw rs[U];
+            typename F::Act as[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool own = u * SLOTS + g < nblk;
+                rs[u] = F::load(stage + mis + (u * SLOTS + g) * F::BB, k);
+                as[u] = F::load_act(act, own ? b : 0, k);
+                b += adv;
+                b = b >= nb ? b - nb : b;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int f = u * SLOTS + g;
+                const float c = F::compute(rs[u], as[u], k);
+                *((k == 0 && f < nblk) ? contrib + f : dump + lane) = c;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+            // per row, blocks in order (eval_single_lm_row_dot's accumulation)
+            if (lane < nrows) {
+                const float *cr = contrib + lane * nb;
+                int bb = 0;
+                for (; bb + 8 <= nb; bb += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = cr[bb + i];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc += v[i];
+                }
+                for (; bb < nb; ++bb) acc += cr[bb];
+            }
+        }
+        if (wr) {
+            const int row = row0 + orow;
             if (a.res) acc = acc + a.res[row];
             if constexpr (AMAX)
                 if (am.ids && am.ids[row] >= am.id_limit) acc = -1e30f;  // a row past the tensor (E:11150)
