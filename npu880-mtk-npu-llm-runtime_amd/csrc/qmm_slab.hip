@@ -343,6 +343,8 @@ static hipError_t launch_slab_t(const MatArgs *tasks, int n, const typename ActO
     return hipGetLastError();
 }
 
+int mfma_cu_count();
+
 // hipErrorNotSupported (nothing launched) where the slab kernel does not
 // apply: K not a multiple of 256, operand sections missing, rows of an
 // aligned format not 16-B aligned, or offsets past the 32-bit buffer range.
@@ -358,8 +360,16 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
         if (aligned && ((reinterpret_cast<uintptr_t>(tasks[i].w) | tasks[i].row_bytes) & 15)) return hipErrorNotSupported;
         if (size_t(tasks[i].N) * tasks[i].row_bytes + 16 >= (size_t(1) << 31)) return hipErrorNotSupported;
     }
-    // 64 rows x 64 tokens, two workgroups per CU (measured best at M = 512)
-    //                              RW TW PR PD
+    // 64 rows x 64 tokens, two workgroups per CU (measured best at M = 512
+    // where those slabs give at least two workgroups per CU: gate 9728 x
+    // 2560, QKV 6144 x 2560); 64 x 32 (three or four per CU) where they give
+    // fewer (O 2560 x 4096 at M = 512: 28.5 -> 23.9 us, down 2560 x 9728:
+    // 77.8 -> 75.3 us). Measured slower at M = 512: 32 x 128, 32 x 64, 64 x 16,
+    // 32 x 32, three stages, and two row tiles per wave.
+    int slabs = 0;
+    for (int i = 0; i < n; ++i) slabs += (tasks[i].N + 63) / 64;
+    //                                  RW TW PR PD
+    if (slabs * ((a.M + 63) / 64) < 2 * mfma_cu_count()) return launch_slab_t<SlabCfg<F, 1, 2, 4, 2>, F>(tasks, n, x, s);
     return launch_slab_t<SlabCfg<F, 1, 4, 4, 2>, F>(tasks, n, x, s);
 }
 
