@@ -110,6 +110,48 @@ __device__ __attribute__((always_inline)) inline void gemv_wg(const MatArgs &a, 
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     if constexpr (F::kStaged) stage_store();
     lds_barrier();
+    // 4a. rows whose blocks fit one batch and whose block slots fill one
+    // 16-lane DPP row (4 lanes per block, R = SLOTS / 4): the row's 4 lane
+    // groups take its blocks in runs of bpg = ceil(nb / 4) <= U and sum them
+    // in order along the groups in registers, as the persistent kernel does
+    // (slots past the row's blocks add +0.0, which changes no sum)
+    constexpr bool CHAIN = F::kStaged && G == 4 && SLOTS == 4 * R && U <= 3;
+    if constexpr (CHAIN) {
+        if (nb <= 4 * U) {
+            const int r = g / 4, q = g % 4, bpg = (nb + 3) / 4;
+            typename F::Raw rs[U];
+            typename F::Act as[U];
+            bool own[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int b = q * bpg + u;
+                own[u] = u < bpg && b < nb && r < nrows;
+                rs[u] = F::load(stage + span_mis + (own[u] ? r * nb + b : 0) * F::BB, k);
+                as[u] = F::load_act(act, own[u] ? b : 0, k);
+            }
+            float c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float v = F::compute(rs[u], as[u], k);
+                c[u] = own[u] ? v : 0.0f;
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {  // row_shr:4 gives groups q = 0 a +0.0 start
+                float t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x114,
+                                                                                0xF, 0xF, true));
+#pragma unroll
+                for (int u = 0; u < U; ++u) t = t + c[u];
+                acc = t;
+            }
+            if (q == 3 && k == 0 && r < nrows) {
+                const int row = row0 + r;
+                if (a.res) acc = acc + a.res[row];
+                a.y[row] = acc;
+            }
+            return;  // (nb is the task's: every wave of the workgroup returns here)
+        }
+    }
     // 4. block terms. b = f mod nb advances by SLOTS mod nb per wave step;
     // every lane stores (lanes that own no term into the dump), so the steps
     // are straight-line code the scheduler can overlap.
