@@ -497,15 +497,17 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     lds_barrier();
-    // 3. groups. Where a row's block slots fill one 16-lane DPP row (4
-    // lanes per block, R = SLOTS / 4), the row's GPR = 4 lane groups take its
-    // blocks in consecutive runs of bpg = ceil(nb / 4) <= U, and the row sum
-    // (blocks in order, eval_single_lm_row_dot's accumulation) runs along
-    // them in registers: group q adds its run to the sum group q - 1 passes
-    // it, in GPR steps. Slots past the row's blocks add +0.0, which leaves
-    // every sum unchanged (none is -0.0: each starts from +0.0). Otherwise
-    // the block terms meet in LDS and one lane per row sums them.
-    constexpr bool CHAIN = G == 4 && SLOTS == 4 * R;
+    // 3. groups. With 4 lanes per block (R = 1, 2 or 4 rows of 16 / R lane
+    // groups each), a row's GPR lane groups take its blocks in consecutive
+    // runs of bpg = ceil(nb / GPR) <= U, and the row sum (blocks in order,
+    // eval_single_lm_row_dot's accumulation) runs along them in registers:
+    // group q adds its run to the sum group q - 1 passes it, in GPR steps.
+    // The sum moves 4 lanes up within a 16-lane DPP row (row_shr:4) and from
+    // a row's lane 15 into the next row (row_bcast:15). Slots past the row's
+    // blocks add +0.0, which leaves every sum unchanged (none is -0.0: each
+    // starts from +0.0). Other formats: the block terms meet in LDS and one
+    // lane per row sums them.
+    constexpr bool CHAIN = G == 4 && SLOTS % R == 0;
     constexpr int GPR = CHAIN ? SLOTS / R : 1;
     const int bpg = (nb + GPR - 1) / GPR;
     [[maybe_unused]] const int adv = SLOTS % nb;
@@ -547,12 +549,18 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
                 c[u] = own[u] ? v : 0.0f;
             }
             // after step h the groups q <= h hold their sums through their
-            // runs; row_shr:4 gives groups q = 0 a +0.0 start
+            // runs (each group takes its left neighbour's sum; groups q = 0
+            // start from +0.0)
             float sacc = 0.0f;
 #pragma unroll
             for (int h = 0; h < GPR; ++h) {
                 float t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sacc), 0x114,
                                                                                 0xF, 0xF, true));
+                if constexpr (GPR > 4) {
+                    const float up = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sacc), 0x142, 0xF, 0xF, true));
+                    t = q == 0 ? 0.0f : (q & 3) == 0 ? up : t;
+                }
 #pragma unroll
                 for (int u = 0; u < U; ++u) t = t + c[u];
                 sacc = t;
