@@ -110,15 +110,16 @@ __device__ __attribute__((always_inline)) inline void gemv_wg(const MatArgs &a, 
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
     if constexpr (F::kStaged) stage_store();
     lds_barrier();
-    // 4a. rows whose blocks fit one batch and whose block slots fill one
-    // 16-lane DPP row (4 lanes per block, R = SLOTS / 4): the row's 4 lane
-    // groups take its blocks in runs of bpg = ceil(nb / 4) <= U and sum them
-    // in order along the groups in registers, as the persistent kernel does
-    // (slots past the row's blocks add +0.0, which changes no sum)
-    constexpr bool CHAIN = F::kStaged && G == 4 && SLOTS == 4 * R && U <= 3;
+    // 4a. rows whose blocks fit one batch, 4 lanes per block (R = 1, 2 or 4
+    // rows of GPR = 16 / R lane groups): the row's lane groups take its
+    // blocks in runs of bpg = ceil(nb / GPR) <= U and sum them in order
+    // along the groups in registers, as the persistent kernel does (slots
+    // past the row's blocks add +0.0, which changes no sum)
+    constexpr bool CHAIN = F::kStaged && G == 4 && SLOTS % R == 0 && U <= 3;
+    constexpr int GPR = CHAIN ? SLOTS / R : 1;
     if constexpr (CHAIN) {
-        if (nb <= 4 * U) {
-            const int r = g / 4, q = g % 4, bpg = (nb + 3) / 4;
+        if (nb <= GPR * U) {
+            const int r = g / GPR, q = g % GPR, bpg = (nb + GPR - 1) / GPR;
             typename F::Raw rs[U];
             typename F::Act as[U];
             bool own[U];
@@ -137,14 +138,19 @@ __device__ __attribute__((always_inline)) inline void gemv_wg(const MatArgs &a, 
             }
             float acc = 0.0f;
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {  // row_shr:4 gives groups q = 0 a +0.0 start
+            for (int h = 0; h < GPR; ++h) {  // each group takes its left neighbour's sum; q = 0 starts at +0.0
                 float t = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x114,
                                                                                 0xF, 0xF, true));
+                if constexpr (GPR > 4) {
+                    const float up = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x142, 0xF, 0xF, true));
+                    t = q == 0 ? 0.0f : (q & 3) == 0 ? up : t;
+                }
 #pragma unroll
                 for (int u = 0; u < U; ++u) t = t + c[u];
                 acc = t;
             }
-            if (q == 3 && k == 0 && r < nrows) {
+            if (q == GPR - 1 && k == 0 && r < nrows) {
                 const int row = row0 + r;
                 if (a.res) acc = acc + a.res[row];
                 a.y[row] = acc;
