@@ -161,7 +161,7 @@ int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, 
  * down: cols = N, any type but Q8_0. N % 256 == 0. Results equal the three
  * steps run as separate calls (qmm_gemm_multi_dispatch, qmm_swiglu_q8k,
  * qmm_gemm_multi_dispatch_prequantized), bit for bit. Two launches where
- * they apply — gate/up Q4_K with K <= 3072 (SwiGLU in the gate/up
+ * they apply — gate/up Q4_K or Q5_K with K <= 3072 (SwiGLU in the gate/up
  * epilogue), down Q4_K or Q6_K with N <= 12288 on the batch-1 persistent
  * grid (h quantized in its prologue) — else the three steps as separate
  * launches. Uses the context's buffers: qmm_reserve(ctx, 1, N) sizes them

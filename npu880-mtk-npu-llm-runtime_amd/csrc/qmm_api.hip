@@ -726,7 +726,8 @@ int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_
     // then the down GEMV on h in fp16
     const qmm::MatArgs da = mat_args(dn, 1, N);
     uint32_t *hx = static_cast<uint32_t *>(hq);
-    if (gate->type == qmm::kQ4_K && dn.rows > 0 && K % 256 == 0 && K <= 3072 && N <= 12288 &&
+    if ((gate->type == qmm::kQ4_K || gate->type == qmm::kQ5_K) && dn.rows > 0 && K % 256 == 0 && K <= 3072 &&
+        N <= 12288 &&
         qmm::launch_gemv_x16(dn.type, da, reinterpret_cast<const uint16_t *>(hx), ctx->stream, false) == hipSuccess) {
         qmm::FfnArgs a{};
         a.wg = static_cast<const uint8_t *>(gate->w_base);
@@ -738,6 +739,7 @@ int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_
         a.K = K;
         a.F = N;
         a.rb1 = int(gate->row_bytes);
+        a.type = gate->type;
         hipError_t e = qmm::launch_ffn_gate_up(a, x, xk, ctx->stream);
         if (e == hipSuccess) e = qmm::launch_gemv_x16(dn.type, da, reinterpret_cast<const uint16_t *>(hx), ctx->stream);
         return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "FFN block launch");

@@ -38,12 +38,13 @@ __device__ inline void wave_lds_fence() {
 
 }  // namespace
 
-// FUSED: x32 is quantized here; otherwise prek holds the prequantized input
-// row. NC: 16-B stage loads per lane of a group.
-template <bool FUSED, int NC>
+// FG: the gate/up format (FmtQ4K4 or FmtQ5K4, 4 lanes per block); FUSED:
+// x32 is quantized here, otherwise prek holds the prequantized input row.
+// NC: 16-B stage loads per lane of a group.
+template <class FG, bool FUSED, int NC>
 __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float *__restrict__ x32, Q8KView prek) {
     extern __shared__ __align__(16) uint8_t lds[];
-    using FG = FmtQ4K4;
+    static_assert(FG::G == 4, "a row's lane groups fill one 16-lane DPP row");
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int g = lane / FG::G, k = lane % FG::G;
     const int K = a.K, F = a.F, nb = K / 256;
@@ -106,8 +107,8 @@ __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float
         for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
         wave_lds_fence();
         if (gw + stride < ngroups) stage_load(gw + stride);
-        FG::Raw rs[kU];
-        FG::Act as[kU];
+        typename FG::Raw rs[kU];
+        typename FG::Act as[kU];
         bool own[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
@@ -160,7 +161,7 @@ int cus_of_device() {
     return cus[dev];
 }
 
-template <bool FUSED, int NC>
+template <class FG, bool FUSED, int NC>
 hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
     const int ngroups = (a.F + kRP - 1) / kRP;
     const int quads = (ngroups + 3) / 4;
@@ -169,9 +170,24 @@ hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &x
     // workgroups 15.9 us, 760 16.1, 1024 16.7, 384 17.2)
     const int cus = cus_of_device();
     const int wgs = max(1, min(2 * cus, quads * 5 / 8));
-    hipLaunchKernelGGL((ffn_gate_up_kernel<FUSED, NC>), dim3(unsigned(wgs)), dim3(256), gate_up_lds_bytes(a.K, NC), s,
-                       a, x32, xk);
+    hipLaunchKernelGGL((ffn_gate_up_kernel<FG, FUSED, NC>), dim3(unsigned(wgs)), dim3(256), gate_up_lds_bytes(a.K, NC),
+                       s, a, x32, xk);
     return hipGetLastError();
+}
+
+// the stage loads per lane a group needs (whole 16-B units, both spans): 6
+// for Q4_K at K = 2560, 7 for Q5_K (or Q4_K at K = 3072), 9 for Q5_K at 3072
+template <class FG>
+hipError_t launch_gate_up_f(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
+    const int need = (2 * kRP * (a.K / 256) * FG::BB + 1023) / 1024;
+    if (x32) {
+        if (need <= 6) return launch_gate_up_t<FG, true, 6>(a, x32, xk, s);
+        if (need <= 7) return launch_gate_up_t<FG, true, 7>(a, x32, xk, s);
+        return launch_gate_up_t<FG, true, 9>(a, x32, xk, s);
+    }
+    if (need <= 6) return launch_gate_up_t<FG, false, 6>(a, x32, xk, s);
+    if (need <= 7) return launch_gate_up_t<FG, false, 7>(a, x32, xk, s);
+    return launch_gate_up_t<FG, false, 9>(a, x32, xk, s);
 }
 
 }  // namespace
@@ -179,9 +195,9 @@ hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &x
 hipError_t launch_ffn_gate_up(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
     if (a.K % 256 || a.K > 3072 || a.F % 256 || a.F <= 0 || a.rb1 % 16 || !a.hx) return hipErrorNotSupported;
     if (!x32 && (!xk.qs || !xk.d || !xk.bs)) return hipErrorNotSupported;
-    const int need = (2 * kRP * (a.K / 256) * FmtQ4K4::BB + 1023) / 1024;  // 16-B loads per lane
-    if (x32) return need <= 6 ? launch_gate_up_t<true, 6>(a, x32, xk, s) : launch_gate_up_t<true, 7>(a, x32, xk, s);
-    return need <= 6 ? launch_gate_up_t<false, 6>(a, x32, xk, s) : launch_gate_up_t<false, 7>(a, x32, xk, s);
+    if (a.type == kQ4_K) return launch_gate_up_f<FmtQ4K4>(a, x32, xk, s);
+    if (a.type == kQ5_K) return launch_gate_up_f<FmtQ5K4>(a, x32, xk, s);
+    return hipErrorNotSupported;
 }
 
 }  // namespace qmm

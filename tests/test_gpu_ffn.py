@@ -133,8 +133,11 @@ def _same(a, b, h=True):
     (3072, 12288, 3072, TYPE_Q4_K, TYPE_Q6_K, False, False),  # 7 loads per group, 3 rounds of h
     (2560, 3072, 8192, TYPE_Q4_K, TYPE_Q6_K, True, True),     # 4 down rows per wave
     (2560, 4096, 1000, TYPE_Q4_K, TYPE_Q6_K, False, True),    # down too short for the persistent grid
-    (2560, 4096, 2560, qmm_hip.TYPE_Q5_K, TYPE_Q6_K, False, True),  # Q5_K gate/up
-], ids=["model", "q4k_down_prequant", "k3072_f12288", "f3072_h8192", "h1000_separate", "q5k_separate"])
+    (2560, 4096, 2560, qmm_hip.TYPE_Q5_K, TYPE_Q6_K, False, True),  # Q5_K gate/up, down too short
+    (2560, 9728, 2560, qmm_hip.TYPE_Q5_K, TYPE_Q6_K, False, True),  # Q5_K gate/up: 7 loads per group
+    (3072, 12288, 3072, qmm_hip.TYPE_Q5_K, TYPE_Q4_K, True, False),  # Q5_K at K = 3072: 9 loads per group
+], ids=["model", "q4k_down_prequant", "k3072_f12288", "f3072_h8192", "h1000_separate", "q5k_separate", "q5k_model",
+        "q5k_k3072"])
 def test_ffn_block_one_call(ctx, oracle, case):
     K, F, H, tg, td, pre, res = case
     say(f"ffn_block K={K} F={F} H={H} gate={tg} down={td} pre={pre} res={res}")
