@@ -1046,13 +1046,23 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     if (size_t((a.M + 15) & ~15) * size_t(a.K) >= (size_t(1) << 31)) return hipErrorInvalidValue;
     using G = typename Folded<F>::T;
     // 9..64 tokens over K > 3072, and Q8_0 at any K: 16-row x 16-token tiles,
-    // each chunk's 4 blocks split over the 4 waves, two workgroups per CU.
-    // The long K walk then runs in 4 (or more) times the workgroups of the
-    // 64-row tiles (measured, Q6_K 2560 x 9728 at M = 16 / 32 / 64: 13.2 /
-    // 18.7 / 27.0 us against 22.6 / 29.1 / 44.7; Q8_0 2560 x 2560: 10.5 /
-    // 12.1 / 17.0 against 15.7 / 20.8 / 22.7)
-    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>))
-        return launch_tile_t<TileCfg<G, 1, 1, 1, 1, 4, 16, 2, 100 * 1024>, G>(tasks, n, x, s);
+    // each chunk's 4 blocks split over the 4 waves, two workgroups per CU,
+    // where the configurations below would leave CUs idle: at 9..16 tokens
+    // always, at 17..32 where the 32 x 32 tiles number fewer than the CUs,
+    // at 33..64 where the 64 x 32 tiles number fewer than 5/8 of them.
+    // Measured: Q6_K 2560 x 9728 at M = 16 / 32 / 64 13.2 / 18.7 / 27.0 us
+    // against 22.6 / 29.1 / 44.7; Q8_0 2560 x 2560 10.5 / 12.1 / 17.0 against
+    // 15.7 / 20.8 / 22.7; on taller tensors (Q4_K / Q6_K 9728 x 4096, Q8_0
+    // 6144 x 2560) faster at M = 16 (12.0 / 14.9 / 13.3 against 13.6 / 16.5 /
+    // 15.1), slower at M = 64 (27.9 / 36.4 / 27.5 against 21.8 / 28.9 / 23.0)
+    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>)) {
+        int wg = 0;  // workgroups of the configuration below
+        for (int i = 0; i < n; ++i)
+            wg += a.M <= 32 ? (tasks[i].N + 31) / 32 : (tasks[i].N + 63) / 64 * ((a.M + 31) / 32);
+        const int cus = mfma_cu_count();
+        if (a.M <= 16 || (a.M <= 32 ? wg < cus : 8 * wg < 5 * cus))
+            return launch_tile_t<TileCfg<G, 1, 1, 1, 1, 4, 16, 2, 100 * 1024>, G>(tasks, n, x, s);
+    }
     // up to 32 tokens over K <= 3072: the resident-tile kernel
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
@@ -1086,9 +1096,6 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
         return launch_tile<G>(tasks, n, x, s);
     } else {
         if (a.M <= 32) return launch_tile_t<TileCfg<F, 1, 2, 2, 1, 2, 16, 2, 80 * 1024>, F>(tasks, n, x, s);
-        // 64 rows x 16 tokens: three token groups at 33..48 tokens (Q4_K
-        // 9728 x 2560 at M = 48: 12.5 us against 14.9 for 32-token tiles)
-        if (a.M <= 48) return launch_tile_t<TileCfg<F, 1, 1, 4, 1, 1, 16, 2, 64 * 1024>, F>(tasks, n, x, s);
         // 64 rows x 32 tokens: half the activation re-reads of 32-row tiles
         if (a.M <= 64) return launch_tile_t<TileCfg<F, 1, 2, 4, 1, 1, 16, 2, 53 * 1024>, F>(tasks, n, x, s);
         // folded formats: one row tile decoded per wave, shared by 4 (Q6_K: 3)
