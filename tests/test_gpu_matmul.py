@@ -125,6 +125,13 @@ def test_mfma_k_split_tiles(ctx, oracle, type_id, N, K, M):
     _run(ctx, oracle, type_id, N, K, M, seed=1700 + K + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 9728, 4096, 64), (TYPE_Q6_K, 8192, 4096, 24)])
+def test_mfma_wide_tiles_long_k(ctx, oracle, type_id, N, K, M):
+    """17..64 tokens over K > 3072 on tensors tall enough to fill the CUs
+    with 32 x 32 / 64 x 32 tiles (the K-split tiles are not used there)."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1800 + K + M)
+
+
 @pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 6144, 2560, 8), (TYPE_Q6_K, 13000, 1024, 3),
                                            (TYPE_Q5_K, 300, 3072, 16), (TYPE_Q4_K, 4111, 768, 11),
                                            (TYPE_Q6_K, 3000, 2560, 7)])
