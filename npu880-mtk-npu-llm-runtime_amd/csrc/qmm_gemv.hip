@@ -656,6 +656,21 @@ static int cu_count() {
     }
     return cus[dev];
 }
+// Workgroups of the persistent batch-1 grid for `quads` (four row groups
+// each, one per wave): where the quads are exactly 2, 3 or 4 per CU, a whole
+// number of workgroups per CU whose waves take a whole number of groups each
+// (measured, K = 2560: 8192 rows on one workgroup per CU, Q4_K / Q5_K / Q6_K
+// 4.65 / 5.40 / 6.80 -> 4.34 / 4.82 / 5.98 us; 12288 rows on three, 5.72 /
+// 6.85 / 8.63 -> 5.50 / 6.45 / 7.70; 16384 rows on two, Q4_K / Q6_K 6.79 /
+// 10.15 -> 6.19 / 9.19); otherwise 5/8 of a workgroup per quad, at most
+// three per CU (380 workgroups for the 608 quads of 9728 rows, 768 for the
+// LM head's 9496)
+static int persist_grid(int quads, int cus) {
+    if (quads == 2 * cus) return cus;
+    if (quads == 3 * cus) return 3 * cus;
+    if (quads == 4 * cus) return 2 * cus;
+    return min(3 * cus, quads * 5 / 8);
+}
 // Calls launch(std::integral_constant<int, NC>) with the fewest 16-B stage
 // loads per lane (NST - 2 .. NST) that cover a batch of `blocks` blocks from
 // any 16-B misalignment.
@@ -696,7 +711,7 @@ static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, cons
     const int nb = a.K / F::QK, cus = cu_count();
     const int wg0 = ((a.N + R - 1) / R + 3) / 4;
     if (a.N < (IsQ80<F>::v ? 8192 : 4096) || R * nb > (64 / F::G) * U || wg0 < 2 * cus) return hipErrorNotSupported;
-    const int wgs = min(3 * cus, wg0 * 5 / 8);
+    const int wgs = persist_grid(wg0, cus);
     if (wgs > kMaxArgmaxParts || (pre.part && pre.nparts > 1024)) return hipErrorNotSupported;
     *nparts = wgs;
     return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
@@ -726,14 +741,12 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     }
     const size_t lds = gemv_lds_bytes_t<F, R, U>(tasks[0].K);
     const dim3 grid(unsigned(g.wg0[n]));
-    // one task of at least two workgroups' rows per CU: a persistent grid of
-    // 5/8 of a workgroup per row group, at most 3 per CU (measured: 380
-    // workgroups for 608 groups, 768 for the 9496 of the LM head)
+    // one task of at least two workgroups' rows per CU: the persistent grid
     if constexpr (F::kStaged) {
         const int nb = tasks[0].K / F::QK;
         const int cus = cu_count();
         if (n == 1 && R * nb <= (64 / F::G) * U && g.wg0[1] >= 2 * cus) {
-            const int wgs = min(3 * cus, g.wg0[1] * 5 / 8);
+            const int wgs = persist_grid(g.wg0[1], cus);
             return launch_gemv_persist_t<F, R, U>(tasks[0], x32, xk, x0, lds, wgs, s);
         }
     }
@@ -823,7 +836,7 @@ static hipError_t launch_gemv_x16_t(const MatArgs &a, const uint16_t *x16, hipSt
     const int cus = cu_count();
     if (a.K % 256 || a.K > 4096 * kX16Rounds || R * nb > (64 / F::G) * U || wg < 2 * cus) return hipErrorNotSupported;
     if (!launch) return hipSuccess;
-    const int wgs = min(3 * cus, wg * 5 / 8);
+    const int wgs = persist_grid(wg, cus);
     const float *xp = reinterpret_cast<const float *>(x16);
     switch (R) {
         case kGemvR: return launch_gemv_persist_t<F, kGemvR, U, false, true>(a, xp, {}, {}, gemv_lds_bytes_t<F, kGemvR, U>(a.K), wgs, s);

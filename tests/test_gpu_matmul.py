@@ -87,6 +87,13 @@ def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
     _run(ctx, oracle, type_id, N, K, 1, seed=N + type_id)
 
 
+@pytest.mark.parametrize("type_id,N", [(TYPE_Q5_K, 8192), (TYPE_Q6_K, 12288), (TYPE_Q4_K, 16384)])
+def test_gemv_whole_groups_per_wave(ctx, oracle, type_id, N):
+    """Batch 1 on 2, 3 or 4 quads of row groups per CU: the persistent grid
+    of one, three or two workgroups per CU, every wave taking whole groups."""
+    _run(ctx, oracle, type_id, N, 2560, 1, seed=N + 3 * type_id)
+
+
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K])
 def test_gemv_residual(ctx, oracle, type_id):
     _run(ctx, oracle, type_id, 300, 2560, 1, seed=5, residual=True)
