@@ -268,9 +268,10 @@ int run_tasks(qmm_context *ctx, const float *x32, const void *q8k, const void *q
 
 // Checks of a prequantized input for a validated task list.
 // Sections of the dispatcher's own Q8_K buffer that no kernel of an M >= 2
-// call reads: bsum32 (read only by the batch-1 GEMV on prequantized input),
-// the row-major codes above 64 tokens (the tile and slab kernels read the
-// tiles section), the fp16 values without an F32 / F16 task.
+// call reads: bsum32 (read only by the batch-1 GEMV on prequantized input;
+// its 2..4-token form sums the codes itself), the row-major codes above 64
+// tokens (the tile and slab kernels read the tiles section), the fp16 values
+// without an F32 / F16 task.
 unsigned q8k_skip(int M, const qmm_matrix_task *tasks, int n_tasks) {
     unsigned skip = qmm::kSkipBs;
     if (M > 64) skip |= qmm::kSkipQs;

@@ -240,6 +240,10 @@ hipError_t launch_ffn_gate_up(const FfnArgs &a, const float *x32, const Q8KView 
 // Q6_K on the persistent grid, else hipErrorNotSupported (nothing
 // launched). launch = false: only whether it applies.
 hipError_t launch_gemv_x16(uint32_t type, const MatArgs &a, const uint16_t *x16, hipStream_t s, bool launch = true);
+// 2 <= M <= 4 tokens of one Q4_K / Q5_K / Q6_K task on a prequantized input
+// (its codes, scales and 32-code sums) in the batch-1 GEMV's shape, else
+// hipErrorNotSupported (nothing launched)
+hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s);
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 

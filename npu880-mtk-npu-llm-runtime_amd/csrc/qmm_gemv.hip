@@ -633,6 +633,118 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
     }
 }
 
+// ------------------------------------------- 2..4 tokens, batch-1 shape
+// The persistent kernel's structure for 2 <= M <= MT <= 4 tokens on a
+// prequantized input (the codes and scales of the Q8_K buffer; the 32-code
+// sums are formed from the codes, so the buffer's bsum32 section is not
+// read): every token's row is filled into LDS once per workgroup, and each
+// wave's row groups are
+// staged and unpacked once for all tokens; per token the lane groups form
+// the block terms (the batch-1 expression) and sum them in block order
+// along each row's lane groups in registers. Each output equals the batch-1
+// GEMV of its token, bit for bit. 4 lanes per block, R = 1, 2 or 4.
+template <class F, int R, int U, int NC, int MT>
+__global__ __launch_bounds__(256) void gemv_mt_kernel(MatArgs a, Q8KView prek) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int G = F::G, SLOTS = 64 / G, GPR = SLOTS / R;
+    static_assert(G == 4 && SLOTS % R == 0 && F::kStaged, "4 lanes per block, whole rows per DPP rows");
+    if (scan_stopped(a.scan)) return;
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    const int g = lane / G, k = lane % G;
+    const int K = a.K, nb = K / F::QK, M = a.M;
+    const int ngroups = (a.N + R - 1) / R;
+    const size_t act_bytes = gemv_act_lds_bytes(false, K);
+    uint8_t *stage = lds + MT * act_bytes + size_t(wid) * NC * 1024;
+
+    uint4 st[NC];
+    auto stage_load = [&](int gr) __attribute__((always_inline)) {
+        const int rows = max(0, min(R, a.N - gr * R));
+        const uint8_t *span = a.w + size_t(rows > 0 ? gr * R : 0) * a.row_bytes;
+        const int mis = int(reinterpret_cast<uintptr_t>(span) & 15);
+        const int bytes = (mis + max(rows * nb, 1) * F::BB + 15) & ~15;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(span - mis), short(0), bytes, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+            st[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t(16 * (64 * j + lane)), 0, kNonTemporal));
+    };
+
+    // 1. the tokens' rows requested, then the first group's bytes; the rows into LDS
+    int gw = int(blockIdx.x) * 4 + wid;
+    const int stride = int(gridDim.x) * 4;
+    CPre cp[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        if (t < M)
+            cpre_load<false, false>(prek.qs + size_t(t) * K, prek.d + size_t(t) * nb, nullptr, K, cp[t]);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_load(min(gw, ngroups - 1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        if (t < M)
+            cpre_fill<false, std::is_same_v<F, FmtQ6K4>, true>(cp[t], prek.qs + size_t(t) * K, prek.d + size_t(t) * nb,
+                                                                nullptr, K, gemv_act_view(lds + t * act_bytes, false, K));
+    lds_barrier();
+
+    // 2. groups (as the batch-1 persistent kernel's register row sums)
+    const int bpg = (nb + GPR - 1) / GPR;
+    const int r = g / GPR, q = g % GPR;
+    for (; gw < ngroups; gw += stride) {
+        const int row0 = gw * R;
+        const int nrows = min(R, a.N - row0);
+        const int mis = int(reinterpret_cast<uintptr_t>(a.w + size_t(row0) * a.row_bytes) & 15);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int j = 0; j < NC; ++j) *reinterpret_cast<uint4 *>(stage + 16 * (64 * j + lane)) = st[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        if (gw + stride < ngroups) stage_load(gw + stride);
+        typename F::Raw rs[U];
+        bool own[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int b = q * bpg + u;
+            own[u] = u < bpg && b < nb && r < nrows;
+            rs[u] = F::load(stage + mis + (own[u] ? r * nb + b : 0) * F::BB, k);
+        }
+        const bool wr = q == GPR - 1 && k == 0 && r < nrows;
+        const int row = row0 + r;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (t >= M) break;  // the same in every lane
+            const LdsAct act = gemv_act_view(lds + t * act_bytes, false, K);
+            float c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int b = q * bpg + u;
+                const float v = F::compute(rs[u], F::load_act(act, own[u] ? b : 0, k), k);
+                c[u] = own[u] ? v : 0.0f;
+            }
+            float acc = 0.0f;
+#pragma unroll
+            for (int h = 0; h < GPR; ++h) {  // each group takes its left neighbour's sum; q = 0 starts at +0.0
+                float s = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x114,
+                                                                                0xF, 0xF, true));
+                if constexpr (GPR > 4) {
+                    const float up = __builtin_bit_cast(
+                        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc), 0x142, 0xF, 0xF, true));
+                    s = q == 0 ? 0.0f : (q & 3) == 0 ? up : s;
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) s = s + c[u];
+                acc = s;
+            }
+            if (wr) {
+                if (a.res) acc = acc + a.res[size_t(t) * a.ldr + row];
+                a.y[size_t(t) * a.ldy + row] = acc;
+            }
+        }
+    }
+}
+
+
 size_t gemv_lds_bytes(uint32_t type, int K) {
     switch (type) {
         case kQ4_K: return gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K);
@@ -865,6 +977,47 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
         case kF32:
         case kF16: return launch_gemv_mixed(tasks, n, x32, xk, x0, s);
         default: return hipErrorInvalidValue;
+    }
+}
+
+template <class F, int R, int U, int MT>
+static hipError_t launch_gemv_mt_r(const MatArgs &a, const Q8KView &xk, hipStream_t s) {
+    const int nb = a.K / F::QK;
+    if (R * nb > (64 / F::G) * U) return hipErrorNotSupported;
+    const int cus = cu_count();
+    const int quads = ((a.N + R - 1) / R + 3) / 4;
+    const int wgs = quads >= 2 * cus ? persist_grid(quads, cus) : quads;
+    const size_t lds = MT * gemv_act_lds_bytes(false, a.K) + size_t(4) * stage_chunks<F, U>() * 1024;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
+    return with_stage_chunks<F, U>(R * nb, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        hipLaunchKernelGGL((gemv_mt_kernel<F, R, U, NC, MT>), dim3(unsigned(wgs)), dim3(256), lds, s, a, xk);
+        return hipGetLastError();
+    });
+}
+
+template <class F, int U>
+static hipError_t launch_gemv_mt_t(const MatArgs &a, const Q8KView &xk, hipStream_t s) {
+    // rows per wave as for a batch-1 launch of the same tensor
+    const int R = a.N >= 4096 ? kGemvR : a.K <= 4096 ? 2 : 1;
+    if (a.M <= 2) {
+        if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 2>(a, xk, s);
+        if (R == 2) return launch_gemv_mt_r<F, 2, U, 2>(a, xk, s);
+        return launch_gemv_mt_r<F, 1, U, 2>(a, xk, s);
+    }
+    if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 4>(a, xk, s);
+    if (R == 2) return launch_gemv_mt_r<F, 2, U, 4>(a, xk, s);
+    return launch_gemv_mt_r<F, 1, U, 4>(a, xk, s);
+}
+
+hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s) {
+    const MatArgs &a = tasks[0];
+    if (n != 1 || a.M < 2 || a.M > 4 || a.K % 256 || a.K > 16384 || !xk.qs || !xk.d) return hipErrorNotSupported;
+    switch (type) {
+        case kQ4_K: return launch_gemv_mt_t<FmtQ4K4, 3>(a, xk, s);
+        case kQ5_K: return launch_gemv_mt_t<FmtQ5K4, 3>(a, xk, s);
+        case kQ6_K: return launch_gemv_mt_t<FmtQ6K4, 3>(a, xk, s);
+        default: return hipErrorNotSupported;
     }
 }
 

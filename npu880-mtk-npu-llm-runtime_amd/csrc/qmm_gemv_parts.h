@@ -359,7 +359,8 @@ __device__ inline void x16_fill(const uint4 (&q)[kX16Rounds][2], int K, const Ld
 // Prequantized row: 16-B code chunks, scales and bsum32 per thread.
 struct CPre { uint4 q[4]; int32_t bs[2]; float d[2]; };
 
-template <bool Q80>
+// BS = false: the 32-code sums are not read (bs may be null)
+template <bool Q80, bool BS = true>
 __device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t *bs, int K, CPre &p) {
     const int t = threadIdx.x, t0 = 64 * int(threadIdx.x >> 6);
     const int nq = K >> 4, nd = Q80 ? (K >> 5) : (K >> 8);
@@ -370,7 +371,7 @@ __device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t
         if (t0 + 256 * i < nq) p.q[i] = ld16(qs + 16 * min(t + 256 * i, nq - 1));
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        if constexpr (!Q80)
+        if constexpr (!Q80 && BS)
             if (t0 + 256 * i < (K >> 5)) p.bs[i] = bs[min(t + 256 * i, (K >> 5) - 1)];
         if (t0 + 256 * i < nd) p.d[i] = d[min(t + 256 * i, nd - 1)];
     }
@@ -379,7 +380,9 @@ __device__ inline void cpre_load(const int8_t *qs, const float *d, const int32_t
 __device__ inline int sum16_codes(uint4 q) {
     return sdot4(int(q.w), 0x01010101, sdot4(int(q.z), 0x01010101, sdot4(int(q.y), 0x01010101, sdot4(int(q.x), 0x01010101, 0))));
 }
-template <bool Q80, bool BS16 = false>
+// BSC: the 32-code sums formed here from the codes (exact integers, the
+// quantizer's bsum32) instead of read from the buffer; K <= 16384
+template <bool Q80, bool BS16 = false, bool BSC = false>
 __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d, const int32_t *bs,
                                  int K, const LdsAct &a) {
     const int t = threadIdx.x;
@@ -389,12 +392,19 @@ __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d
     int32_t *lb = const_cast<int32_t *>(a.bs);
     int32_t *l16 = const_cast<int32_t *>(a.bs16);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (t + 256 * i < nq) {
-            const int g = t + 256 * i;
+    for (int i = 0; i < 4; ++i) {
+        const int g = t + 256 * i;
+        if (g < nq) {
             *reinterpret_cast<uint4 *>(lq + lds_pad(16 * g)) = p.q[i];
             if constexpr (BS16) l16[bs16_pos(g >> 4, 16 * (g & 15))] = sum16_codes(p.q[i]);
         }
+        if constexpr (BSC && !Q80) {
+            // codes 16 g .. 16 g + 15 here and 16 (g ^ 1) .. in the lane next door
+            const int s16 = g < nq ? sum16_codes(p.q[i]) : 0;
+            const int s32 = s16 + dpp_xor1(s16);
+            if (g < nq && !(g & 1)) lb[g >> 1] = s32;
+        }
+    }
     for (int i = t + 1024; i < nq; i += 256) {
         const uint4 q = ld16(qs + 16 * i);
         *reinterpret_cast<uint4 *>(lq + lds_pad(16 * i)) = q;
@@ -402,10 +412,12 @@ __device__ inline void cpre_fill(const CPre &p, const int8_t *qs, const float *d
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        if (t + 256 * i < nbs) lb[t + 256 * i] = p.bs[i];
+        if constexpr (!BSC)
+            if (t + 256 * i < nbs) lb[t + 256 * i] = p.bs[i];
         if (t + 256 * i < nd) ld[t + 256 * i] = p.d[i];
     }
-    for (int i = t + 512; i < nbs; i += 256) lb[i] = bs[i];
+    if constexpr (!BSC)
+        for (int i = t + 512; i < nbs; i += 256) lb[i] = bs[i];
     for (int i = t + 512; i < nd; i += 256) ld[i] = d[i];
 }
 

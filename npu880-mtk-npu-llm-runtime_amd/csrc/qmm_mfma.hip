@@ -1185,6 +1185,15 @@ int mfma_cu_count() {
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
+    // one k-quant task at 2 tokens, or at 3..4 on a tensor tall enough that
+    // the MFMA kernels need several rounds of workgroups: the batch-1 GEMV's
+    // shape (measured, M = 2: Q4_K 9728 x 2560 7.75 -> 6.16 us, Q6_K 2560 x
+    // 9728 13.57 -> 9.00, Q6_K 151936 x 2560 111 -> 62; M = 4: Q6_K 151936 x
+    // 2560 111 -> 93, while Q4_K 9728 x 2560 went 7.73 -> 8.58)
+    if (n == 1 && (tasks[0].M == 2 || (tasks[0].M <= 4 && tasks[0].N >= 96 * mfma_cu_count()))) {
+        const hipError_t e = launch_gemv_mt(type, tasks, n, xk, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     switch (type) {
         case kQ4_K: return launch_tile<MQ4K>(tasks, n, xk, s);
         case kQ5_K: return launch_tile<MQ5K>(tasks, n, xk, s);

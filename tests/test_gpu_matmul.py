@@ -87,6 +87,16 @@ def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
     _run(ctx, oracle, type_id, N, K, 1, seed=N + type_id)
 
 
+@pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 2560, 2, False), (TYPE_Q5_K, 300, 4096, 2, True),
+                                                    (TYPE_Q6_K, 2560, 9728, 2, True), (TYPE_Q5_K, 4099, 3072, 2, False),
+                                                    (TYPE_Q6_K, 30000, 2560, 3, True), (TYPE_Q4_K, 25000, 1024, 4, False)])
+def test_gemv_two_to_four_tokens(ctx, oracle, type_id, N, K, M, residual):
+    """2 tokens, and 3..4 on tensors past 96 rows per CU: the batch-1 GEMV's
+    shape with every token's row in LDS (4-, 2- and 1-row groups, ragged
+    last group, residual)."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1900 + N + M, residual=residual)
+
+
 @pytest.mark.parametrize("type_id,N", [(TYPE_Q5_K, 8192), (TYPE_Q6_K, 12288), (TYPE_Q4_K, 16384)])
 def test_gemv_whole_groups_per_wave(ctx, oracle, type_id, N):
     """Batch 1 on 2, 3 or 4 quads of row groups per CU: the persistent grid
