@@ -224,7 +224,10 @@ typedef struct {
  * margin ends the active batch at p + 1 (E:11203-11209: later positions are
  * no longer updated), and at a checkpoint the scan stops when every active
  * position's best reaches the chunk's threshold. A chunk after the stop
- * reads no weights. scan_state (device int32[4]) receives: chunks read,
+ * reads no weights. Chunks after which nothing is decided (no checkpoint,
+ * no drafts to prune) share one launch with the chunks that follow them, up
+ * to the next deciding chunk: the same results, fewer launches.
+ * scan_state (device int32[4]) receives: chunks read,
  * active positions, 1 if the scan stopped early, 0. The script-specific
  * extended rows (E:11194-11240) are the caller's: qmm_eval_rows_argmax. */
 int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, int K,

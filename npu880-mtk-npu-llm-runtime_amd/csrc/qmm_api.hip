@@ -343,6 +343,7 @@ struct PendingStep {
     bool checkpoint = false;
     int c = 0;
     void *bufs[2] = {nullptr, nullptr};
+    int launches = 0;  // the scan's launches so far: consecutive ones alternate buffers
 };
 
 int launch_pending(qmm_context *ctx, PendingStep &pend, float *best_val, uint32_t *best_id, const qmm::ScanStep &st,
@@ -377,7 +378,7 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
     act_views(q8k, q80, M, K, xk, x0);
     const bool round16 = ids == nullptr;  // chunk scans compare fp16 logits (E:11175), indexed rows fp32
     if (M == 1 && step && pend) {  // a scan chunk: its step waits for the next chunk's launch
-        void *mine = pend->bufs[step->c & 1];
+        void *mine = pend->bufs[pend->launches++ & 1];
         qmm::PrevStep pre{};
         if (pend->on)
             pre = qmm::PrevStep{pend->part, pend->nparts, pend->row_base, pend->thresh, pend->checkpoint ? 1 : 0,
@@ -865,9 +866,28 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
         return fail(ctx, QMM_EINVAL, "bad LM-head scan parameters");
     if (!aligned(best_val, 4) || !aligned(best_id, 4) || !aligned(scan_state, 4))
         return fail(ctx, QMM_EALIGN, "best_val/best_id/scan_state must be 4-B aligned");
-    // validate every launch's task before the first launch
-    const int chunk = std::min(params->chunk_rows, vocab_rows);
+    // Chunks share a launch up to the next chunk after which something is
+    // decided: a checkpoint (E:11248-11256) or, with drafts, the pruning
+    // (E:11203-11209, after every chunk). In between nothing changes the
+    // scan's course, and the strict running update over the merged rows
+    // (the first row holding the largest value, if it beats the best) is
+    // the chunk-by-chunk updates' result.
     const int nchunks = (vocab_rows + params->chunk_rows - 1) / params->chunk_rows;
+    const bool prunes = draft_ids && M >= 2;
+    auto decides = [&](int c) {
+        return prunes || c == nchunks - 1 || (params->n_thresholds > 0 && c >= params->first_checkpoint);
+    };
+    std::vector<std::pair<int, int>> groups;  // [first chunk, last chunk] of each launch
+    int chunk = 0;                            // rows of the largest launch
+    for (int c0 = 0; c0 < nchunks;) {
+        int c1 = c0;
+        while (!decides(c1)) ++c1;
+        groups.emplace_back(c0, c1);
+        const int64_t end = std::min<int64_t>(int64_t(c1 + 1) * params->chunk_rows, vocab_rows);
+        chunk = std::max(chunk, int(end - int64_t(c0) * params->chunk_rows));
+        c0 = c1 + 1;
+    }
+    // validate every launch's task before the first launch
     qmm_matrix_task tc, tp, td;
     int rc = lm_task(ctx, q8k, q80, M, K, w_lm, type, chunk, nullptr, tc);
     if (!rc && n_pre > 0) rc = lm_task(ctx, q8k, q80, M, K, w_lm, type, n_pre, nullptr, tp);
@@ -903,16 +923,18 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
         e = qmm::launch_scan_cand(M, cdot, draft_ids, uint32_t(vocab_rows), best_val, best_id, cand, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "candidate launch");
     }
-    // the chunks (E:11158-11257): each does nothing once the scan has stopped
+    // the chunks (E:11158-11257), a launch per group: each does nothing once
+    // the scan has stopped
     PendingStep pend;
     pend.bufs[0] = work + lm_scratch(M, chunk, rb, false, false).total();
     pend.bufs[1] = static_cast<uint8_t *>(pend.bufs[0]) + part_b;
     qmm::ScanStep last{};
-    for (int c = 0; c < nchunks; ++c) {
-        const int r0 = c * params->chunk_rows;
+    for (const auto &gr : groups) {
+        const int c = gr.second;  // the group's last chunk: its threshold and checkpoint
+        const int r0 = gr.first * params->chunk_rows;
         qmm_matrix_task t = tc;
         t.w_base = wb + size_t(r0) * rb;
-        t.rows = std::min(params->chunk_rows, vocab_rows - r0);
+        t.rows = int(std::min<int64_t>(int64_t(c + 1) * params->chunk_rows, vocab_rows) - r0);
         t.dst_stride = size_t(t.rows);
         qmm::ScanStep step;
         step.cand = cand;
