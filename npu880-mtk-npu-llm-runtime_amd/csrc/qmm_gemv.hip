@@ -389,9 +389,12 @@ __global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const flo
 // computes the current one (one batch per group: R nb <= SLOTS U). After the
 // fill the waves never synchronize with each other.
 // X16: x32 holds an fp16 row (reinterpreted), quantized in the kernel.
+// The body of one workgroup of the persistent grid: workgroup wgi of the
+// nwg that share the task's row groups.
 template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false>
-__global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const float *__restrict__ x32,
-                                                           Q8KView prek, Q80View pre0, AmaxOut am) {
+__device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a, const float *__restrict__ x32,
+                                                                      Q8KView prek, Q80View pre0, AmaxOut am,
+                                                                      int wgi, int nwg) {
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
@@ -433,8 +436,8 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
             st[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t(16 * (64 * j + lane)), 0, kNonTemporal));
     };
 
-    int gw = int(blockIdx.x) * 4 + wid;
-    const int stride = int(gridDim.x) * 4;
+    int gw = wgi * 4 + wid;
+    const int stride = nwg * 4;
     // 0. a scan's step after the previous chunk (the partials are requested
     // ahead of the activations; the decision precedes every weight request,
     // so a chunk the step stops reads no weights)
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
                 }
                 const int stop = q.checkpoint && (act == 0 || !(bv < q.thresh));
                 pstop = stop;
-                if (blockIdx.x == 0) {
+                if (wgi == 0) {
                     q.best_val[0] = bv;
                     q.best_id[0] = bi;
                     q.st[kScanChunks] = q.c + 1;
@@ -628,8 +631,43 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
         if (threadIdx.x == 0) {
             Best r = wsb[0];
             for (int w = 1; w < 4; ++w) r = better(r, wsb[w]);
-            static_cast<Best *>(am.part)[blockIdx.x] = r;
+            static_cast<Best *>(am.part)[wgi] = r;
         }
+    }
+}
+
+template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false>
+__global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const float *__restrict__ x32,
+                                                           Q8KView prek, Q80View pre0, AmaxOut am) {
+    gemv_persist_wg<F, R, U, FUSED, NC, AMAX, X16>(a, x32, prek, pre0, am, int(blockIdx.x), int(gridDim.x));
+}
+
+// ------------------------------ several formats on one persistent grid
+// A batch-1 task group of several k-quant formats (with F32 / F16 tasks
+// beside them) in one launch, the k-quant tasks on the persistent grid:
+// task t owns the workgroups grp.wg0[t] .. grp.wg0[t + 1] - 1, which share
+// its row groups exactly as the one-task persistent kernel's grid does
+// (the slices are in proportion to the tasks' row groups); every workgroup
+// fills its own activations. F32 / F16 tasks keep one row per wave. The
+// stage loads per lane are the format's largest count less D (the launcher
+// takes the largest D that still covers every task's row groups). Each
+// output equals the one-task launch's, bit for bit.
+template <bool FUSED, int D>
+__global__ __launch_bounds__(256) void gemv_mixed_persist_kernel(MatGroup grp, const float *__restrict__ x32,
+                                                                 Q8KView prek, Q80View pre0) {
+    int bx = 0;
+    const int t = group_task(grp, int(blockIdx.x), bx);
+    const MatArgs a = grp.t[t];
+    const int nwg = grp.wg0[t + 1] - grp.wg0[t];
+    constexpr int N4 = stage_chunks<FmtQ4K4, 3>() - D, N5 = stage_chunks<FmtQ5K4, 3>() - D;
+    constexpr int N6 = stage_chunks<FmtQ6K4, 3>() - D;
+    switch (a.type) {
+        case kQ4_K: gemv_persist_wg<FmtQ4K4, kGemvR, 3, FUSED, N4, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
+        case kQ5_K: gemv_persist_wg<FmtQ5K4, kGemvR, 3, FUSED, N5, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
+        case kQ6_K: gemv_persist_wg<FmtQ6K4, kGemvR, 3, FUSED, N6, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
+        case kF32: gemv_float_wg<false, 1, FUSED>(a, bx, x32, prek.h); break;
+        case kF16: gemv_float_wg<true, 1, FUSED>(a, bx, x32, prek.h); break;
+        default: break;
     }
 }
 
@@ -922,9 +960,85 @@ static hipError_t launch_gemv_mixed_r(const MatArgs *tasks, int n, const float *
     return hipGetLastError();
 }
 
+// A mixed group on the persistent grid (gemv_mixed_persist_kernel): its
+// k-quant tasks (Q4_K / Q5_K / Q6_K, R = kGemvR rows per group within one
+// batch) hold at least two workgroups' row groups per CU in all; the grid is
+// the one-task kernel's for that many row groups, dealt to the k-quant tasks
+// in proportion to their row groups. hipErrorNotSupported (nothing launched)
+// where that does not apply.
+static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
+                                            const Q80View &x0, hipStream_t s) {
+    const int K = tasks[0].K, nb = K / 256, cus = cu_count();
+    if (K % 256 || kGemvR * nb > 16 * 3) return hipErrorNotSupported;
+    int quads[kMaxGroup] = {}, total = 0, d = 2, fw = 0;
+    size_t lds = 0;
+    for (int i = 0; i < n; ++i) {
+        const uint32_t ty = tasks[i].type;
+        if (ty == kF32 || ty == kF16) {
+            fw += (tasks[i].N + 3) / 4;  // one row per wave
+            continue;
+        }
+        int bb, nst;
+        switch (ty) {
+            case kQ4_K: bb = FmtQ4K4::BB; nst = stage_chunks<FmtQ4K4, 3>(); lds = max(lds, gemv_lds_bytes_t<FmtQ4K4, kGemvR, 3>(K)); break;
+            case kQ5_K: bb = FmtQ5K4::BB; nst = stage_chunks<FmtQ5K4, 3>(); lds = max(lds, gemv_lds_bytes_t<FmtQ5K4, kGemvR, 3>(K)); break;
+            case kQ6_K: bb = FmtQ6K4::BB; nst = stage_chunks<FmtQ6K4, 3>(); lds = max(lds, gemv_lds_bytes_t<FmtQ6K4, kGemvR, 3>(K)); break;
+            default: return hipErrorNotSupported;
+        }
+        // 16-B stage loads per lane a group needs from any misalignment (as with_stage_chunks)
+        const int need = ((15 + kGemvR * nb * bb + 15) / 16 + 63) / 64;
+        d = min(d, nst - need);
+        quads[i] = ((tasks[i].N + kGemvR - 1) / kGemvR + 3) / 4;
+        total += quads[i];
+    }
+    if (total < 2 * cus || d < 0) return hipErrorNotSupported;
+    // the merged bodies hold more registers than any one-format kernel: the
+    // grid is the one-task grid, but never more than the workgroups that are
+    // resident at once
+    const void *fn = nullptr;
+    if (d >= 2) fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 2>)
+                         : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 2>);
+    else if (d == 1) fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 1>)
+                              : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 1>);
+    else fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 0>)
+                  : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 0>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess || per_cu < 1) {
+        (void)hipGetLastError();
+        return hipErrorNotSupported;
+    }
+    const int G = min(persist_grid(total, cus), max(cus, per_cu * cus - fw));
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    int cum = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        int w;
+        if (quads[i] == 0) {
+            w = (tasks[i].N + 3) / 4;
+        } else {
+            w = max(1, int(int64_t(G) * (cum + quads[i]) / total - int64_t(G) * cum / total));
+            cum += quads[i];
+        }
+        g.wg0[i + 1] = g.wg0[i] + w;
+    }
+    const dim3 grid(unsigned(g.wg0[n]));
+    auto go = [&](auto dd) {
+        constexpr int DD = decltype(dd)::value;
+        if (x32) hipLaunchKernelGGL((gemv_mixed_persist_kernel<true, DD>), grid, dim3(256), lds, s, g, x32, xk, x0);
+        else hipLaunchKernelGGL((gemv_mixed_persist_kernel<false, DD>), grid, dim3(256), lds, s, g, x32, xk, x0);
+        return hipGetLastError();
+    };
+    if (d >= 2) return go(std::integral_constant<int, 2>{});
+    if (d == 1) return go(std::integral_constant<int, 1>{});
+    return go(std::integral_constant<int, 0>{});
+}
+
 hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk, const Q80View &x0,
                              hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
+    if (const hipError_t e = launch_gemv_mixed_persist(tasks, n, x32, xk, x0, s); e != hipErrorNotSupported) return e;
     int64_t rows = 0;
     for (int i = 0; i < n; ++i) rows += tasks[i].N;
     // rows per wave as for one k-quant launch of the group's size

@@ -131,3 +131,19 @@ def test_mixed_group_large_k(ctx, oracle):
     specs = [(TYPE_Q6_K, 40), (TYPE_Q4_K, 24), (TYPE_F32, 8)]
     for M in (1, 5):
         _check(_run_group(ctx, oracle, specs, M, 9728, seed=350 + M), f"mixed K=9728 M={M}")
+
+
+@pytest.mark.parametrize("specs,K,pre", [
+    ([(TYPE_Q5_K, 8192), (TYPE_Q4_K, 4096), (TYPE_F32, 32), (TYPE_F32, 32)], 2560, True),
+    ([(TYPE_Q5_K, 8192), (TYPE_F32, 32)], 2560, False),
+    ([(TYPE_F16, 40), (TYPE_Q4_K, 8192), (TYPE_Q5_K, 2048), (TYPE_Q6_K, 1000)], 3072, False),
+    ([(TYPE_Q6_K, 6144), (TYPE_Q4_K, 2048), (TYPE_Q5_K, 8)], 2560, True),
+])
+def test_mixed_groups_persistent_grid(ctx, oracle, specs, K, pre):
+    """Batch-1 groups with enough k-quant row groups for the persistent grid
+    (every k-quant task on its own slice of it, F32 / F16 rows one per wave):
+    each format's stage-load count, fused and prequantized input, ragged
+    row counts, a task smaller than one workgroup's row groups."""
+    say(f"mixed persistent {[(qmm_hip.TYPE_NAMES[t], n) for t, n in specs]} K={K} prequantized={pre}")
+    _check(_run_group(ctx, oracle, specs, 1, K, seed=360 + K + len(specs), prequantized=pre),
+           f"mixed persistent K={K}")
