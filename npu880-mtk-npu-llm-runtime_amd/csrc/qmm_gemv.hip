@@ -914,6 +914,9 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
     });
 }
 
+static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
+                                            const Q80View &x0, hipStream_t s);
+
 // Rows per wave by the launch's total rows and K (measured per shape): the
 // k-quants take 4 from 4096 rows, else 2 up to K = 4096, else 1 (the 2560-row
 // K = 9728 down projection: 12.4 -> 8.9 us with 1); Q8_0 (34-B blocks, 5
@@ -921,6 +924,12 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
 template <class F, int U>
 static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                                    const Q80View &x0, hipStream_t s) {
+    // several k-quant tasks of one format: each on its own slice of one
+    // persistent grid, where their row groups are enough for it
+    if constexpr (!IsQ80<F>::v)
+        if (n > 1)
+            if (const hipError_t e = launch_gemv_mixed_persist(tasks, n, x32, xk, x0, s); e != hipErrorNotSupported)
+                return e;
     int64_t rows = 0;
     for (int i = 0; i < n; ++i) rows += tasks[i].N;
     const bool q80 = IsQ80<F>::v;

@@ -147,3 +147,15 @@ def test_mixed_groups_persistent_grid(ctx, oracle, specs, K, pre):
     say(f"mixed persistent {[(qmm_hip.TYPE_NAMES[t], n) for t, n in specs]} K={K} prequantized={pre}")
     _check(_run_group(ctx, oracle, specs, 1, K, seed=360 + K + len(specs), prequantized=pre),
            f"mixed persistent K={K}")
+
+
+@pytest.mark.parametrize("specs,pre", [
+    ([(TYPE_Q4_K, 9728), (TYPE_Q4_K, 9728)], False),
+    ([(TYPE_Q6_K, 4096), (TYPE_Q6_K, 4096), (TYPE_Q6_K, 1000)], True),
+    ([(TYPE_Q5_K, 6144), (TYPE_Q5_K, 1024), (TYPE_Q5_K, 1024)], False),
+])
+def test_one_format_groups_persistent_grid(ctx, oracle, specs, pre):
+    """Batch-1 groups of one k-quant format ({gate, up}, {q, k, v}) on slices
+    of one persistent grid, bit-exact against the oracle."""
+    say(f"one-format persistent {[(qmm_hip.TYPE_NAMES[t], n) for t, n in specs]} prequantized={pre}")
+    _check(_run_group(ctx, oracle, specs, 1, 2560, seed=380 + len(specs), prequantized=pre), "one-format persistent")
