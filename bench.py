@@ -471,7 +471,9 @@ def bench_ffn(ctx, args):
 
 def bench_rmsnorm_gemv(ctx, args):
     """RMSNorm -> Q8_K (qmm_rmsnorm_q8k) then the Q4_K 9728 x 2560 GEMV on the
-    prequantized row, against the RMSNorm alone (M = 1, K = 2560)."""
+    prequantized row, against the RMSNorm alone (M = 1, K = 2560), and the
+    same pair as one call (qmm_gemm_multi_dispatch_rmsnorm: the norm inside
+    the GEMV's activation fill, one launch)."""
     N, K = synth.GEMV_Q4K["N"], synth.GEMV_Q4K["K"]
     w = Replicated(ctx, synth.TYPE_Q4_K, N, K, 0, 0)
     x = ctx.upload(synth.activations(1, K, seed=1))
@@ -486,10 +488,13 @@ def bench_rmsnorm_gemv(ctx, args):
         ctx.gemm_multi_dispatch_prequantized(q, None, 1, K, [w.task(i, y)])
 
     ms, _ = timed(ctx, step, steps, 10, w.R)
+    ms_fused, _ = timed(ctx, lambda i: ctx.gemm_multi_dispatch_rmsnorm(x, gm, 1, K, [w.task(i, y)]), steps, 10, w.R)
     w.free()
     for b in (x, gm, q, y):
         ctx.free(b)
-    out = {"us_rmsnorm_q8k": round(ms_norm * 1e3, 3), "us_rmsnorm_then_gemv": round(ms * 1e3, 3)}
+    nbytes = N * 1440 + 2 * K * 4 + N * 4  # weights + fp32 x + gamma + fp32 y
+    out = {"us_rmsnorm_q8k": round(ms_norm * 1e3, 3), "us_rmsnorm_then_gemv": round(ms * 1e3, 3),
+           "us_rmsnorm_fused_gemv": round(ms_fused * 1e3, 3), "gbs_fused": round(gbs(nbytes, ms_fused), 1)}
     log(f"RMSNorm->Q8_K + GEMV: {out}")
     return out
 

@@ -256,6 +256,19 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K,
 int qmm_gemm_multi_dispatch_prequantized(qmm_context *ctx, const void *q8k, const void *q80,
                                          int M, int K, qmm_matrix_task *tasks, int n_tasks);
 
+/* The engine's normed projection: rmsnorm_fp16_rows_fast of x [M][K] with
+ * gamma (E:4264-4314, the producer that sets the prequantized flag,
+ * E:4303-4312), then sdot_gemm_multi_dispatch on that prequantized input
+ * (E:4188-4262, E:4207-4208) — the pair qmm_rmsnorm_q8k +
+ * qmm_gemm_multi_dispatch_prequantized in one call, with the same results.
+ * At M = 1 with only Q4_K / Q5_K / Q6_K tasks on the batch-1 persistent grid
+ * the norm runs inside each workgroup's activation fill (one launch);
+ * otherwise the norm's kernel writes the context's buffers (and, for Q8_0
+ * tasks, the normed row's Q8_0) and the tasks run on them. K % 256 == 0,
+ * K <= 16384; x and gamma 16-B aligned. */
+int qmm_gemm_multi_dispatch_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int M, int K,
+                                    qmm_matrix_task *tasks, int n_tasks);
+
 /* qmm_gemm_multi_dispatch that allocates nothing. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

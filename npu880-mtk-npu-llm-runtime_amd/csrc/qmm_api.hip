@@ -791,6 +791,48 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
     return run_tasks(ctx, nullptr, q8k, q80, M, K, tasks, n_tasks);
 }
 
+int qmm_gemm_multi_dispatch_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int M, int K,
+                                    qmm_matrix_task *tasks, int n_tasks) {
+    if (!ctx) return QMM_EINVAL;
+    if (!x || !gamma) return fail(ctx, QMM_EINVAL, "null x or gamma");
+    bool need_q8k, need_q80;
+    int rc = check_tasks(ctx, M, K, tasks, n_tasks, &need_q8k, &need_q80);
+    if (rc) return rc;
+    if (K % 256) return fail(ctx, QMM_ESHAPE, "K must be a multiple of 256");
+    if (K > 16384) return fail(ctx, QMM_ESHAPE, "K above 16384");
+    if (!aligned(x, 16) || !aligned(gamma, 16)) return fail(ctx, QMM_EALIGN, "x and gamma must be 16-B aligned");
+    if ((rc = use_device(ctx))) return rc;
+    // batch 1, k-quant tasks: the norm inside every workgroup's activation fill
+    if (M == 1 && !need_q80) {
+        qmm::MatArgs group[qmm::kMaxGroup];
+        int n = 0;
+        bool fits = true;
+        for (int t = 0; t < n_tasks && fits; ++t) {
+            if (tasks[t].rows == 0) continue;
+            if (n == qmm::kMaxGroup || is_float(tasks[t].type)) fits = false;
+            else group[n++] = mat_args(tasks[t], 1, K);
+        }
+        if (fits && n > 0) {
+            const hipError_t e = qmm::launch_gemv_rms(group, n, x, gamma, ctx->stream);
+            if (e == hipSuccess) return QMM_OK;
+            if (e != hipErrorNotSupported) return hip_fail(ctx, e, "matmul launch");
+        }
+    }
+    // else the norm's own kernel into the context's buffers, then the tasks
+    const size_t k_bytes = qmm::Q8KLayout(M, K).total;
+    const size_t y_bytes = need_q80 ? align256(size_t(M) * size_t(K) * 4) : 0;
+    const size_t z_bytes = need_q80 ? qmm::Q80Layout(M, K).total : 0;
+    if ((rc = ensure_act(ctx, k_bytes + y_bytes + z_bytes))) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->act);
+    float *y = need_q80 ? reinterpret_cast<float *>(base + k_bytes) : nullptr;
+    void *q80 = need_q80 ? base + k_bytes + y_bytes : nullptr;
+    hipError_t e = qmm::launch_rmsnorm_q8k(x, gamma, M, K, y, base, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+    if (need_q80 && (e = qmm::launch_quantize_q8_0(y, M, K, q80, ctx->stream)) != hipSuccess)
+        return hip_fail(ctx, e, "quantize_q8_0 launch");
+    return run_tasks(ctx, nullptr, base, q80, M, K, tasks, n_tasks);
+}
+
 int qmm_gemm_multi_dispatch_noalloc(qmm_context *ctx, const float *x, int M, int K, qmm_matrix_task *tasks,
                                     int n_tasks) {
     if (!ctx) return QMM_EINVAL;

@@ -180,6 +180,10 @@ size_t gemv_lds_bytes(uint32_t type, int K);
 // workgroup runs its own task's format. Its LDS need per type and K:
 hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk, const Q80View &x0,
                              hipStream_t s);
+// batch-1 k-quant group on the row before its RMSNorm, the norm fused into
+// the activation fill; hipErrorNotSupported (nothing launched) where it does
+// not apply
+hipError_t launch_gemv_rms(const MatArgs *tasks, int n, const float *x32, const float *gamma, hipStream_t s);
 size_t gemv_mixed_lds_bytes(uint32_t type, int K);
 // M = 1 GEMV of one task with the LM head's running (max, argmax) fused into
 // its persistent grid: each workgroup writes one partial (value, row) to part
@@ -306,6 +310,32 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// RMSNorm's scale of one row (rmsnorm_fp16_rows_fast, E:4264-4314) in a
+// 256-thread workgroup, in the batch-1 activation fill's layout: thread t of
+// wave w, 16-lane row r = (t / 16) % 4 and lane sub = t % 16 adds the squares
+// of the fp16-rounded values 16 sub .. 16 sub + 15 of the row's 256-value
+// chunks 16 i + 4 w + r (i = 0, 1, ... while inside the row) in order into s;
+// the wave adds the 64 sums by a fixed butterfly, and the four wave sums meet
+// as (w0 + w1) + (w2 + w3); inv_rms = 1 / sqrtf(sum * (1 / K) + 1e-6f)
+// (E:4295). part: 4 floats of LDS. Every workgroup that calls it on the same
+// row gets the same value (not the reference's row-ordered sum: its last bits
+// may differ).
+__device__ inline float rms_add4(float s, float4 h) {
+    s += h.x * h.x;
+    s += h.y * h.y;
+    s += h.z * h.z;
+    s += h.w * h.w;
+    return s;
+}
+__device__ inline float rms_inv(float s, int K, float *part) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    lds_barrier();
+    const float sum_sq = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv_k = 1.0f / (float)K;
+    return 1.0f / sqrtf(sum_sq * inv_k + 1.0e-6f);  // E:4295
 }
 __device__ inline uint2 ld8(const void *p) { return *reinterpret_cast<const uint2 *>(p); }
 // 8 bytes starting at a 2-B aligned address: the aligned dwords that hold

@@ -390,11 +390,16 @@ __global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const flo
 // fill the waves never synchronize with each other.
 // X16: x32 holds an fp16 row (reinterpreted), quantized in the kernel.
 // The body of one workgroup of the persistent grid: workgroup wgi of the
-// nwg that share the task's row groups.
-template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false>
+// nwg that share the task's row groups. RMS (with FUSED, K <= 4096): x32 is
+// the row before its RMSNorm, gamma the norm's weights; the workgroup forms
+// the normed fp16 row (rmsnorm_fp16_rows_fast, E:4264-4314, the same values
+// as rmsnorm_q8k_kernel) and quantizes that.
+template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false, bool RMS = false>
 __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a, const float *__restrict__ x32,
                                                                       Q8KView prek, Q80View pre0, AmaxOut am,
-                                                                      int wgi, int nwg) {
+                                                                      int wgi, int nwg,
+                                                                      const float *__restrict__ gamma = nullptr) {
+    static_assert(!RMS || (FUSED && !X16 && !AMAX), "the RMSNorm fill takes an fp32 row");
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
@@ -465,6 +470,10 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
         if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
     }
     else cpre_load<q80>(pq, pd, pb, K, cp);
+    // RMS: the norm's weights, in the fill's order
+    [[maybe_unused]] XPre gp;
+    if constexpr (RMS)
+        if (x_has(0, K)) x_load(gamma, K, x_chunk(0, K), gp);
     if constexpr (AMAX) {
         if (am.pre.part) {
             __shared__ Best psh[4];
@@ -502,6 +511,26 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     stage_load(min(gw, ngroups - 1));
     __builtin_amdgcn_sched_barrier(0);
     // 2. the activations into LDS, once
+    if constexpr (RMS) {
+        // the sum of squares over the lane's 16 values of round 0 (K <= 4096:
+        // the whole row), duplicates of the last chunk left out
+        __shared__ float rms_part[4];
+        float ss = 0.0f;
+        if (x_has(0, K) && 4 * (int(threadIdx.x) >> 6) + ((int(threadIdx.x) >> 4) & 3) < (K >> 8)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                ss = rms_add4(ss, make_float4(round_to_fp16(xp.v[i].x), round_to_fp16(xp.v[i].y),
+                                              round_to_fp16(xp.v[i].z), round_to_fp16(xp.v[i].w)));
+        }
+        const float inv_rms = rms_inv(ss, K, rms_part);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // y = fp16((x * inv_rms) * fp16(gamma)), E:4301
+            xp.v[i].x = round_to_fp16(round_to_fp16(xp.v[i].x) * inv_rms * round_to_fp16(gp.v[i].x));
+            xp.v[i].y = round_to_fp16(round_to_fp16(xp.v[i].y) * inv_rms * round_to_fp16(gp.v[i].y));
+            xp.v[i].z = round_to_fp16(round_to_fp16(xp.v[i].z) * inv_rms * round_to_fp16(gp.v[i].z));
+            xp.v[i].w = round_to_fp16(round_to_fp16(xp.v[i].w) * inv_rms * round_to_fp16(gp.v[i].w));
+        }
+    }
     if constexpr (X16) x16_fill<q80, std::is_same_v<F, FmtQ6K4>>(x16q, K, act);
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
@@ -652,9 +681,12 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
 // stage loads per lane are the format's largest count less D (the launcher
 // takes the largest D that still covers every task's row groups). Each
 // output equals the one-task launch's, bit for bit.
-template <bool FUSED, int D>
+// RMS: x32 is the row before its RMSNorm (gamma: the norm's weights), every
+// task a k-quant one; each workgroup normalizes the row itself.
+template <bool FUSED, int D, bool RMS = false>
 __global__ __launch_bounds__(256) void gemv_mixed_persist_kernel(MatGroup grp, const float *__restrict__ x32,
-                                                                 Q8KView prek, Q80View pre0) {
+                                                                 Q8KView prek, Q80View pre0,
+                                                                 const float *__restrict__ gamma) {
     int bx = 0;
     const int t = group_task(grp, int(blockIdx.x), bx);
     const MatArgs a = grp.t[t];
@@ -662,14 +694,37 @@ __global__ __launch_bounds__(256) void gemv_mixed_persist_kernel(MatGroup grp, c
     constexpr int N4 = stage_chunks<FmtQ4K4, 3>() - D, N5 = stage_chunks<FmtQ5K4, 3>() - D;
     constexpr int N6 = stage_chunks<FmtQ6K4, 3>() - D;
     switch (a.type) {
-        case kQ4_K: gemv_persist_wg<FmtQ4K4, kGemvR, 3, FUSED, N4, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
-        case kQ5_K: gemv_persist_wg<FmtQ5K4, kGemvR, 3, FUSED, N5, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
-        case kQ6_K: gemv_persist_wg<FmtQ6K4, kGemvR, 3, FUSED, N6, false>(a, x32, prek, pre0, AmaxOut{}, bx, nwg); break;
-        case kF32: gemv_float_wg<false, 1, FUSED>(a, bx, x32, prek.h); break;
-        case kF16: gemv_float_wg<true, 1, FUSED>(a, bx, x32, prek.h); break;
+        case kQ4_K:
+            gemv_persist_wg<FmtQ4K4, kGemvR, 3, FUSED, N4, false, false, RMS>(a, x32, prek, pre0, AmaxOut{}, bx, nwg, gamma);
+            break;
+        case kQ5_K:
+            gemv_persist_wg<FmtQ5K4, kGemvR, 3, FUSED, N5, false, false, RMS>(a, x32, prek, pre0, AmaxOut{}, bx, nwg, gamma);
+            break;
+        case kQ6_K:
+            gemv_persist_wg<FmtQ6K4, kGemvR, 3, FUSED, N6, false, false, RMS>(a, x32, prek, pre0, AmaxOut{}, bx, nwg, gamma);
+            break;
+        case kF32:
+            if constexpr (!RMS) gemv_float_wg<false, 1, FUSED>(a, bx, x32, prek.h);
+            break;
+        case kF16:
+            if constexpr (!RMS) gemv_float_wg<true, 1, FUSED>(a, bx, x32, prek.h);
+            break;
         default: break;
     }
 }
+
+template <class F> struct FmtTag { using type = F; };
+
+// One task on the row before its RMSNorm: the one-task persistent grid with
+// the norm in its fill, the task's arguments passed directly (no group
+// table to resolve before the first activation load).
+template <class F, int NC>
+__global__ __launch_bounds__(256) void gemv_persist_rms_kernel(MatArgs a, const float *__restrict__ x32,
+                                                               const float *__restrict__ gamma) {
+    gemv_persist_wg<F, kGemvR, 3, true, NC, false, false, true>(a, x32, Q8KView{}, Q80View{}, AmaxOut{},
+                                                               int(blockIdx.x), int(gridDim.x), gamma);
+}
+
 
 // ------------------------------------------- 2..4 tokens, batch-1 shape
 // The persistent kernel's structure for 2 <= M <= MT <= 4 tokens on a
@@ -915,7 +970,7 @@ static hipError_t launch_gemv_t(const MatArgs *tasks, int n, const float *x32, c
 }
 
 static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
-                                            const Q80View &x0, hipStream_t s);
+                                            const Q80View &x0, hipStream_t s, const float *gamma = nullptr);
 
 // Rows per wave by the launch's total rows and K (measured per shape): the
 // k-quants take 4 from 4096 rows, else 2 up to K = 4096, else 1 (the 2560-row
@@ -976,14 +1031,17 @@ static hipError_t launch_gemv_mixed_r(const MatArgs *tasks, int n, const float *
 // in proportion to their row groups. hipErrorNotSupported (nothing launched)
 // where that does not apply.
 static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
-                                            const Q80View &x0, hipStream_t s) {
+                                            const Q80View &x0, hipStream_t s, const float *gamma) {
     const int K = tasks[0].K, nb = K / 256, cus = cu_count();
     if (K % 256 || kGemvR * nb > 16 * 3) return hipErrorNotSupported;
+    const bool rms = gamma != nullptr;  // (K <= 3072 here: the fill's sum of squares covers it)
+    if (rms && !x32) return hipErrorNotSupported;
     int quads[kMaxGroup] = {}, total = 0, d = 2, fw = 0;
     size_t lds = 0;
     for (int i = 0; i < n; ++i) {
         const uint32_t ty = tasks[i].type;
         if (ty == kF32 || ty == kF16) {
+            if (rms) return hipErrorNotSupported;
             fw += (tasks[i].N + 3) / 4;  // one row per wave
             continue;
         }
@@ -1001,47 +1059,83 @@ static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const f
         total += quads[i];
     }
     if (total < 2 * cus || d < 0) return hipErrorNotSupported;
-    // the merged bodies hold more registers than any one-format kernel: the
-    // grid is the one-task grid, but never more than the workgroups that are
-    // resident at once
-    const void *fn = nullptr;
-    if (d >= 2) fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 2>)
-                         : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 2>);
-    else if (d == 1) fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 1>)
-                              : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 1>);
-    else fn = x32 ? reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<true, 0>)
-                  : reinterpret_cast<const void *>(&gemv_mixed_persist_kernel<false, 0>);
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess || per_cu < 1) {
-        (void)hipGetLastError();
-        return hipErrorNotSupported;
+    // The merged bodies hold more registers than any one-format kernel: the
+    // grid is the one-task grid, but never more than the workgroups resident
+    // at once (a one-format kernel per group measured no faster).
+    uint32_t one = 0;
+    for (int i = 0; i < n && fw == 0; ++i) {
+        if (one == 0) one = tasks[i].type;
+        else if (tasks[i].type != one) one = ~0u;
     }
-    const int G = min(persist_grid(total, cus), max(cus, per_cu * cus - fw));
-    MatGroup g{};
-    g.n = n;
-    g.wg0[0] = 0;
-    int cum = 0;
-    for (int i = 0; i < n; ++i) {
-        g.t[i] = tasks[i];
-        int w;
-        if (quads[i] == 0) {
-            w = (tasks[i].N + 3) / 4;
-        } else {
-            w = max(1, int(int64_t(G) * (cum + quads[i]) / total - int64_t(G) * cum / total));
-            cum += quads[i];
+    if (fw > 0) one = ~0u;
+    const int dd = min(d, 2);
+    auto run = [&](auto kern) -> hipError_t {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256, lds) !=
+                hipSuccess || per_cu < 1) {
+            (void)hipGetLastError();
+            return hipErrorNotSupported;
         }
-        g.wg0[i + 1] = g.wg0[i] + w;
-    }
-    const dim3 grid(unsigned(g.wg0[n]));
-    auto go = [&](auto dd) {
-        constexpr int DD = decltype(dd)::value;
-        if (x32) hipLaunchKernelGGL((gemv_mixed_persist_kernel<true, DD>), grid, dim3(256), lds, s, g, x32, xk, x0);
-        else hipLaunchKernelGGL((gemv_mixed_persist_kernel<false, DD>), grid, dim3(256), lds, s, g, x32, xk, x0);
+        const int G = min(persist_grid(total, cus), max(cus, per_cu * cus - fw));
+        MatGroup g{};
+        g.n = n;
+        g.wg0[0] = 0;
+        int cum = 0;
+        for (int i = 0; i < n; ++i) {
+            g.t[i] = tasks[i];
+            int w;
+            if (quads[i] == 0) {
+                w = (tasks[i].N + 3) / 4;
+            } else {
+                w = max(1, int(int64_t(G) * (cum + quads[i]) / total - int64_t(G) * cum / total));
+                cum += quads[i];
+            }
+            g.wg0[i + 1] = g.wg0[i] + w;
+        }
+        hipLaunchKernelGGL(kern, dim3(unsigned(g.wg0[n])), dim3(256), lds, s, g, x32, xk, x0, gamma);
         return hipGetLastError();
     };
-    if (d >= 2) return go(std::integral_constant<int, 2>{});
-    if (d == 1) return go(std::integral_constant<int, 1>{});
-    return go(std::integral_constant<int, 0>{});
+    // one task of one format on the row before its norm: its arguments
+    // passed directly, at stage-load count NST - D
+    auto one_task = [&](auto fmt) -> hipError_t {
+        using F = typename decltype(fmt)::type;
+        constexpr int NST = stage_chunks<F, 3>();
+        auto go1 = [&](auto kern) -> hipError_t {
+            int per_cu = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256,
+                                                             lds) != hipSuccess || per_cu < 1) {
+                (void)hipGetLastError();
+                return hipErrorNotSupported;
+            }
+            const int G = min(persist_grid(total, cus), per_cu * cus);
+            hipLaunchKernelGGL(kern, dim3(unsigned(G)), dim3(256), lds, s, tasks[0], x32, gamma);
+            return hipGetLastError();
+        };
+        if (dd == 2) return go1(gemv_persist_rms_kernel<F, NST - 2>);
+        if (dd == 1) return go1(gemv_persist_rms_kernel<F, NST - 1>);
+        return go1(gemv_persist_rms_kernel<F, NST>);
+    };
+    if (rms && n == 1) {
+        switch (one) {
+            case kQ4_K: return one_task(FmtTag<FmtQ4K4>{});
+            case kQ5_K: return one_task(FmtTag<FmtQ5K4>{});
+            case kQ6_K: return one_task(FmtTag<FmtQ6K4>{});
+            default: break;
+        }
+    }
+    if (rms) {
+        if (dd == 2) return run(gemv_mixed_persist_kernel<true, 2, true>);
+        if (dd == 1) return run(gemv_mixed_persist_kernel<true, 1, true>);
+        return run(gemv_mixed_persist_kernel<true, 0, true>);
+    }
+    if (x32) {
+        if (dd == 2) return run(gemv_mixed_persist_kernel<true, 2>);
+        if (dd == 1) return run(gemv_mixed_persist_kernel<true, 1>);
+        return run(gemv_mixed_persist_kernel<true, 0>);
+    }
+    if (dd == 2) return run(gemv_mixed_persist_kernel<false, 2>);
+    if (dd == 1) return run(gemv_mixed_persist_kernel<false, 1>);
+    return run(gemv_mixed_persist_kernel<false, 0>);
 }
 
 hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk, const Q80View &x0,
@@ -1054,6 +1148,16 @@ hipError_t launch_gemv_mixed(const MatArgs *tasks, int n, const float *x32, cons
     if (rows >= 4096) return launch_gemv_mixed_r<kGemvR>(tasks, n, x32, xk, x0, s);
     if (tasks[0].K <= 4096) return launch_gemv_mixed_r<2>(tasks, n, x32, xk, x0, s);
     return launch_gemv_mixed_r<1>(tasks, n, x32, xk, x0, s);
+}
+
+// A batch-1 group (one task or several) of k-quant tasks on the row before
+// its RMSNorm: the norm fused into every workgroup's activation fill, on the
+// persistent slices; hipErrorNotSupported (nothing launched) where those do
+// not apply (the caller then runs the norm's own kernel and the group on
+// its Q8_K buffer).
+hipError_t launch_gemv_rms(const MatArgs *tasks, int n, const float *x32, const float *gamma, hipStream_t s) {
+    if (n < 1 || n > kMaxGroup || !x32 || !gamma) return hipErrorNotSupported;
+    return launch_gemv_mixed_persist(tasks, n, x32, Q8KView{}, Q80View{}, s, gamma);
 }
 
 size_t gemv_mixed_lds_bytes(uint32_t type, int K) {

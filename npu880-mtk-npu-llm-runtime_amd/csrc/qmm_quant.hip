@@ -126,24 +126,25 @@ __global__ __launch_bounds__(256) void rmsnorm_q8k_kernel(const float *__restric
     const float *xr = x + m * size_t(K);
     const int nq = K >> 2;  // float4s in the row
     float4 h[NJ];
-    float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int q = t + 256 * j;
         const float4 v = q < nq ? reinterpret_cast<const float4 *>(xr)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
         h[j] = make_float4(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z), round_to_fp16(v.w));
-        s += h[j].x * h[j].x;
-        s += h[j].y * h[j].y;
-        s += h[j].z * h[j].z;
-        s += h[j].w * h[j].w;
     }
+    // the sum of squares in the batch-1 activation fill's layout (so the GEMV
+    // that normalizes its own input forms the same inv_rms)
+    float s = 0.0f;
+    const int nc = K >> 8, sub = t & 15;
+    for (int c = 4 * wid + ((t >> 4) & 3); c < nc; c += 16) {
+        const float4 *q = reinterpret_cast<const float4 *>(xr + c * 256 + 16 * sub);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (lane == 0) part[wid] = s;
-    __syncthreads();
-    const float sum_sq = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inv_k = 1.0f / (float)K;
-    const float inv_rms = 1.0f / sqrtf(sum_sq * inv_k + 1.0e-6f);  // E:4295
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = q[i];
+            s = rms_add4(s, make_float4(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z), round_to_fp16(v.w)));
+        }
+    }
+    const float inv_rms = rms_inv(s, K, part);
     const size_t nbk = size_t(K) >> 8;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {

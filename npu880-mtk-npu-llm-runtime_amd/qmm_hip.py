@@ -108,6 +108,7 @@ _SIGNATURES = [
     ("qmm_gemm_multi_dispatch_prequantized", C.c_int,
      [_p, _p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_gemm_multi_dispatch_noalloc", C.c_int, [_p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
+    ("qmm_gemm_multi_dispatch_rmsnorm", C.c_int, [_p, _p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_noalloc_scratch_bytes", C.c_size_t, []),
     ("qmm_graph_begin", C.c_int, [_p]),
     ("qmm_graph_end", C.c_int, [_p, C.POINTER(_p)]),
@@ -445,6 +446,14 @@ class Context:
     def gemm_multi_dispatch(self, x, M: int, K: int, tasks: Sequence[MatrixTask]):
         arr = self._tasks(M, K, tasks)
         self._call("qmm_gemm_multi_dispatch", self._h, _p(_addr(x)), M, K, arr, len(tasks))
+        for t, a in zip(tasks, arr):
+            t.start_row = a.start_row
+
+    def gemm_multi_dispatch_rmsnorm(self, x, gamma, M: int, K: int, tasks: Sequence[MatrixTask]):
+        """qmm_gemm_multi_dispatch_rmsnorm: RMSNorm of x with gamma, then the tasks."""
+        arr = self._tasks(M, K, tasks)
+        self._call("qmm_gemm_multi_dispatch_rmsnorm", self._h, _p(_addr(x)), _p(_addr(gamma)), M, K, arr,
+                   len(tasks))
         for t, a in zip(tasks, arr):
             t.start_row = a.start_row
 

@@ -89,3 +89,63 @@ def test_rmsnorm_block_mismatch_rate(ctx, oracle):
     assert blocks.mean() < 0.25
     for b in (xb, gb, q):
         ctx.free(b)
+
+
+def _normed_dispatch(ctx, oracle, specs, M, K, seed):
+    """qmm_gemm_multi_dispatch_rmsnorm against qmm_rmsnorm_q8k followed by the
+    prequantized dispatch (bit-exact: the same normed values, the same
+    codes), and against the oracle's norm and dispatch within the tolerance
+    (its row-ordered sum of squares may move a code)."""
+    import qmm_hip
+    import synth
+    from gpu_util import TOL, norm_err
+    g = np.random.default_rng(seed)
+    x = (g.standard_normal((M, K)) * 2).astype(np.float32)
+    gamma = g.uniform(0.5, 1.5, K).astype(np.float32)
+    xb, gb = ctx.upload(x), ctx.upload(gamma)
+    ws, wbs, ya, yb = [], [], [], []
+    for i, (t, n) in enumerate(specs):
+        w = synth.float_rows(t, n, K, seed + 1 + i) if t in (0, 1) else synth.weights(t, n, K, seed=seed + 1 + i)
+        ws.append(w)
+        wbs.append(ctx.weight_upload(w, t, n, K))
+        ya.append(ctx.malloc(M * n * 4))
+        yb.append(ctx.malloc(M * n * 4))
+    ctx.gemm_multi_dispatch_rmsnorm(xb, gb, M, K, [qmm_hip.MatrixTask(wbs[i], t, n, K, ya[i], n)
+                                                   for i, (t, n) in enumerate(specs)])
+    q8k = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    yn = ctx.malloc(M * K * 4)
+    ctx.rmsnorm_q8k(xb, gb, M, K, yn, q8k)
+    q80 = None
+    if any(t == qmm_hip.TYPE_Q8_0 for t, _ in specs):
+        q80 = ctx.malloc(ctx.lib.qmm_q8_0_bytes(M, K))
+        ctx.quantize_q8_0(yn, M, K, q80)
+    ctx.gemm_multi_dispatch_prequantized(q8k, q80, M, K, [qmm_hip.MatrixTask(wbs[i], t, n, K, yb[i], n)
+                                                          for i, (t, n) in enumerate(specs)])
+    ctx.sync()
+    ry, _ = oracle.rmsnorm_q8k(x, gamma)
+    exp = oracle.gemm_multi(ry, [dict(w=w, type=t, rows=n) for w, (t, n) in zip(ws, specs)])
+    for i, (t, n) in enumerate(specs):
+        got = ctx.d2h(ya[i], np.float32, (M, n))
+        two = ctx.d2h(yb[i], np.float32, (M, n))
+        assert np.array_equal(got.view(np.uint32), two.view(np.uint32)), f"task {i}: fused != two steps"
+        err = norm_err(got, exp[i])
+        say(f"  task {i} {qmm_hip.TYPE_NAMES[t]} {n}: vs oracle {err:.2e}")
+        assert err <= TOL
+    for b in [xb, gb, q8k, yn] + wbs + ya + yb + ([q80] if q80 is not None else []):
+        ctx.free(b)
+
+
+@pytest.mark.parametrize("specs,M,K", [
+    ([(12, 9728)], 1, 2560),                          # one task: the norm in the fill
+    ([(13, 6144), (13, 1024), (13, 1024)], 1, 2560),  # {q, k, v} of one format
+    ([(13, 8192), (12, 4096)], 1, 2560),              # two formats
+    ([(12, 8192), (14, 4096)], 1, 3072),              # Q6_K, K = 3072 (the fill's largest)
+    ([(12, 256)], 1, 2560),                           # too few rows: norm kernel + dispatch
+    ([(12, 9728), (8, 512)], 1, 2560),                # a Q8_0 task: the normed row's Q8_0
+    ([(13, 4096), (0, 32)], 1, 2560),                 # an F32 task
+    ([(12, 4096)], 3, 2560),                          # M > 1
+    ([(14, 8192)], 1, 9728),                          # K past the fill's sum
+])
+def test_rmsnorm_dispatch(ctx, oracle, specs, M, K):
+    say(f"rmsnorm dispatch {specs} M={M} K={K}")
+    _normed_dispatch(ctx, oracle, specs, M, K, seed=7 * K + len(specs) + M)
