@@ -26,6 +26,8 @@
 // with 16 B of padding per 256 values so lanes on consecutive blocks hit
 // different banks. Vector-memory counters retire in order, so the fill
 // waits only for the input loads; the workgroup barrier orders LDS only.
+#include <mutex>
+
 #include "qmm_gemv_parts.h"
 
 namespace qmm {
@@ -861,6 +863,31 @@ static int cu_count() {
     }
     return cus[dev];
 }
+// Workgroups of kernel fn (256 threads, lds bytes of dynamic LDS) resident
+// on one CU at once, from the runtime's occupancy query, remembered per
+// device, kernel and LDS size; 0 where the query fails.
+static int resident_per_cu(const void *fn, size_t lds) {
+    struct Entry { int dev; const void *fn; size_t lds; int n; };
+    static std::mutex mu;
+    static Entry seen[64];
+    static int nseen = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int i = 0; i < nseen; ++i)
+            if (seen[i].dev == dev && seen[i].fn == fn && seen[i].lds == lds) return seen[i].n;
+    }
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (nseen < 64) seen[nseen++] = Entry{dev, fn, lds, n};
+    return n;
+}
+
 // Workgroups of the persistent batch-1 grid for `quads` (four row groups
 // each, one per wave): where the quads are exactly 2, 3 or 4 per CU, a whole
 // number of workgroups per CU whose waves take a whole number of groups each
@@ -1070,12 +1097,8 @@ static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const f
     if (fw > 0) one = ~0u;
     const int dd = min(d, 2);
     auto run = [&](auto kern) -> hipError_t {
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256, lds) !=
-                hipSuccess || per_cu < 1) {
-            (void)hipGetLastError();
-            return hipErrorNotSupported;
-        }
+        const int per_cu = resident_per_cu(reinterpret_cast<const void *>(kern), lds);
+        if (per_cu < 1) return hipErrorNotSupported;
         const int G = min(persist_grid(total, cus), max(cus, per_cu * cus - fw));
         MatGroup g{};
         g.n = n;
@@ -1101,12 +1124,8 @@ static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const f
         using F = typename decltype(fmt)::type;
         constexpr int NST = stage_chunks<F, 3>();
         auto go1 = [&](auto kern) -> hipError_t {
-            int per_cu = 0;
-            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256,
-                                                             lds) != hipSuccess || per_cu < 1) {
-                (void)hipGetLastError();
-                return hipErrorNotSupported;
-            }
+            const int per_cu = resident_per_cu(reinterpret_cast<const void *>(kern), lds);
+            if (per_cu < 1) return hipErrorNotSupported;
             const int G = min(persist_grid(total, cus), per_cu * cus);
             hipLaunchKernelGGL(kern, dim3(unsigned(G)), dim3(256), lds, s, tasks[0], x32, gamma);
             return hipGetLastError();
