@@ -432,7 +432,10 @@ def bench_ffn(ctx, args):
     SiLU(gate)*up -> Q8_K, down Q6_K 2560x9728 with its residual —
     qmm_ffn_block (gate/up with SwiGLU in its epilogue, then the down GEMV
     on h in fp16: two launches), and beside it the three separate calls
-    (dispatch, swiglu, prequantized dispatch)."""
+    (dispatch, swiglu, prequantized dispatch); then the block behind its
+    input RMSNorm: the norm's launch followed by qmm_ffn_block on its Q8_K
+    row, against qmm_ffn_block_rmsnorm (the norm in the gate/up launch's
+    fill: two launches in all)."""
     H, F = 2560, 9728
     tg, tu, td = synth.FFN["gate"], synth.FFN["up"], synth.FFN["down"]
     block = 2 * F * synth.row_bytes(tg[0], H) + H * synth.row_bytes(td[0], F)
@@ -454,17 +457,31 @@ def bench_ffn(ctx, args):
         ctx.swiglu_q8k(g, u, 1, F, h, q)
         ctx.gemm_multi_dispatch_prequantized(q, None, 1, F, [wd.task(i, y, res=res)])
 
+    gm = ctx.upload(np.random.default_rng(75).uniform(0.5, 1.5, H).astype(np.float32))
+    xq = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, H))
+
+    def norm_then_block(i):
+        ctx.rmsnorm_q8k(x, gm, 1, H, None, xq)
+        ctx.ffn_block(None, xq, H, wg.task(i, g), wu.task(i, u), wd.task(i, y, res=res), None)
+
+    def norm_block(i):
+        ctx.ffn_block_rmsnorm(x, gm, H, wg.task(i, g), wu.task(i, u), wd.task(i, y, res=res), None)
+
     steps = max(50, args.steps // 10)
     ms, _ = timed(ctx, block_call, steps, 10, R)
     ms3, _ = timed(ctx, three_calls, steps, 10, R)
+    ms_n2, _ = timed(ctx, norm_then_block, steps, 10, R)
+    ms_n1, _ = timed(ctx, norm_block, steps, 10, R)
     alg = block + H * 4 + H * 4 + H * 4  # weights + fp32 x, residual in + fp32 y out (the fused minimum)
     for b in (wg, wu, wd):
         b.free()
-    for b in (x, res, g, u, h, y, q):
+    for b in (x, res, g, u, h, y, q, gm, xq):
         ctx.free(b)
     out = {"us_per_block": round(ms * 1e3, 3), "algorithmic_bytes": alg, "gbs": round(gbs(alg, ms), 1),
            "replicas": R, "launches": "qmm_ffn_block: gate+up with SwiGLU (one launch), down GEMV on fp16 h",
-           "three_calls_us": round(ms3 * 1e3, 3)}
+           "three_calls_us": round(ms3 * 1e3, 3),
+           "with_input_rmsnorm": {"us_norm_then_block": round(ms_n2 * 1e3, 3),
+                                  "us_ffn_block_rmsnorm": round(ms_n1 * 1e3, 3)}}
     log(f"FFN block: {out}")
     return out
 

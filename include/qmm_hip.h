@@ -168,6 +168,15 @@ int qmm_swiglu_q8k(qmm_context *ctx, const float *gate, const float *up, int M, 
  * for graph capture. */
 int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_matrix_task *gate,
                   qmm_matrix_task *up, qmm_matrix_task *down, float *h_out);
+/* The FFN block behind its input norm (E:8287-8296 after the block's
+ * rmsnorm_fp16_rows_fast, E:4264-4314): qmm_rmsnorm_q8k of x [K] with gamma,
+ * then qmm_ffn_block on that prequantized row, in one call with the same
+ * outputs. Where the two-launch form applies the norm runs inside the
+ * gate/up launch's activation fill (two launches in all); else the norm's
+ * kernel, then the three steps. K % 256 == 0, K <= 16384; x and gamma 16-B
+ * aligned. */
+int qmm_ffn_block_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int K, qmm_matrix_task *gate,
+                          qmm_matrix_task *up, qmm_matrix_task *down, float *h_out);
 /* rmsnorm_fp16_rows_fast (E:4264-4314) with its Q8_K output (E:4303-4305,
  * the producer that sets the prequantized flag, E:4312): per row of x
  * [M][K], y = fp16(x * inv_rms * gamma), inv_rms = 1 / sqrt(mean(x^2) +

@@ -695,9 +695,12 @@ int qmm_rmsnorm_q8k(qmm_context *ctx, const float *x, const float *gamma, int M,
     return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "rmsnorm launch");
 }
 
-int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_matrix_task *gate,
-                  qmm_matrix_task *up, qmm_matrix_task *down, float *h_out) {
-    if (!ctx) return QMM_EINVAL;
+namespace {
+
+// qmm_ffn_block, and with gamma (x then the row before its RMSNorm) the
+// block behind its input norm
+int ffn_block(qmm_context *ctx, const float *x, const float *gamma, const void *q8k, int K, qmm_matrix_task *gate,
+              qmm_matrix_task *up, qmm_matrix_task *down, float *h_out) {
     if (!gate || !up || !down) return fail(ctx, QMM_EINVAL, "null task");
     if ((x == nullptr) == (q8k == nullptr)) return fail(ctx, QMM_EINVAL, "give exactly one of x and q8k");
     qmm_matrix_task gu[2] = {*gate, *up};
@@ -717,7 +720,9 @@ int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_
     if ((rc = check_tasks(ctx, 1, N, &dn, 1, &dn_q8k, &dn_q80))) return rc;
     if (dn_q80) return fail(ctx, QMM_ETYPE, "a Q8_0 down task needs Q8_0 activations; h is quantized to Q8_K");
     if ((rc = use_device(ctx))) return rc;
-    if ((rc = ensure_act(ctx, ffn_scratch_bytes(N)))) return rc;
+    // (with the norm, the normed row's Q8_K behind the block's scratch, for the three-step form)
+    const size_t norm_b = gamma ? align256(qmm::Q8KLayout(1, K).total) : 0;
+    if ((rc = ensure_act(ctx, ffn_scratch_bytes(N) + norm_b))) return rc;
     uint8_t *scr = static_cast<uint8_t *>(ctx->act);
     void *hq = scr;  // h's Q8_K (separate launches) or h in fp16 (one launch)
     float *h = h_out ? h_out : reinterpret_cast<float *>(scr + align256(qmm::Q8KLayout(1, N).total));
@@ -742,15 +747,41 @@ int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_
         a.F = N;
         a.rb1 = int(gate->row_bytes);
         a.type = gate->type;
+        a.gamma = gamma;
         hipError_t e = qmm::launch_ffn_gate_up(a, x, xk, ctx->stream);
         if (e == hipSuccess) e = qmm::launch_gemv_x16(dn.type, da, reinterpret_cast<const uint16_t *>(hx), ctx->stream);
         return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "FFN block launch");
     }
-    // the reference's three steps as separate launches
+    // the reference's three steps as separate launches (after the norm's own)
+    if (gamma) {
+        void *nq = scr + ffn_scratch_bytes(N);
+        const hipError_t e = qmm::launch_rmsnorm_q8k(x, gamma, 1, K, nullptr, nq, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+        x = nullptr;
+        q8k = nq;
+    }
     if ((rc = run_tasks(ctx, x, q8k, nullptr, 1, K, gu, 2))) return rc;
     const hipError_t e = qmm::launch_swiglu_q8k(gate->dst, up->dst, 1, N, h, hq, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "swiglu launch");
     return run_tasks(ctx, nullptr, hq, nullptr, 1, N, &dn, 1);
+}
+
+}  // namespace
+
+int qmm_ffn_block(qmm_context *ctx, const float *x, const void *q8k, int K, qmm_matrix_task *gate,
+                  qmm_matrix_task *up, qmm_matrix_task *down, float *h_out) {
+    if (!ctx) return QMM_EINVAL;
+    return ffn_block(ctx, x, nullptr, q8k, K, gate, up, down, h_out);
+}
+
+int qmm_ffn_block_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int K, qmm_matrix_task *gate,
+                          qmm_matrix_task *up, qmm_matrix_task *down, float *h_out) {
+    if (!ctx) return QMM_EINVAL;
+    if (!x || !gamma) return fail(ctx, QMM_EINVAL, "null x or gamma");
+    if (K % 256) return fail(ctx, QMM_ESHAPE, "K must be a multiple of 256");
+    if (K > 16384) return fail(ctx, QMM_ESHAPE, "K above 16384");
+    if (!aligned(gamma, 16)) return fail(ctx, QMM_EALIGN, "gamma must be 16-B aligned");
+    return ffn_block(ctx, x, gamma, nullptr, K, gate, up, down, h_out);
 }
 
 int qmm_dequantize_f16(qmm_context *ctx, const void *w_blocks, uint32_t type, int64_t rows,

@@ -237,6 +237,7 @@ struct FfnArgs {
     int K, F;
     int rb1;           // row bytes of gate / up
     uint32_t type;     // gate / up format: kQ4_K or kQ5_K
+    const float *gamma = nullptr;  // the input norm's weights: x is the row before its RMSNorm
 };
 hipError_t launch_ffn_gate_up(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s);
 // M = 1 GEMV of one task on an fp16 activation row x16 (16-B aligned, K %

@@ -41,8 +41,11 @@ __device__ inline void wave_lds_fence() {
 // FG: the gate/up format (FmtQ4K4 or FmtQ5K4, 4 lanes per block); FUSED:
 // x32 is quantized here, otherwise prek holds the prequantized input row.
 // NC: 16-B stage loads per lane of a group.
-template <class FG, bool FUSED, int NC>
+// RMS (with FUSED, K <= 4096): x32 is the row before its RMSNorm, a.gamma
+// the norm's weights; the workgroup forms the normed row in its fill.
+template <class FG, bool FUSED, int NC, bool RMS = false>
 __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float *__restrict__ x32, Q8KView prek) {
+    static_assert(!RMS || FUSED, "the RMSNorm fill takes the fp32 row");
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(FG::G == 4, "a row's lane groups fill one 16-lane DPP row");
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -74,8 +77,11 @@ __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float
     const int stride = int(gridDim.x) * 4;
     XPre xp;
     CPre cp;
+    [[maybe_unused]] XPre gp;
     if constexpr (FUSED) {
         if (x_has(0, K)) x_load(x32, K, x_chunk(0, K), xp);
+        if constexpr (RMS)
+            if (x_has(0, K)) x_load(a.gamma, K, x_chunk(0, K), gp);
     } else {
         cpre_load<false>(prek.qs, prek.d, prek.bs, K, cp);
     }
@@ -83,6 +89,10 @@ __global__ __launch_bounds__(256) void ffn_gate_up_kernel(FfnArgs a, const float
     __builtin_amdgcn_sched_barrier(0);
     if (gw < ngroups) stage_load(gw);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RMS) {
+        __shared__ float rms_part[4];
+        rms_fill_transform(xp, gp, K, rms_part);
+    }
     if constexpr (FUSED) x_fill<false, false>(xp, x32, K, act);
     else cpre_fill<false, false>(cp, prek.qs, prek.d, prek.bs, K, act);
     lds_barrier();
@@ -161,7 +171,7 @@ int cus_of_device() {
     return cus[dev];
 }
 
-template <class FG, bool FUSED, int NC>
+template <class FG, bool FUSED, int NC, bool RMS = false>
 hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
     const int ngroups = (a.F + kRP - 1) / kRP;
     const int quads = (ngroups + 3) / 4;
@@ -170,7 +180,7 @@ hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &x
     // workgroups 15.9 us, 760 16.1, 1024 16.7, 384 17.2)
     const int cus = cus_of_device();
     const int wgs = max(1, min(2 * cus, quads * 5 / 8));
-    hipLaunchKernelGGL((ffn_gate_up_kernel<FG, FUSED, NC>), dim3(unsigned(wgs)), dim3(256), gate_up_lds_bytes(a.K, NC),
+    hipLaunchKernelGGL((ffn_gate_up_kernel<FG, FUSED, NC, RMS>), dim3(unsigned(wgs)), dim3(256), gate_up_lds_bytes(a.K, NC),
                        s, a, x32, xk);
     return hipGetLastError();
 }
@@ -180,6 +190,12 @@ hipError_t launch_gate_up_t(const FfnArgs &a, const float *x32, const Q8KView &x
 template <class FG>
 hipError_t launch_gate_up_f(const FfnArgs &a, const float *x32, const Q8KView &xk, hipStream_t s) {
     const int need = (2 * kRP * (a.K / 256) * FG::BB + 1023) / 1024;
+    if (a.gamma) {  // (K <= 3072: round 0 of the fill holds the whole row)
+        if (!x32) return hipErrorNotSupported;
+        if (need <= 6) return launch_gate_up_t<FG, true, 6, true>(a, x32, xk, s);
+        if (need <= 7) return launch_gate_up_t<FG, true, 7, true>(a, x32, xk, s);
+        return launch_gate_up_t<FG, true, 9, true>(a, x32, xk, s);
+    }
     if (x32) {
         if (need <= 6) return launch_gate_up_t<FG, true, 6>(a, x32, xk, s);
         if (need <= 7) return launch_gate_up_t<FG, true, 7>(a, x32, xk, s);

@@ -514,24 +514,8 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     __builtin_amdgcn_sched_barrier(0);
     // 2. the activations into LDS, once
     if constexpr (RMS) {
-        // the sum of squares over the lane's 16 values of round 0 (K <= 4096:
-        // the whole row), duplicates of the last chunk left out
         __shared__ float rms_part[4];
-        float ss = 0.0f;
-        if (x_has(0, K) && 4 * (int(threadIdx.x) >> 6) + ((int(threadIdx.x) >> 4) & 3) < (K >> 8)) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                ss = rms_add4(ss, make_float4(round_to_fp16(xp.v[i].x), round_to_fp16(xp.v[i].y),
-                                              round_to_fp16(xp.v[i].z), round_to_fp16(xp.v[i].w)));
-        }
-        const float inv_rms = rms_inv(ss, K, rms_part);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {  // y = fp16((x * inv_rms) * fp16(gamma)), E:4301
-            xp.v[i].x = round_to_fp16(round_to_fp16(xp.v[i].x) * inv_rms * round_to_fp16(gp.v[i].x));
-            xp.v[i].y = round_to_fp16(round_to_fp16(xp.v[i].y) * inv_rms * round_to_fp16(gp.v[i].y));
-            xp.v[i].z = round_to_fp16(round_to_fp16(xp.v[i].z) * inv_rms * round_to_fp16(gp.v[i].z));
-            xp.v[i].w = round_to_fp16(round_to_fp16(xp.v[i].w) * inv_rms * round_to_fp16(gp.v[i].w));
-        }
+        rms_fill_transform(xp, gp, K, rms_part);
     }
     if constexpr (X16) x16_fill<q80, std::is_same_v<F, FmtQ6K4>>(x16q, K, act);
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);

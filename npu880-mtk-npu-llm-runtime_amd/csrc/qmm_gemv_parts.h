@@ -263,6 +263,31 @@ __device__ inline void x_load(const float *__restrict__ x, int K, int c, XPre &p
     p.v[3] = q[3];
 }
 
+// The batch-1 fill on the row before its RMSNorm (K <= 4096: round 0 holds
+// the whole row): the workgroup's sum of squares in the fill's layout
+// (rms_inv; duplicates of the last chunk left out), then the lane's values
+// become y = fp16((fp16(x) * inv_rms) * fp16(gamma)) (E:4301), the values
+// rmsnorm_q8k_kernel forms. gp: the lane's gamma values, loaded as x_load
+// loads x. Every wave of the workgroup calls it (a workgroup barrier).
+__device__ inline void rms_fill_transform(XPre &xp, const XPre &gp, int K, float *part) {
+    const int wid = int(threadIdx.x) >> 6;
+    float ss = 0.0f;
+    if (x_has(0, K) && 4 * wid + ((int(threadIdx.x) >> 4) & 3) < (K >> 8)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ss = rms_add4(ss, make_float4(round_to_fp16(xp.v[i].x), round_to_fp16(xp.v[i].y),
+                                          round_to_fp16(xp.v[i].z), round_to_fp16(xp.v[i].w)));
+    }
+    const float inv_rms = rms_inv(ss, K, part);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        xp.v[i].x = round_to_fp16(round_to_fp16(xp.v[i].x) * inv_rms * round_to_fp16(gp.v[i].x));
+        xp.v[i].y = round_to_fp16(round_to_fp16(xp.v[i].y) * inv_rms * round_to_fp16(gp.v[i].y));
+        xp.v[i].z = round_to_fp16(round_to_fp16(xp.v[i].z) * inv_rms * round_to_fp16(gp.v[i].z));
+        xp.v[i].w = round_to_fp16(round_to_fp16(xp.v[i].w) * inv_rms * round_to_fp16(gp.v[i].w));
+    }
+}
+
 // Quantize the lane's 16 values of chunk c into the LDS row: Q8_K
 // (quantize_row_fp16_to_q8_k, E:925-990) or Q8_0 (E:1016-1064), after
 // rounding each value to fp16. `store` is false for clamped duplicates.

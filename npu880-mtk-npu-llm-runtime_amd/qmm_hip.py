@@ -90,6 +90,7 @@ _SIGNATURES = [
     ("qmm_swiglu_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_rmsnorm_q8k", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, _p]),
     ("qmm_ffn_block", C.c_int, [_p, _p, _p, C.c_int, _p, _p, _p, _p]),
+    ("qmm_ffn_block_rmsnorm", C.c_int, [_p, _p, _p, C.c_int, _p, _p, _p, _p]),
     ("qmm_gguf_open", C.c_int, [C.c_char_p, _p]),
     ("qmm_gguf_close", C.c_int, [_p]),
     ("qmm_gguf_header", C.c_int, [_p, _p, _p, _p, _p]),
@@ -430,6 +431,14 @@ class Context:
         dn = self._tasks(1, down.cols, [down])
         self._call("qmm_ffn_block", self._h, _p(_addr(x)), _p(_addr(q8k)), K, C.byref(gu[0]), C.byref(gu[1]),
                    C.byref(dn[0]), _p(_addr(h_out)))
+
+    def ffn_block_rmsnorm(self, x, gamma, K: int, gate: MatrixTask, up: MatrixTask, down: MatrixTask,
+                          h_out=None):
+        """qmm_ffn_block_rmsnorm: the block on x (fp32 [K]) after its RMSNorm with gamma."""
+        gu = self._tasks(1, K, [gate, up])
+        dn = self._tasks(1, down.cols, [down])
+        self._call("qmm_ffn_block_rmsnorm", self._h, _p(_addr(x)), _p(_addr(gamma)), K, C.byref(gu[0]),
+                   C.byref(gu[1]), C.byref(dn[0]), _p(_addr(h_out)))
 
     def dequantize_f16(self, w, type_id: int, rows: int, cols: int, dst):
         self._call("qmm_dequantize_f16", self._h, _p(_addr(w)), type_id, rows, cols, _p(_addr(dst)))

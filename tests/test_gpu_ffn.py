@@ -202,3 +202,33 @@ def test_ffn_block_graph_replays(ctx):
         _same(blk.read(got), ref)
     ctx.graph_destroy(gr)
     blk.free()
+
+
+@pytest.mark.parametrize("case", [
+    # K, F, H, gate/up type, down type, residual
+    (2560, 9728, 2560, TYPE_Q4_K, TYPE_Q6_K, True),            # the model's block: the norm in the gate/up fill
+    (3072, 12288, 3072, qmm_hip.TYPE_Q5_K, TYPE_Q4_K, False),  # Q5_K gate/up at K = 3072
+    (2560, 4096, 1000, TYPE_Q4_K, TYPE_Q6_K, True),            # down too short: the norm's kernel, three steps
+    (4096, 4096, 2560, TYPE_Q4_K, TYPE_Q6_K, False),           # K past the fill: the norm's kernel, three steps
+], ids=["model", "q5k_k3072", "three_steps", "k4096_three_steps"])
+def test_ffn_block_rmsnorm(ctx, oracle, case):
+    """qmm_ffn_block_rmsnorm equals qmm_rmsnorm_q8k followed by qmm_ffn_block
+    on that prequantized row, bit for bit (gate, up, h, down)."""
+    K, F, H, tg, td, residual = case
+    say(f"ffn block rmsnorm K={K} F={F} H={H}")
+    f = _Ffn(ctx, K, F, H, tg, td, seed=90 + K + F, residual=residual)
+    gamma = np.random.default_rng(K + F).uniform(0.5, 1.5, K).astype(np.float32)
+    gb = ctx.upload(gamma)
+    f.bufs.append(gb)
+    g, u, h, y = f.out()
+    tg_, tu_, td_ = f.tasks(g, u, y)
+    ctx.ffn_block_rmsnorm(f.xb, gb, K, tg_, tu_, td_, h)
+    nq = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, K))
+    f.bufs.append(nq)
+    ctx.rmsnorm_q8k(f.xb, gb, 1, K, None, nq)
+    g2, u2, h2, y2 = f.out()
+    tg2, tu2, td2 = f.tasks(g2, u2, y2)
+    ctx.ffn_block(None, nq, K, tg2, tu2, td2, h2)
+    ctx.sync()
+    _same(f.read((g, u, h, y)), f.read((g2, u2, h2, y2)))
+    f.free()
