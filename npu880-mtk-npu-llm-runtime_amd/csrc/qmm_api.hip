@@ -344,6 +344,7 @@ struct PendingStep {
     int c = 0;
     void *bufs[2] = {nullptr, nullptr};
     int launches = 0;  // the scan's launches so far: consecutive ones alternate buffers
+    bool seed = false;  // the next launch is the scan's first and seeds its state (no init launch)
 };
 
 int launch_pending(qmm_context *ctx, PendingStep &pend, float *best_val, uint32_t *best_id, const qmm::ScanStep &st,
@@ -383,9 +384,17 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
         if (pend->on)
             pre = qmm::PrevStep{pend->part, pend->nparts, pend->row_base, pend->thresh, pend->checkpoint ? 1 : 0,
                                 pend->c, best_val, best_id, scan};
+        const bool seed = pend->seed;  // (then the state is not read: it is this launch's to write)
+        if (seed) {
+            pre.best_val = best_val;
+            pre.best_id = best_id;
+            pre.st = scan;
+            pre.init = 1;
+            pend->seed = false;
+        }
         int nparts = 0;
-        e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, scan), xk, x0, round16, ids, id_limit, mine, &nparts,
-                                    ctx->stream, pre);
+        e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, seed ? nullptr : scan), xk, x0, round16, ids, id_limit,
+                                    mine, &nparts, ctx->stream, pre);
         if (e == hipSuccess) {
             pend->on = true;
             pend->part = mine;
@@ -396,7 +405,7 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
             pend->c = step->c;
             return QMM_OK;
         }
-        if (e != hipErrorNotSupported) return hip_fail(ctx, e, "GEMV + argmax launch");
+        if (e != hipErrorNotSupported || seed) return hip_fail(ctx, e, "GEMV + argmax launch");
         int rc = launch_pending(ctx, *pend, best_val, best_id, *step, scan);
         if (rc) return rc;
     } else if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
@@ -980,8 +989,26 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
     float *cdot = reinterpret_cast<float *>(scr + cand_b);
     uint8_t *work = scr + cand_b + cdot_b;
     const uint8_t *wb = static_cast<const uint8_t *>(w_lm);
-    hipError_t e = qmm::launch_scan_init(M, best_val, best_id, cand, scan_state, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "scan init launch");
+    PendingStep pend;
+    // At batch 1 with nothing evaluated ahead of the chunks, the first chunk's
+    // launch seeds the scan's state (where it takes the fused argmax grid)
+    // instead of a launch of its own.
+    hipError_t e;
+    {
+        qmm_matrix_task t0 = tc;
+        t0.rows = int(std::min<int64_t>(int64_t(groups[0].second + 1) * params->chunk_rows, vocab_rows));
+        qmm::Q8KView xk;
+        qmm::Q80View x0;
+        act_views(q8k, q80, 1, K, xk, x0);
+        int np = 0;
+        pend.seed = M == 1 && n_pre == 0 &&
+                    qmm::launch_gemv_argmax(t0.type, mat_args(t0, 1, K), xk, x0, true, nullptr, 0u, nullptr, &np,
+                                            ctx->stream, qmm::PrevStep{}, false) == hipSuccess;
+    }
+    if (!pend.seed) {
+        e = qmm::launch_scan_init(M, best_val, best_id, cand, scan_state, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "scan init launch");
+    }
     // the rows every position evaluates first (end-of-text rows), fp32, in list order (E:11143-11146)
     if (n_pre > 0 && (rc = lm_argmax_run(ctx, q8k, q80, M, K, tp, 0, pre_ids, uint32_t(vocab_rows), nullptr, best_val,
                                          best_id, work, nullptr, nullptr)))
@@ -998,7 +1025,6 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
     }
     // the chunks (E:11158-11257), a launch per group: each does nothing once
     // the scan has stopped
-    PendingStep pend;
     pend.bufs[0] = work + lm_scratch(M, chunk, rb, false, false).total();
     pend.bufs[1] = static_cast<uint8_t *>(pend.bufs[0]) + part_b;
     qmm::ScanStep last{};

@@ -447,9 +447,19 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     const int stride = nwg * 4;
     // 0. a scan's step after the previous chunk (the partials are requested
     // ahead of the activations; the decision precedes every weight request,
-    // so a chunk the step stops reads no weights)
+    // so a chunk the step stops reads no weights). The scan's first launch
+    // at batch 1 seeds its state instead (E:11138-11141): nothing in this
+    // launch reads it, the next launch does.
     Best pb4[4];
     if constexpr (AMAX) {
+        if (am.pre.init && wgi == 0 && threadIdx.x == 0) {
+            am.pre.best_val[0] = -1e30f;
+            am.pre.best_id[0] = 0;
+            am.pre.st[kScanChunks] = 0;
+            am.pre.st[kScanActive] = 1;
+            am.pre.st[kScanStopped] = 0;
+            am.pre.st[kScanPad] = 0;
+        }
         if (am.pre.part) {
             const Best *pp = static_cast<const Best *>(am.pre.part);
 #pragma unroll
@@ -922,7 +932,7 @@ static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, cons
 template <class F, int U>
 static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                                        const uint32_t *ids, uint32_t id_limit, void *part, int *nparts,
-                                       hipStream_t s, const PrevStep &pre) {
+                                       hipStream_t s, const PrevStep &pre, bool launch) {
     constexpr int R = kGemvR;
     const int nb = a.K / F::QK, cus = cu_count();
     const int wg0 = ((a.N + R - 1) / R + 3) / 4;
@@ -930,17 +940,18 @@ static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, cons
     const int wgs = persist_grid(wg0, cus);
     if (wgs > kMaxArgmaxParts || (pre.part && pre.nparts > 1024)) return hipErrorNotSupported;
     *nparts = wgs;
+    if (!launch) return hipSuccess;
     return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
                                                 AmaxOut{part, round16 ? 1 : 0, ids, id_limit, pre});
 }
 
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                               const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
-                              const PrevStep &pre) {
+                              const PrevStep &pre, bool launch) {
     switch (type) {
-        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
-        case kQ5_K: return launch_gemv_argmax_t<FmtQ5K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
-        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre);
+        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
+        case kQ5_K: return launch_gemv_argmax_t<FmtQ5K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
+        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
         default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
     }
 }
