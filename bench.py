@@ -572,9 +572,32 @@ def bench_lm_head(ctx, args):
         res[label] = {"us": round(ms_s * 1e3, 2), "chunks_read": chunks, "stopped_early": bool(state[2]),
                       "best_row": best, "weight_bytes_read": read, "gbs_effective": round(gbs(read, ms_s), 1)}
         log(f"LM-head scan {label}: {res[label]}")
+    # the early-exit scan behind the final RMSNorm: gamma = the row's rms, so the normed row is the row
+    # (to fp16 rounding) and the planted row still ends the scan after chunk 0
+    xr = a.host[0:1].astype(np.float32)
+    xb = ctx.upload(xr)
+    gm = ctx.upload(np.full(K, np.sqrt(np.mean(xr.astype(np.float64) ** 2) + 1e-6), np.float32))
+    qn = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, K))
+
+    def norm_then_scan(i):
+        ctx.rmsnorm_q8k(xb, gm, 1, K, None, qn)
+        ctx.lm_head_scan(qn, None, 1, K, S.ptr(i), synth.TYPE_Q6_K, N, 24832, thresholds=CHUNK_THRESH, best_val=bv,
+                         best_id=bi, scan_state=st)
+
+    def scan_rmsnorm(i):
+        ctx.lm_head_scan_rmsnorm(xb, gm, 1, K, S.ptr(i), synth.TYPE_Q6_K, N, 24832, thresholds=CHUNK_THRESH,
+                                 best_val=bv, best_id=bi, scan_state=st)
+
+    nres = {}
+    for label, fn in (("us_norm_then_scan", norm_then_scan), ("us_scan_rmsnorm", scan_rmsnorm)):
+        ms_s, _ = timed(ctx, fn, max(50, args.steps // 20), 3, S.R)
+        nres[label] = round(ms_s * 1e3, 2)
+        nres[label.replace("us_", "chunks_read_")] = int(ctx.d2h(st, np.int32, (4,))[0])
+    log(f"LM-head scan early_exit behind the final norm: {nres}")
+    res["early_exit_behind_final_rmsnorm"] = nres
     lm["scan_151936_chunks_24832"] = res
     S.free()
-    for b in (bv, bi, st):
+    for b in (bv, bi, st, xb, gm, qn):
         ctx.free(b)
     a.free()
     return lm

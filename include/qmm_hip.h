@@ -245,6 +245,21 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
                      const uint32_t *draft_ids, float *best_val, uint32_t *best_id,
                      int32_t *scan_state);
 
+/* run_final_norm_and_lm_head_batch_sdot whole: its final RMSNorm of the rows
+ * x [M][K] with gamma (rmsnorm_fp16_rows_fast, E:11129), then the scan above
+ * on the normed rows — the pair qmm_rmsnorm_q8k + qmm_lm_head_scan in one
+ * call, with the same results. At M = 1 with no pre_ids and every chunk
+ * launch of a Q4_K / Q5_K / Q6_K tensor on the batch-1 persistent grid,
+ * each chunk launch normalizes the row in its activation fill (no launch of
+ * the norm's own); otherwise the norm's kernel writes the context's buffers
+ * (and, for a Q8_0 tensor, the normed row's Q8_0) first. K % 256 == 0,
+ * K <= 16384; x and gamma 16-B aligned. */
+int qmm_lm_head_scan_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int M, int K,
+                             const void *w_lm, uint32_t type, int vocab_rows,
+                             const qmm_lm_scan_params *params, const uint32_t *pre_ids, int n_pre,
+                             const uint32_t *draft_ids, float *best_val, uint32_t *best_id,
+                             int32_t *scan_state);
+
 /* -------------------------------------------------------------- dequant */
 /* dequant_contiguous_fast (E:3856-3902): rows x cols packed blocks -> fp16
  * bits [rows][cols] (for validation; not on the matmul path). F16 rows are

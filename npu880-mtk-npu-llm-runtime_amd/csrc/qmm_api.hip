@@ -345,6 +345,8 @@ struct PendingStep {
     void *bufs[2] = {nullptr, nullptr};
     int launches = 0;  // the scan's launches so far: consecutive ones alternate buffers
     bool seed = false;  // the next launch is the scan's first and seeds its state (no init launch)
+    const float *x32 = nullptr;    // non-null: every chunk launch takes this row before its RMSNorm
+    const float *gamma = nullptr;  // (the norm's weights)
 };
 
 int launch_pending(qmm_context *ctx, PendingStep &pend, float *best_val, uint32_t *best_id, const qmm::ScanStep &st,
@@ -394,7 +396,7 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
         }
         int nparts = 0;
         e = qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K, seed ? nullptr : scan), xk, x0, round16, ids, id_limit,
-                                    mine, &nparts, ctx->stream, pre);
+                                    mine, &nparts, ctx->stream, pre, true, pend->x32, pend->gamma);
         if (e == hipSuccess) {
             pend->on = true;
             pend->part = mine;
@@ -405,7 +407,7 @@ int lm_argmax_run(qmm_context *ctx, const void *q8k, const void *q80, int M, int
             pend->c = step->c;
             return QMM_OK;
         }
-        if (e != hipErrorNotSupported || seed) return hip_fail(ctx, e, "GEMV + argmax launch");
+        if (e != hipErrorNotSupported || seed || pend->x32) return hip_fail(ctx, e, "GEMV + argmax launch");
         int rc = launch_pending(ctx, *pend, best_val, best_id, *step, scan);
         if (rc) return rc;
     } else if (M == 1) {  // the GEMV's persistent grid reduces to one partial per workgroup
@@ -936,10 +938,15 @@ int qmm_eval_rows_argmax(qmm_context *ctx, const void *q8k, const void *q80, int
                      best_id);
 }
 
-int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_lm,
-                     uint32_t type, int vocab_rows, const qmm_lm_scan_params *params, const uint32_t *pre_ids,
-                     int n_pre, const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int32_t *scan_state) {
-    if (!ctx) return QMM_EINVAL;
+// The scan over quantized activations (q8k / q80), or, with x32, over the
+// row before its RMSNorm (gamma): at batch 1 with nothing evaluated ahead of
+// the chunks and every chunk launch on the fused argmax grid, each launch
+// normalizes the row in its fill; otherwise the norm's own kernel first
+// writes q8k (and, for a Q8_0 tensor, y and q80).
+static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const float *x32, const float *gamma, float *y,
+                   int M, int K, const void *w_lm, uint32_t type, int vocab_rows, const qmm_lm_scan_params *params,
+                   const uint32_t *pre_ids, int n_pre, const uint32_t *draft_ids, float *best_val, uint32_t *best_id,
+                   int32_t *scan_state) {
     if (!params || !best_val || !best_id || !scan_state || vocab_rows <= 0 || M <= 0 || n_pre < 0 ||
         (n_pre > 0 && !pre_ids))
         return fail(ctx, QMM_EINVAL, "bad LM-head scan arguments");
@@ -995,15 +1002,29 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
     // instead of a launch of its own.
     hipError_t e;
     {
-        qmm_matrix_task t0 = tc;
-        t0.rows = int(std::min<int64_t>(int64_t(groups[0].second + 1) * params->chunk_rows, vocab_rows));
         qmm::Q8KView xk;
         qmm::Q80View x0;
         act_views(q8k, q80, 1, K, xk, x0);
-        int np = 0;
-        pend.seed = M == 1 && n_pre == 0 &&
-                    qmm::launch_gemv_argmax(t0.type, mat_args(t0, 1, K), xk, x0, true, nullptr, 0u, nullptr, &np,
-                                            ctx->stream, qmm::PrevStep{}, false) == hipSuccess;
+        auto fused = [&](const std::pair<int, int> &gr, const float *g) {
+            qmm_matrix_task t = tc;
+            const int r0 = gr.first * params->chunk_rows;
+            t.rows = int(std::min<int64_t>(int64_t(gr.second + 1) * params->chunk_rows, vocab_rows) - r0);
+            int np = 0;
+            return qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K), xk, x0, true, nullptr, 0u, nullptr, &np,
+                                           ctx->stream, qmm::PrevStep{}, false, x32, g) == hipSuccess;
+        };
+        pend.seed = M == 1 && n_pre == 0 && fused(groups[0], nullptr);
+        bool normed = x32 && pend.seed;
+        for (size_t i = 0; i < groups.size() && normed; ++i) normed = fused(groups[i], gamma);
+        if (normed) {
+            pend.x32 = x32;
+            pend.gamma = gamma;
+        } else if (x32) {  // the norm's own launch, into q8k (and y, q80 for a Q8_0 tensor)
+            e = qmm::launch_rmsnorm_q8k(x32, gamma, M, K, q80 ? y : nullptr, const_cast<void *>(q8k), ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+            if (q80 && (e = qmm::launch_quantize_q8_0(y, M, K, const_cast<void *>(q80), ctx->stream)) != hipSuccess)
+                return hip_fail(ctx, e, "quantize_q8_0 launch");
+        }
     }
     if (!pend.seed) {
         e = qmm::launch_scan_init(M, best_val, best_id, cand, scan_state, ctx->stream);
@@ -1048,6 +1069,38 @@ int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, 
             return rc;
     }
     return launch_pending(ctx, pend, best_val, best_id, last, scan_state);
+}
+
+int qmm_lm_head_scan(qmm_context *ctx, const void *q8k, const void *q80, int M, int K, const void *w_lm,
+                     uint32_t type, int vocab_rows, const qmm_lm_scan_params *params, const uint32_t *pre_ids,
+                     int n_pre, const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int32_t *scan_state) {
+    if (!ctx) return QMM_EINVAL;
+    return lm_scan(ctx, q8k, q80, nullptr, nullptr, nullptr, M, K, w_lm, type, vocab_rows, params, pre_ids, n_pre,
+                   draft_ids, best_val, best_id, scan_state);
+}
+
+int qmm_lm_head_scan_rmsnorm(qmm_context *ctx, const float *x, const float *gamma, int M, int K, const void *w_lm,
+                             uint32_t type, int vocab_rows, const qmm_lm_scan_params *params,
+                             const uint32_t *pre_ids, int n_pre, const uint32_t *draft_ids, float *best_val,
+                             uint32_t *best_id, int32_t *scan_state) {
+    if (!ctx) return QMM_EINVAL;
+    if (!x || !gamma) return fail(ctx, QMM_EINVAL, "null x or gamma");
+    if (M <= 0 || K <= 0) return fail(ctx, QMM_EINVAL, "bad LM-head scan arguments");
+    if (K % 256) return fail(ctx, QMM_ESHAPE, "K must be a multiple of 256");
+    if (K > 16384) return fail(ctx, QMM_ESHAPE, "K above 16384");
+    if (!aligned(x, 16) || !aligned(gamma, 16)) return fail(ctx, QMM_EALIGN, "x and gamma must be 16-B aligned");
+    int rc = use_device(ctx);
+    if (rc) return rc;
+    // the norm's output buffers, for the scans that take the norm's own launch
+    const bool q80 = type == QMM_TYPE_Q8_0;
+    const size_t k_bytes = qmm::Q8KLayout(M, K).total;
+    const size_t y_bytes = q80 ? align256(size_t(M) * size_t(K) * 4) : 0;
+    const size_t z_bytes = q80 ? qmm::Q80Layout(M, K).total : 0;
+    if ((rc = ensure_act(ctx, k_bytes + y_bytes + z_bytes))) return rc;
+    uint8_t *base = static_cast<uint8_t *>(ctx->act);
+    return lm_scan(ctx, base, q80 ? base + k_bytes + y_bytes : nullptr, x, gamma,
+                   q80 ? reinterpret_cast<float *>(base + k_bytes) : nullptr, M, K, w_lm, type, vocab_rows, params,
+                   pre_ids, n_pre, draft_ids, best_val, best_id, scan_state);
 }
 
 int qmm_graph_begin(qmm_context *ctx) {

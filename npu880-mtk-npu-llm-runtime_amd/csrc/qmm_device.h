@@ -215,7 +215,8 @@ struct AmaxOut {
 };
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                               const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
-                              const PrevStep &pre = PrevStep{}, bool launch = true);
+                              const PrevStep &pre = PrevStep{}, bool launch = true, const float *x32 = nullptr,
+                              const float *gamma = nullptr);
 hipError_t launch_argmax_final(const void *part, int nparts, const uint32_t *ids, uint32_t row_base,
                                float *best_val, uint32_t *best_id, const int32_t *st, hipStream_t s);
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,

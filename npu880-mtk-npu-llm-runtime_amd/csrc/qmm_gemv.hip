@@ -401,7 +401,7 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
                                                                       Q8KView prek, Q80View pre0, AmaxOut am,
                                                                       int wgi, int nwg,
                                                                       const float *__restrict__ gamma = nullptr) {
-    static_assert(!RMS || (FUSED && !X16 && !AMAX), "the RMSNorm fill takes an fp32 row");
+    static_assert(!RMS || (FUSED && !X16), "the RMSNorm fill takes an fp32 row");
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
@@ -721,6 +721,16 @@ __global__ __launch_bounds__(256) void gemv_persist_rms_kernel(MatArgs a, const 
                                                                int(blockIdx.x), int(gridDim.x), gamma);
 }
 
+// The running argmax GEMV on the row before its RMSNorm (the LM head behind
+// the final norm, run_final_norm_and_lm_head_batch_sdot): every workgroup
+// normalizes and quantizes the row in its fill, as gemv_persist_rms_kernel.
+template <class F, int NC>
+__global__ __launch_bounds__(256) void gemv_argmax_rms_kernel(MatArgs a, const float *__restrict__ x32,
+                                                              const float *__restrict__ gamma, AmaxOut am) {
+    gemv_persist_wg<F, kGemvR, 3, true, NC, true, false, true>(a, x32, Q8KView{}, Q80View{}, am, int(blockIdx.x),
+                                                              int(gridDim.x), gamma);
+}
+
 
 // ------------------------------------------- 2..4 tokens, batch-1 shape
 // The persistent kernel's structure for 2 <= M <= MT <= 4 tokens on a
@@ -929,29 +939,48 @@ static hipError_t launch_gemv_persist_t(const MatArgs &a, const float *x32, cons
 
 // The persistent grid of one task (R = kGemvR) with the running argmax
 // fused; NotSupported (nothing launched) where that grid does not apply.
+// Below two workgroups per CU the grid is one workgroup per four row groups
+// (each wave's first group is its only one; the waves past the last group
+// stage the last group's bytes and hold no rows). gamma: x32 is the row
+// before its RMSNorm, normalized and quantized in every workgroup's fill.
 template <class F, int U>
 static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                                        const uint32_t *ids, uint32_t id_limit, void *part, int *nparts,
-                                       hipStream_t s, const PrevStep &pre, bool launch) {
+                                       hipStream_t s, const PrevStep &pre, bool launch, const float *x32,
+                                       const float *gamma) {
     constexpr int R = kGemvR;
     const int nb = a.K / F::QK, cus = cu_count();
     const int wg0 = ((a.N + R - 1) / R + 3) / 4;
-    if (a.N < (IsQ80<F>::v ? 8192 : 4096) || R * nb > (64 / F::G) * U || wg0 < 2 * cus) return hipErrorNotSupported;
-    const int wgs = persist_grid(wg0, cus);
+    if (R * nb > (64 / F::G) * U || (gamma && !x32)) return hipErrorNotSupported;
+    const int wgs = wg0 < 2 * cus ? wg0 : persist_grid(wg0, cus);
     if (wgs > kMaxArgmaxParts || (pre.part && pre.nparts > 1024)) return hipErrorNotSupported;
     *nparts = wgs;
     if (!launch) return hipSuccess;
-    return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, gemv_lds_bytes_t<F, R, U>(a.K), wgs, s,
-                                                AmaxOut{part, round16 ? 1 : 0, ids, id_limit, pre});
+    const AmaxOut am{part, round16 ? 1 : 0, ids, id_limit, pre};
+    const size_t lds = gemv_lds_bytes_t<F, R, U>(a.K);
+    if (gamma)
+        return with_stage_chunks<F, U>(R * nb, [&](auto nc) {
+            constexpr int NC = decltype(nc)::value;
+            hipLaunchKernelGGL((gemv_argmax_rms_kernel<F, NC>), dim3(unsigned(wgs)), dim3(256), lds, s, a, x32, gamma,
+                               am);
+            return hipGetLastError();
+        });
+    return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, lds, wgs, s, am);
 }
 
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                               const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
-                              const PrevStep &pre, bool launch) {
+                              const PrevStep &pre, bool launch, const float *x32, const float *gamma) {
     switch (type) {
-        case kQ4_K: return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
-        case kQ5_K: return launch_gemv_argmax_t<FmtQ5K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
-        case kQ6_K: return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch);
+        case kQ4_K:
+            return launch_gemv_argmax_t<FmtQ4K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch, x32,
+                                                    gamma);
+        case kQ5_K:
+            return launch_gemv_argmax_t<FmtQ5K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch, x32,
+                                                    gamma);
+        case kQ6_K:
+            return launch_gemv_argmax_t<FmtQ6K4, 3>(a, xk, x0, round16, ids, id_limit, part, nparts, s, pre, launch, x32,
+                                                    gamma);
         default: return hipErrorNotSupported;  // Q8_0 takes the persistent grid only at K <= 320
     }
 }

@@ -104,6 +104,8 @@ _SIGNATURES = [
                                        _p, _p, _p]),
     ("qmm_lm_head_scan", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int,
                                    C.POINTER(LmScanParams), _p, C.c_int, _p, _p, _p, _p]),
+    ("qmm_lm_head_scan_rmsnorm", C.c_int, [_p, _p, _p, C.c_int, C.c_int, _p, C.c_uint32, C.c_int,
+                                           C.POINTER(LmScanParams), _p, C.c_int, _p, _p, _p, _p]),
     ("qmm_dequantize_f16", C.c_int, [_p, _p, C.c_uint32, C.c_int64, C.c_int64, _p]),
     ("qmm_gemm_multi_dispatch", C.c_int, [_p, _p, C.c_int, C.c_int, C.POINTER(_Task), C.c_int]),
     ("qmm_gemm_multi_dispatch_prequantized", C.c_int,
@@ -420,6 +422,17 @@ class Context:
         self._call("qmm_lm_head_scan", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_lm)), type_id,
                    vocab_rows, C.byref(prm), _p(_addr(pre_ids)), n_pre, _p(_addr(draft_ids)), _p(_addr(best_val)),
                    _p(_addr(best_id)), _p(_addr(scan_state)))
+
+    def lm_head_scan_rmsnorm(self, x, gamma, M: int, K: int, w_lm, type_id: int, vocab_rows: int, chunk_rows: int,
+                             thresholds=None, first_checkpoint: int = 0, prune_margin: float = 1e-3, pre_ids=None,
+                             n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None):
+        """qmm_lm_head_scan_rmsnorm: the final RMSNorm of x with gamma, then the chunked vocabulary scan."""
+        thr = None if thresholds is None else (C.c_float * len(thresholds))(*[float(t) for t in thresholds])
+        prm = LmScanParams(chunk_rows, thr if thr is not None else None, 0 if thr is None else len(thresholds),
+                           first_checkpoint, prune_margin)
+        self._call("qmm_lm_head_scan_rmsnorm", self._h, _p(_addr(x)), _p(_addr(gamma)), M, K, _p(_addr(w_lm)),
+                   type_id, vocab_rows, C.byref(prm), _p(_addr(pre_ids)), n_pre, _p(_addr(draft_ids)),
+                   _p(_addr(best_val)), _p(_addr(best_id)), _p(_addr(scan_state)))
 
     def swiglu_q8k(self, gate, up, M: int, N: int, h_out, out):
         self._call("qmm_swiglu_q8k", self._h, _p(_addr(gate)), _p(_addr(up)), M, N,

@@ -296,3 +296,87 @@ def test_scan_tall_chunks_batch1(ctx, oracle, case):
         got, exp = _scan(ctx, oracle, 1, 993, [(4 * CH2 + 9, 0, 40.0)], None, V=V2, CH=CH2)
         _same(got, exp, 5, 1, 0)
         assert int(got[1][0]) == 4 * CH2 + 9
+
+
+# ------------------------------------------- the scan behind the final norm
+def _scan_rmsnorm(ctx, oracle, M, seed, plan, thresholds, first_checkpoint=0, pre=None, draft=None, V=V, CH=CH):
+    """qmm_lm_head_scan_rmsnorm against qmm_rmsnorm_q8k followed by
+    qmm_lm_head_scan on its output: (best, id, state) bit-identical, and the
+    two-step result against the oracle's scan of that Q8_K row. The plan's
+    rows are planted against the normed row."""
+    K = 2560
+    x = synth.activations(M, K, seed=seed + 1)
+    gamma = np.random.default_rng(seed + 2).uniform(0.5, 1.5, K).astype(np.float32)
+    xb, gb = ctx.upload(x), ctx.upload(gamma)
+    qb = ctx.malloc(ctx.lib.qmm_q8k_bytes(M, K))
+    ctx.rmsnorm_q8k(xb, gb, M, K, None, qb)
+    ctx.sync()
+    q = ctx.read_q8k(qb, M, K)
+    w = lm_plant.base_tensor(V + 16, K, seed)
+    lm_plant.plant(w, oracle, q, plan, K)
+    wb = ctx.weight_upload(w, TYPE_Q6_K, V + 16, K)
+    preb = ctx.upload(np.asarray(pre, np.uint32)) if pre is not None else None
+    drb = ctx.upload(np.asarray(draft, np.uint32)) if draft is not None else None
+    runs = []
+    for fused in (False, True):
+        bv, bi = ctx.malloc(M * 4), ctx.malloc(M * 4)
+        st = ctx.upload(np.full(4, -7, np.int32))
+        kw = dict(thresholds=thresholds, first_checkpoint=first_checkpoint, pre_ids=preb,
+                  n_pre=0 if pre is None else len(pre), draft_ids=drb, best_val=bv, best_id=bi, scan_state=st)
+        if fused:
+            ctx.lm_head_scan_rmsnorm(xb, gb, M, K, wb, TYPE_Q6_K, V, CH, **kw)
+        else:
+            ctx.lm_head_scan(qb, None, M, K, wb, TYPE_Q6_K, V, CH, **kw)
+        ctx.sync()
+        runs.append((ctx.d2h(bv, np.float32, (M,)), ctx.d2h(bi, np.uint32, (M,)), ctx.d2h(st, np.int32, (4,))))
+        for b in (bv, bi, st):
+            ctx.free(b)
+    exp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, thresholds, first_checkpoint, 1e-3, pre, draft)
+    for b in (xb, gb, qb, wb, preb, drb):
+        if b is not None:
+            ctx.free(b)
+    (sv, si, ss), (fv, fi, fs) = runs
+    assert np.array_equal(sv.view(np.uint32), fv.view(np.uint32)), (sv, fv)
+    assert np.array_equal(si, fi), (si, fi)
+    assert np.array_equal(ss, fs), (ss, fs)
+    return runs[0], exp
+
+
+@pytest.mark.parametrize("case", ["chunk0", "chunk2", "checkpoint3", "all", "short_tail", "small_chunks",
+                                  "pre_ids", "drafts"])
+def test_scan_rmsnorm(ctx, oracle, case):
+    """The scan behind its final norm in one call. Batch-1 cases without
+    pre-evaluated rows take the norm inside every chunk launch's fill (tall
+    chunks, a last chunk of 2944 rows, chunks of 4096 rows); pre-evaluated
+    rows and drafts take the norm's own launch first."""
+    T = lm_plant.CHUNK_THRESH
+    V2, CH2 = 60000, 12288
+    say(f"lm scan behind the final norm: {case}")
+    if case == "chunk0":
+        got, exp = _scan_rmsnorm(ctx, oracle, 1, 1010, [(5, 0, 25.0), (CH2 + 3, 0, 60.0)], T, V=V2, CH=CH2)
+        _same(got, exp, 1, 1, 1)
+    elif case == "chunk2":
+        _same(*_scan_rmsnorm(ctx, oracle, 1, 1011, [(2 * CH2 + 77, 0, 14.0)], T, V=V2, CH=CH2), 3, 1, 1)
+    elif case == "checkpoint3":
+        got, exp = _scan_rmsnorm(ctx, oracle, 1, 1012, [(5, 0, 25.0)], T, first_checkpoint=3, V=V2, CH=CH2)
+        _same(got, exp, 4, 1, 1)
+    elif case == "all":
+        got, exp = _scan_rmsnorm(ctx, oracle, 1, 1013, [(4 * CH2 + 9, 0, 40.0)], None, V=V2, CH=CH2)
+        _same(got, exp, 5, 1, 0)
+        assert int(got[1][0]) == 4 * CH2 + 9
+    elif case == "short_tail":  # chunk 4 holds 2944 rows, its maximum the last row
+        V3 = 4 * CH2 + 2944
+        got, exp = _scan_rmsnorm(ctx, oracle, 1, 1014, [(V3 - 1, 0, 9.0)], [30.0] * 4 + [-1e30], V=V3, CH=CH2)
+        _same(got, exp, 5, 1, 1)
+        assert int(got[1][0]) == V3 - 1
+    elif case == "small_chunks":
+        _same(*_scan_rmsnorm(ctx, oracle, 1, 1015, [(2 * CH + 77, 0, 14.0)], T), 3, 1, 1)
+    elif case == "pre_ids":
+        got, exp = _scan_rmsnorm(ctx, oracle, 1, 1016, [(V - 4, 0, 30.0)], T, pre=[V - 2, V - 4])
+        assert int(got[1][0]) == V - 4
+        _same(got, exp, *exp[2:])
+    else:
+        M = 3
+        plan = [(100, 0, 5.0), (1500, 0, 8.0)] + [(CH + 10 * p, p, 12.0) for p in range(1, M)]
+        got, exp = _scan_rmsnorm(ctx, oracle, M, 1017, plan, None, draft=[0, 100, 200])
+        _same(got, exp, 5, 1, 0)
