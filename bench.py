@@ -521,7 +521,8 @@ def bench_lm_head(ctx, args):
     GEMV, the GEMV with its argmax epilogue, and the chunked scan
     (24832-row chunks, chunk_thresh) on a tensor whose chunk 0 holds a row
     at logit 25 (the scan stops after chunk 0) against the same scan
-    without thresholds (all 7 chunks)."""
+    without thresholds and with a threshold at every chunk that no chunk
+    meets (all 7 chunks either way)."""
     N, K = synth.GEMV_Q6K_LMHEAD["N"], synth.GEMV_Q6K_LMHEAD["K"]
     rb = synth.row_bytes(synth.TYPE_Q6_K, K)
     a = Acts(ctx, 1, K, seed=21)
@@ -563,7 +564,8 @@ def bench_lm_head(ctx, args):
                                           best_val=bv, best_id=bi, scan_state=st)
 
     res = {}
-    for label, thr in (("early_exit", CHUNK_THRESH), ("all_chunks", None)):
+    for label, thr in (("early_exit", CHUNK_THRESH), ("all_chunks", None),
+                       ("all_chunks_thresholds_unmet", [1e30] * 7)):
         ms_s, _ = timed(ctx, scan(thr), max(50, args.steps // 20), 3, S.R)
         state = ctx.d2h(st, np.int32, (4,))
         best = int(ctx.d2h(bi, np.uint32, (1,))[0])

@@ -380,3 +380,24 @@ def test_scan_rmsnorm(ctx, oracle, case):
         plan = [(100, 0, 5.0), (1500, 0, 8.0)] + [(CH + 10 * p, p, 12.0) for p in range(1, M)]
         got, exp = _scan_rmsnorm(ctx, oracle, M, 1017, plan, None, draft=[0, 100, 200])
         _same(got, exp, 5, 1, 0)
+
+
+def test_scan_in_a_row(ctx, oracle):
+    """Batch-1 scans in a row on one context, each the oracle's: a stop after
+    chunk 0 (the later launches find the state stopped), all chunks, a stop
+    after chunk 2, a checkpoint at every chunk that none meets, chunks of
+    4095 and of 1024 rows (20 chunks), and a stop after chunk 0 again: every
+    scan seeds its own state, whatever the previous one left."""
+    T = lm_plant.CHUNK_THRESH
+    V2, CH2 = 60000, 12288
+    say("lm scan, scans in a row")
+    _same(*_scan(ctx, oracle, 1, 1020, [(5, 0, 25.0), (CH2 + 3, 0, 60.0)], T, V=V2, CH=CH2), 1, 1, 1)
+    got, exp = _scan(ctx, oracle, 1, 1021, [(4 * CH2 + 9, 0, 40.0)], None, V=V2, CH=CH2)
+    _same(got, exp, 5, 1, 0)
+    _same(*_scan(ctx, oracle, 1, 1022, [(2 * CH2 + 77, 0, 14.0)], T, V=V2, CH=CH2), 3, 1, 1)
+    got, exp = _scan(ctx, oracle, 1, 1023, [(3 * CH2 + 1, 0, 25.0)], [1e30] * 5, V=V2, CH=CH2)
+    _same(got, exp, 5, 1, 0)  # a checkpoint at every chunk, never met
+    assert int(got[1][0]) == 3 * CH2 + 1
+    _same(*_scan(ctx, oracle, 1, 1024, [(2 * 4095 + 7, 0, 14.0)], T, CH=4095), 3, 1, 1)
+    _same(*_scan(ctx, oracle, 1, 1025, [(2 * 1024 + 5, 0, 14.0)], T, CH=1024), 3, 1, 1)
+    _same(*_scan(ctx, oracle, 1, 1026, [(5, 0, 25.0)], T, V=V2, CH=CH2), 1, 1, 1)
