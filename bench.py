@@ -52,10 +52,30 @@ DIRECT = False  # --direct: launch steps one by one instead of replaying a HIP g
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmm_gemm_kernels_pmc.txt")
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_fused_9728x2560_pmc.txt")
 CHUNK_THRESH = [19.5, 16.0, 13.5, 11.5, 10.5, 10.0, 10.0, 10.0, 10.0, -1e30]  # chunk_thresh, E:11245
+SWEEP_MULTS = (1, 2, 4, 8)  # the size sweep: Q4_K GEMVs of 9728 * m rows x 2560
+SWEEP_GRIDS = ((512, 4), (1024, 4), (2048, 4), (512, 8), (1024, 8), (2048, 8))  # stream-read grids tried per size
+SWEEP_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_size_sweep_kernel_trace.txt")
+SWEEP_MARKER_BASE = 3000  # workgroups of the marker launch before sweep section i: 3000 + i
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def under_profiler():
+    """True when a ROCm profiler is attached to this process: its tool
+    library is mapped (rocprofv3 preloads it) or its environment is set.
+    Graph replays crashed the host process under rocprofv3 --kernel-trace
+    (a SIGSEGV below hipGraphLaunch), so such runs launch directly."""
+    if any(k.startswith(("ROCPROF", "ROCPROFILER")) for k in os.environ):
+        return True
+    if "rocprof" in os.environ.get("LD_PRELOAD", ""):
+        return True
+    try:
+        with open("/proc/self/maps") as f:
+            return any("rocprofiler" in ln or "rocprofv3" in ln or "roctracer" in ln for ln in f)
+    except OSError:
+        return False
 
 
 WARM_MS = 4.0  # untimed GPU work right before each timed graph: clocks at their steady state
@@ -260,6 +280,180 @@ def check_against_oracle(ctx, W, a, y):
     return {"norm_err": err, "bit_exact": exact}
 
 
+# ---------------------------------------------------------------- size sweep
+def fit_time(points):
+    """Least-squares T = t0 + bytes / BW over (bytes, us) points: the fixed
+    per-launch time t0 and the marginal rate BW of the bytes themselves."""
+    xs = np.array([p[0] for p in points], np.float64)
+    ys = np.array([p[1] for p in points], np.float64)
+    A = np.vstack([np.ones_like(xs), xs]).T
+    (t0, slope), *_ = np.linalg.lstsq(A, ys, rcond=None)
+    bw = 1.0 / (slope * 1e-6) / 1e9 if slope > 0 else float("inf")
+    return {"t0_us": round(float(t0), 3), "marginal_gbs": round(float(bw), 1),
+            "marginal_frac": round(float(bw / HBM_PEAK_GBS), 4),
+            "max_residual_us": round(float(np.abs(ys - (t0 + slope * xs)).max()), 3)}
+
+
+def sweep_weights(ctx, m, seed=0):
+    """The headline tensor's shape at 9728 * m rows (independent rows per
+    size), rotated over >= 512 MB of replicas."""
+    N, K = 9728 * m, 2560
+    return Replicated(ctx, synth.TYPE_Q4_K, N, K, 0, seed=seed + m)
+
+
+def bench_size_sweep(ctx, args):
+    """The fused Q4_K GEMV (the headline step) and the streaming-read floor
+    at 9728 x {1, 2, 4, 8} rows (K = 2560, rotated replicas), graph-timed as
+    the headline; T = t0 + bytes / BW fitted to each separates the fixed
+    per-launch cost t0 from the marginal rate of the bytes."""
+    K = 2560
+    a = Acts(ctx, 1, K, seed=1)
+    sink = ctx.malloc(4 * 8192)
+    steps = max(50, args.steps // 4)
+    gemv, stream = {}, {}
+    for m in SWEEP_MULTS:
+        W = sweep_weights(ctx, m)
+        N = W.N
+        y = ctx.malloc(N * 4)
+        ms, _ = timed(ctx, lambda i: ctx.gemm_multi_dispatch(a.x, 1, K, [W.task(i, y)]), steps, 10, W.R)
+        alg = N * 1440 + K * 4 + N * 4
+        best = None
+        for wgs, nl in SWEEP_GRIDS:
+            mss, _ = timed(ctx, lambda i: ctx.stream_read(W.ptr(i), W.bytes, wgs, nl, sink), steps, 10, W.R)
+            if best is None or mss < best[0]:
+                best = (mss, wgs, nl)
+        gemv[N] = {"us": round(ms * 1e3, 3), "algorithmic_bytes": alg, "gbs": round(gbs(alg, ms), 1)}
+        stream[N] = {"us": round(best[0] * 1e3, 3), "bytes": W.bytes, "gbs": round(gbs(W.bytes, best[0]), 1),
+                     "grid": f"{best[1]}x{best[2]}"}
+        log(f"size sweep N={N}: fused GEMV {gemv[N]['us']} us ({gemv[N]['gbs']} GB/s); "
+            f"stream read {stream[N]['us']} us ({stream[N]['gbs']} GB/s, {stream[N]['grid']})")
+        ctx.free(y)
+        W.free()
+    ctx.free(sink)
+    a.free()
+    out = {"K": K, "rows": list(gemv), "gemv_fused_q4k": gemv, "stream_read": stream,
+           "fit_gemv": fit_time([(v["algorithmic_bytes"], v["us"]) for v in gemv.values()]),
+           "fit_stream_read": fit_time([(v["bytes"], v["us"]) for v in stream.values()]),
+           "timing": "graph-timed, as the headline"}
+    log(f"size sweep fits: GEMV {out['fit_gemv']}, stream read {out['fit_stream_read']}")
+    return out
+
+
+def sweep_run(args):
+    """The size sweep launched directly, for rocprofv3 --kernel-trace: per
+    size, a marker launch (the streaming-read kernel on 3000 + 2i workgroups)
+    then 16 fused GEMVs; a marker (3000 + 2i + 1) then 16 launches of each
+    streaming-read grid, all over rotated replicas."""
+    ctx = qmm_hip.Context(0)
+    K = 2560
+    a = Acts(ctx, 1, K, seed=1)
+    sink = ctx.malloc(4 * 8192)
+    src = ctx.malloc(4096)
+    for i, m in enumerate(SWEEP_MULTS):
+        W = sweep_weights(ctx, m)
+        y = ctx.malloc(W.N * 4)
+        for s in range(W.R):  # every replica touched once before the traced launches
+            ctx.stream_read(W.ptr(s), W.bytes, 2048, 4, sink)
+        ctx.sync()
+        ctx.stream_read(src, 4096, SWEEP_MARKER_BASE + 2 * i, 1, sink)
+        for s in range(16):
+            ctx.gemm_multi_dispatch(a.x, 1, K, [W.task(s, y)])
+        ctx.sync()
+        ctx.stream_read(src, 4096, SWEEP_MARKER_BASE + 2 * i + 1, 1, sink)
+        for wgs, nl in SWEEP_GRIDS:
+            for s in range(16):
+                ctx.stream_read(W.ptr(s), W.bytes, wgs, nl, sink)
+        ctx.sync()
+        log(f"sweep run N={W.N} done")
+        ctx.free(y)
+        W.free()
+    ctx.close()
+
+
+def sweep_summarize(dirs):
+    """Per size, from rocprofv3 kernel-trace CSVs: the mean traced duration
+    of the fused GEMV and the best grid's mean of the streaming read, then
+    the fits."""
+    rows = []
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+            with open(f) as fh:
+                rows += list(csv.DictReader(fh))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    sec = None
+    gemv, stream, names = {}, {}, {}
+    for r in rows:
+        kn = r["Kernel_Name"]
+        wg = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+        if "stream_read_kernel" in kn and SWEEP_MARKER_BASE <= wg < SWEEP_MARKER_BASE + 2 * len(SWEEP_MULTS):
+            sec = wg - SWEEP_MARKER_BASE
+            continue
+        if sec is None:
+            continue
+        m = SWEEP_MULTS[sec // 2]
+        if sec % 2 == 0 and "gemv_persist_kernel" in kn:
+            gemv.setdefault(m, []).append(us)
+            names[m] = kn
+        elif sec % 2 == 1 and "stream_read_kernel" in kn:
+            stream.setdefault(m, {}).setdefault((wg, kn), []).append(us)
+    return gemv, stream, names
+
+
+def sweep_write(dirs):
+    gemv, stream, names = sweep_summarize(dirs)
+    print("# Size sweep under rocprofv3 --kernel-trace --stats: the fused Q4_K GEMV (the headline")
+    print("# step: fp32 x quantized to Q8_K in the launch, then the GEMV) and the 16-B streaming-read")
+    print("# floor at 9728 x {1, 2, 4, 8} rows of K = 2560, weights rotated over >= 512 MB of")
+    print("# replicas, every dispatch launched directly (16 per size and kernel). Command (run from")
+    print("# /tmp with TMPDIR=/tmp; paths relative to the repository root):")
+    print("#   rocprofv3 --kernel-trace --stats -d gpurun_out/sweep_trace -o run --output-format csv \\")
+    print("#     -- python3 bench.py --sweep-run")
+    print(f"#   python3 bench.py --sweep-summarize gpurun_out/sweep_trace > {os.path.relpath(SWEEP_PROFILE, ROOT)}")
+    print("# Each traced dispatch runs alone (its own ramp-up and drain under the profiler's completion")
+    print("# signal), so a duration here is the graph-timed step's time plus a fixed per-dispatch cost;")
+    print("# the fit T = t0 + bytes / BW puts that cost into t0, and its slope (the marginal rate) is")
+    print("# what both regimes share. fit lines: t0_us, marginal GB/s, marginal fraction of 8 TB/s.")
+    print("# rows  gemv_us  gemv_alg_bytes  stream_us  stream_bytes  stream_grid")
+    gp, sp = [], []
+    for m in SWEEP_MULTS:
+        if m not in gemv or m not in stream:
+            continue
+        N = 9728 * m
+        alg = N * 1440 + 2560 * 4 + N * 4
+        g = float(np.mean(gemv[m]))
+        (wg, kn), v = min(stream[m].items(), key=lambda kv: np.mean(kv[1]))
+        st = float(np.mean(v))
+        nl = kn.split("stream_read_kernel<", 1)[1].split(">", 1)[0] if "stream_read_kernel<" in kn else "?"
+        print(f"{N:6d}  {g:7.3f}  {alg:14d}  {st:9.3f}  {N * 1440:12d}  {wg}x{nl}")
+        print(f"gemv.N{N}.us: {g:.3f}")
+        print(f"stream.N{N}.us: {st:.3f}")
+        gp.append((alg, g))
+        sp.append((N * 1440, st))
+    if gp:
+        print(f"gemv.kernel: {names[SWEEP_MULTS[0]]}")
+        fg, fs = fit_time(gp), fit_time(sp)
+        for k, v in fg.items():
+            print(f"fit_gemv.{k}: {v}")
+        for k, v in fs.items():
+            print(f"fit_stream.{k}: {v}")
+        print(f"gemv.N9728.frac_of_peak: {gp[0][0] / (gp[0][1] * 1e-6) / 1e9 / HBM_PEAK_GBS:.4f}")
+
+
+def sweep_profile():
+    """Figures of the committed size-sweep trace summary (or {})."""
+    out = {}
+    try:
+        with open(SWEEP_PROFILE) as f:
+            for ln in f:
+                if ":" in ln and not ln.startswith("#"):
+                    k, v = ln.split(":", 1)
+                    out[k.strip()] = v.strip()
+    except OSError:
+        pass
+    return out
+
+
 # ---------------------------------------------------------------- GEMM lines
 PMC = None
 
@@ -299,6 +493,10 @@ def gemm_line(name, M, N, K, type_id, ms, extra_bytes=0):
             "frac": round(g / HBM_PEAK_GBS, 4), "int8_tops": round(tops, 2),
             "int8_frac": round(tops / INT8_PEAK_TOPS, 4), "algorithmic_bytes": byts, "int8_ops": ops,
             "counters": pmc_fields(name)}
+    us_prof = (roof["counters"] or {}).get("us_under_profiler")
+    if us_prof:  # the same figures over the kernel's duration under the profiler (direct launches)
+        roof["frac_profiled"] = round(byts / (us_prof * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        roof["int8_frac_profiled"] = round(ops / (us_prof * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)
     return {"us_gemm_kernel": round(ms * 1e3, 3), "tops": round(tops, 3), "gbs": round(g, 1), "roofline": roof}
 
 
@@ -882,14 +1080,20 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extra sections: tree,prefill,mixed,ffn,rms,lm,floor")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra sections: tree,prefill,mixed,ffn,rms,lm,sweep,floor")
     ap.add_argument("--direct", action="store_true",
                     help="launch steps directly, not from a HIP graph (for rocprofv3 runs)")
     ap.add_argument("--pmc-run", action="store_true", help="the GEMM workloads alone, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summarize", nargs="+", metavar="DIR", help="print the counter summary of rocprofv3 CSVs")
+    ap.add_argument("--sweep-run", action="store_true", help="the size sweep launched directly, for rocprofv3")
+    ap.add_argument("--sweep-summarize", nargs="+", metavar="DIR", help="print the size sweep's trace summary")
     args = ap.parse_args()
     if args.pmc_summarize:
         pmc_write(args.pmc_summarize)
+        return
+    if args.sweep_summarize:
+        sweep_write(args.sweep_summarize)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build measures the single-GPU hot path "
@@ -898,7 +1102,13 @@ def main():
     if args.pmc_run:
         pmc_run(args)
         return
+    if args.sweep_run:
+        sweep_run(args)
+        return
     DIRECT = args.direct
+    if not DIRECT and under_profiler():
+        log("a profiler is attached: steps are launched directly (graph replays are not run under a profiler)")
+        DIRECT = True
 
     ctx = qmm_hip.Context(0)
     info = ctx.device_info()
@@ -912,6 +1122,8 @@ def main():
     only = set(filter(None, args.only.split(",")))
     want = (lambda s: not only or s in only)
     if not args.no_extra:
+        if want("sweep"):  # right after the headline, in the same conditions
+            extra["size_sweep_q4k_gemv"] = bench_size_sweep(ctx, args)
         if want("tree"):
             extra.update(bench_tree(ctx, args))
         if want("mixed"):
@@ -960,12 +1172,29 @@ def main():
                      "floor_us_per_launch": floor["us_per_launch"],
                      "frac_of_measured_floor": round(floor["us_per_launch"] / (ms * 1e3), 4)},
         "hbm_read_floor": floor,
+        "roofline_regimes": ("roofline.frac: algorithmic bytes / the graph-timed step (HIP events on the library's "
+                             "stream around graph replays); roofline.frac_profiled: the same over the kernel's mean "
+                             "duration under rocprofv3 --kernel-trace, launched directly "
+                             f"({os.path.relpath(SWEEP_PROFILE, ROOT)}); fit_graph / fit_profiled: T = t0 + bytes / "
+                             "BW over 9728 x {1, 2, 4, 8} rows in each regime, t0 the fixed per-launch time, "
+                             "marginal_frac = BW / 8 TB/s"),
         "gemv_prequantized": head["gemv_prequantized"],
         "cache_resident_us_per_launch": head["cache_resident_us_per_launch"],
         "parity": head["parity"],
         "cpu_baseline": cpu,
         "device": info,
     }
+    prof = sweep_profile()
+    roof = line["roofline"]
+    if "gemv.N9728.frac_of_peak" in prof:
+        roof["frac_profiled"] = float(prof["gemv.N9728.frac_of_peak"])
+        roof["us_per_launch_profiled"] = float(prof["gemv.N9728.us"])
+        roof["fit_profiled"] = {k.split(".", 1)[1]: float(v) for k, v in prof.items() if k.startswith("fit_gemv.")}
+        roof["fit_profiled_stream_read"] = {k.split(".", 1)[1]: float(v) for k, v in prof.items()
+                                            if k.startswith("fit_stream.")}
+    if "size_sweep_q4k_gemv" in extra:
+        roof["fit_graph"] = extra["size_sweep_q4k_gemv"]["fit_gemv"]
+        roof["fit_graph_stream_read"] = extra["size_sweep_q4k_gemv"]["fit_stream_read"]
     line.update(extra)
     print(json.dumps(line), flush=True)
 

@@ -1005,17 +1005,25 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
         qmm::Q8KView xk;
         qmm::Q80View x0;
         act_views(q8k, q80, 1, K, xk, x0);
-        auto fused = [&](const std::pair<int, int> &gr, const float *g) {
+        auto fused = [&](const std::pair<int, int> &gr, const float *g, int &np) {
             qmm_matrix_task t = tc;
             const int r0 = gr.first * params->chunk_rows;
             t.rows = int(std::min<int64_t>(int64_t(gr.second + 1) * params->chunk_rows, vocab_rows) - r0);
-            int np = 0;
+            np = 0;
             return qmm::launch_gemv_argmax(t.type, mat_args(t, 1, K), xk, x0, true, nullptr, 0u, nullptr, &np,
                                            ctx->stream, qmm::PrevStep{}, false, x32, g) == hipSuccess;
         };
-        pend.seed = M == 1 && n_pre == 0 && fused(groups[0], nullptr);
+        int np = 0;
+        pend.seed = M == 1 && n_pre == 0 && fused(groups[0], nullptr, np);
         bool normed = x32 && pend.seed;
-        for (size_t i = 0; i < groups.size() && normed; ++i) normed = fused(groups[i], gamma);
+        // every launch after the first reads its predecessor's per-workgroup
+        // partials, at most 1024 of them (the bound each launch applies to
+        // its PrevStep): where a launch's grid has more, the scan takes the
+        // norm's own launch, before anything is enqueued
+        for (size_t i = 0; i < groups.size() && normed; ++i) {
+            const int prev = np;
+            normed = (i == 0 || prev <= 1024) && fused(groups[i], gamma, np);
+        }
         if (normed) {
             pend.x32 = x32;
             pend.gamma = gamma;

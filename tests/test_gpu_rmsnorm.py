@@ -86,7 +86,10 @@ def test_rmsnorm_block_mismatch_rate(ctx, oracle):
         f"{codes} of {qs.size} codes ({100 * codes / qs.size:.4f} %), each by at most "
         f"{int(np.abs(qs.astype(int) - rqs.astype(int)).max())}")
     assert np.abs(qs.astype(int) - rqs.astype(int)).max() <= 1
-    assert blocks.mean() < 0.25
+    # measured for this seed: 32 of 5120 blocks (0.62 %), 40 of 1.31 M codes;
+    # the bounds leave ~3x headroom, so a changed summation tree shows here
+    assert blocks.mean() <= 0.02
+    assert codes <= 130
     for b in (xb, gb, q):
         ctx.free(b)
 

@@ -76,3 +76,52 @@ def test_noalloc_refuses_inputs_past_the_scratch(ctx):
     ctx.sync()
     for b in (w, y, x):
         ctx.free(b)
+
+
+def test_noalloc_captures_in_a_fresh_context():
+    """The point of the entry point: a context that never reserved or
+    allocated activation buffers captures the dispatch into a HIP graph (a
+    call that needed a buffer would fail the capture with QMM_ENOMEM), and
+    every replay — with eager work, fresh inputs and synchronizations in
+    between — equals the eager allocating dispatch bit for bit, at M = 48
+    (the scratch path) and M = 1 (the fused batch-1 path)."""
+    K = 2560
+    with qmm_hip.Context(0) as fresh, qmm_hip.Context(0) as eager:
+        for M, specs, seed in ((48, [(TYPE_Q4_K, 300), (TYPE_Q8_0, 70), (TYPE_F32, 20)], 540),
+                               (1, [(TYPE_Q4_K, 257), (TYPE_Q6_K, 64)], 550)):
+            say(f"noalloc graph capture in a fresh context: M={M}")
+            xb = fresh.malloc(M * K * 4)
+            ws, tf, te = [], [], []
+            for i, (t, n) in enumerate(specs):
+                host = _weights(t, n, K, seed + 1 + i)
+                wf, we = fresh.weight_upload(host, t, n, K), eager.weight_upload(host, t, n, K)
+                yf, ye = fresh.malloc(M * n * 4), eager.malloc(M * n * 4)
+                ws += [(fresh, wf), (eager, we), (fresh, yf), (eager, ye)]
+                tf.append(qmm_hip.MatrixTask(wf, t, n, K, yf, n))
+                te.append(qmm_hip.MatrixTask(we, t, n, K, ye, n))
+            fresh.graph_begin()
+            fresh.gemm_multi_dispatch_noalloc(xb, M, K, tf)
+            g = fresh.graph_end()
+            try:
+                for r in range(3):
+                    x = synth.activations(M, K, seed=seed + 10 + r)
+                    fresh.h2d(xb, x)
+                    for a in tf:  # a replay that skipped a task would leave this pattern
+                        fresh.h2d(a.dst, np.full(M * a.rows, np.nan, np.float32))
+                    fresh.sync()
+                    fresh.graph_launch(g)
+                    fresh.sync()
+                    xe = eager.upload(x)
+                    eager.gemm_multi_dispatch(xe, M, K, te)
+                    eager.sync()
+                    eager.free(xe)
+                    for i, (a, b) in enumerate(zip(tf, te)):
+                        got = fresh.d2h(a.dst, np.float32, (M, a.rows))
+                        ref = eager.d2h(b.dst, np.float32, (M, b.rows))
+                        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+                            f"M={M} replay {r}: task {i} differs from the eager dispatch"
+            finally:
+                fresh.graph_destroy(g)
+            for c, b in ws:
+                c.free(b)
+            fresh.free(xb)
