@@ -221,6 +221,21 @@ typedef struct {
     int first_checkpoint;    /* first chunk that may end the scan: 0, or 6 where all 7 chunks are
                                 required (g_require_full_7chunks, E:11254) */
     float prune_margin;      /* speculative pruning margin (1e-3f, E:11208) */
+    /* A scan in several calls (zero-initialized fields: the whole scan in one call). This call
+     * scans chunks [chunk_begin, chunk_end) (chunk_end 0: through the last chunk), so a caller can
+     * stop after chunk 0, take the engine's host-side decisions, and continue: the script-gated
+     * exit (E:9717-9733 at batch 1, E:11194-11241 batched) needs the token tables on the host
+     * between chunk 0 and chunk 1. The call's last chunk always runs its step (argmax update,
+     * pruning, its checkpoint test). */
+    int chunk_begin;
+    int chunk_end;
+    int resume;              /* 0: a new scan (best_val / best_id / scan_state seeded as below);
+                                nonzero: continue the scan whose best_val / best_id / scan_state
+                                an earlier call left (same M, K, tensor, draft_ids): nothing is
+                                seeded; pre_ids are evaluated for the active positions only
+                                (the extended-script rows, E:11216-11225), then, with drafts,
+                                the pruning rule is applied once (E:11226-11231) before the
+                                chunks; a stopped scan stays stopped */
 } qmm_lm_scan_params;
 /* best_val / best_id [M] (device) are seeded with -1e30 / 0 (E:11139-11140);
  * then every position evaluates the rows pre_ids[0..n_pre) (device; the

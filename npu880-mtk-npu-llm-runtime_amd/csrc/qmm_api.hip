@@ -955,20 +955,24 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
         return fail(ctx, QMM_EINVAL, "bad LM-head scan parameters");
     if (!aligned(best_val, 4) || !aligned(best_id, 4) || !aligned(scan_state, 4))
         return fail(ctx, QMM_EALIGN, "best_val/best_id/scan_state must be 4-B aligned");
-    // Chunks share a launch up to the next chunk after which something is
-    // decided: a checkpoint (E:11248-11256) or, with drafts, the pruning
-    // (E:11203-11209, after every chunk). In between nothing changes the
-    // scan's course, and the strict running update over the merged rows
-    // (the first row holding the largest value, if it beats the best) is
-    // the chunk-by-chunk updates' result.
     const int nchunks = (vocab_rows + params->chunk_rows - 1) / params->chunk_rows;
+    // this call's chunks [cb, ce); a resumed scan seeds nothing
+    const int cb = params->chunk_begin, ce = params->chunk_end ? params->chunk_end : nchunks;
+    const bool resume = params->resume != 0;
+    if (cb < 0 || ce < cb || ce > nchunks) return fail(ctx, QMM_EINVAL, "bad LM-head scan chunk range");
+    // Chunks share a launch up to the next chunk after which something is
+    // decided: a checkpoint (E:11248-11256), with drafts the pruning
+    // (E:11203-11209, after every chunk), or the call's last chunk. In
+    // between nothing changes the scan's course, and the strict running
+    // update over the merged rows (the first row holding the largest value,
+    // if it beats the best) is the chunk-by-chunk updates' result.
     const bool prunes = draft_ids && M >= 2;
     auto decides = [&](int c) {
-        return prunes || c == nchunks - 1 || (params->n_thresholds > 0 && c >= params->first_checkpoint);
+        return prunes || c == ce - 1 || (params->n_thresholds > 0 && c >= params->first_checkpoint);
     };
     std::vector<std::pair<int, int>> groups;  // [first chunk, last chunk] of each launch
-    int chunk = 0;                            // rows of the largest launch
-    for (int c0 = 0; c0 < nchunks;) {
+    int chunk = std::min(params->chunk_rows, vocab_rows);  // rows of the largest launch
+    for (int c0 = cb; c0 < ce;) {
         int c1 = c0;
         while (!decides(c1)) ++c1;
         groups.emplace_back(c0, c1);
@@ -1014,8 +1018,9 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
                                            ctx->stream, qmm::PrevStep{}, false, x32, g) == hipSuccess;
         };
         int np = 0;
-        pend.seed = M == 1 && n_pre == 0 && fused(groups[0], nullptr, np);
-        bool normed = x32 && pend.seed;
+        const bool first_fused = M == 1 && n_pre == 0 && !groups.empty() && fused(groups[0], nullptr, np);
+        pend.seed = first_fused && !resume;
+        bool normed = x32 && first_fused;
         // every launch after the first reads its predecessor's per-workgroup
         // partials, at most 1024 of them (the bound each launch applies to
         // its PrevStep): where a launch's grid has more, the scan takes the
@@ -1034,15 +1039,21 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
                 return hip_fail(ctx, e, "quantize_q8_0 launch");
         }
     }
-    if (!pend.seed) {
+    if (!pend.seed && !resume) {
         e = qmm::launch_scan_init(M, best_val, best_id, cand, scan_state, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "scan init launch");
     }
-    // the rows every position evaluates first (end-of-text rows), fp32, in list order (E:11143-11146)
+    // the rows every active position evaluates first, fp32, in list order:
+    // the end-of-text rows of a new scan (E:11143-11146, every position
+    // active), the extended-script rows of a resumed one (E:11216-11225)
     if (n_pre > 0 && (rc = lm_argmax_run(ctx, q8k, q80, M, K, tp, 0, pre_ids, uint32_t(vocab_rows), nullptr, best_val,
-                                         best_id, work, nullptr, nullptr)))
+                                         best_id, work, scan_state, nullptr)))
         return rc;
-    // each position's draft candidate (E:11147-11153)
+    // each position's draft candidate (E:11147-11153). A resumed scan
+    // derives the candidates' logits again (the pruning needs them); their
+    // strict update changes nothing, as every position's best already
+    // includes its candidate. Then, after the extended rows, the pruning
+    // rule once (E:11226-11231).
     if (draft_ids && M >= 2) {
         e = qmm::launch_gather_rows(wb, rb, draft_ids + 1, uint32_t(vocab_rows), M - 1, work, nullptr, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "row gather launch");
@@ -1051,6 +1062,11 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
         if ((rc = run_tasks(ctx, nullptr, q8k, q80, M, K, &td, 1))) return rc;
         e = qmm::launch_scan_cand(M, cdot, draft_ids, uint32_t(vocab_rows), best_val, best_id, cand, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "candidate launch");
+        if (resume) {
+            e = qmm::launch_scan_final(nullptr, 0, 0u, best_val, best_id, cand, draft_ids, params->prune_margin, -1e30f,
+                                       false, cb - 1, scan_state, ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "pruning launch");
+        }
     }
     // the chunks (E:11158-11257), a launch per group: each does nothing once
     // the scan has stopped

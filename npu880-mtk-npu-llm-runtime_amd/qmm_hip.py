@@ -47,7 +47,8 @@ class QmmError(RuntimeError):
 class LmScanParams(C.Structure):
     """qmm_lm_scan_params (the chunked vocabulary scan, E:11107-11262)."""
     _fields_ = [("chunk_rows", C.c_int), ("thresholds", C.POINTER(C.c_float)), ("n_thresholds", C.c_int),
-                ("first_checkpoint", C.c_int), ("prune_margin", C.c_float)]
+                ("first_checkpoint", C.c_int), ("prune_margin", C.c_float), ("chunk_begin", C.c_int),
+                ("chunk_end", C.c_int), ("resume", C.c_int)]
 
 
 class _Task(C.Structure):
@@ -414,22 +415,26 @@ class Context:
 
     def lm_head_scan(self, q8k, q80, M: int, K: int, w_lm, type_id: int, vocab_rows: int, chunk_rows: int,
                      thresholds=None, first_checkpoint: int = 0, prune_margin: float = 1e-3, pre_ids=None,
-                     n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None):
-        """qmm_lm_head_scan: the chunked vocabulary scan with early exit and pruning."""
+                     n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None,
+                     chunk_begin: int = 0, chunk_end: int = 0, resume: bool = False):
+        """qmm_lm_head_scan: the chunked vocabulary scan with early exit and pruning; chunks
+        [chunk_begin, chunk_end) of it (chunk_end 0: to the end), a new scan or (resume) the
+        continuation of the one best_val / best_id / scan_state hold."""
         thr = None if thresholds is None else (C.c_float * len(thresholds))(*[float(t) for t in thresholds])
         prm = LmScanParams(chunk_rows, thr if thr is not None else None, 0 if thr is None else len(thresholds),
-                           first_checkpoint, prune_margin)
+                           first_checkpoint, prune_margin, chunk_begin, chunk_end, 1 if resume else 0)
         self._call("qmm_lm_head_scan", self._h, _p(_addr(q8k)), _p(_addr(q80)), M, K, _p(_addr(w_lm)), type_id,
                    vocab_rows, C.byref(prm), _p(_addr(pre_ids)), n_pre, _p(_addr(draft_ids)), _p(_addr(best_val)),
                    _p(_addr(best_id)), _p(_addr(scan_state)))
 
     def lm_head_scan_rmsnorm(self, x, gamma, M: int, K: int, w_lm, type_id: int, vocab_rows: int, chunk_rows: int,
                              thresholds=None, first_checkpoint: int = 0, prune_margin: float = 1e-3, pre_ids=None,
-                             n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None):
+                             n_pre: int = 0, draft_ids=None, best_val=None, best_id=None, scan_state=None,
+                             chunk_begin: int = 0, chunk_end: int = 0, resume: bool = False):
         """qmm_lm_head_scan_rmsnorm: the final RMSNorm of x with gamma, then the chunked vocabulary scan."""
         thr = None if thresholds is None else (C.c_float * len(thresholds))(*[float(t) for t in thresholds])
         prm = LmScanParams(chunk_rows, thr if thr is not None else None, 0 if thr is None else len(thresholds),
-                           first_checkpoint, prune_margin)
+                           first_checkpoint, prune_margin, chunk_begin, chunk_end, 1 if resume else 0)
         self._call("qmm_lm_head_scan_rmsnorm", self._h, _p(_addr(x)), _p(_addr(gamma)), M, K, _p(_addr(w_lm)),
                    type_id, vocab_rows, C.byref(prm), _p(_addr(pre_ids)), n_pre, _p(_addr(draft_ids)),
                    _p(_addr(best_val)), _p(_addr(best_id)), _p(_addr(scan_state)))

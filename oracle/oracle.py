@@ -54,6 +54,13 @@ class _MatrixTask(C.Structure):
     ]
 
 
+class _Script(C.Structure):
+    """qo_script: the LM head's extended-script state (E:9690-9733, E:11185-11241)."""
+    _fields_ = [("is_cyr", _p), ("is_cjk", _p), ("cyr_rows", _p), ("n_cyr", C.c_int), ("cjk_rows", _p),
+                ("n_cjk", C.c_int), ("has_cyr", C.c_int), ("has_cjk", C.c_int), ("require_full", C.c_int),
+                ("batch1", C.c_int)]
+
+
 class Oracle:
     """The C restatement (liboracle.so)."""
 
@@ -93,6 +100,9 @@ class Oracle:
         L.qo_lm_head_scan.restype = C.c_int
         L.qo_lm_head_scan.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p, C.c_int,
                                       C.c_int, C.c_float, _p, C.c_int, _p, _p, _p, _p, _p]
+        L.qo_lm_head_scan_script.restype = C.c_int
+        L.qo_lm_head_scan_script.argtypes = [C.c_uint32, _p, C.c_int, C.c_int, C.c_int, _p, _p, _p, C.c_int, _p,
+                                             C.c_int, C.c_float, _p, C.c_int, _p, C.POINTER(_Script), _p, _p, _p, _p]
 
     # fp16 ----------------------------------------------------------------
     def f32_to_fp16(self, x) -> np.ndarray:
@@ -304,6 +314,42 @@ class Oracle:
         if n < 0:
             raise ValueError("oracle rejected the scan")
         return bv, bi, n, act.value, stp.value
+
+    def lm_head_scan_script(self, q8k, w, type_id: int, vocab_rows: int, K: int, chunk_rows: int, thresholds=None,
+                            margin: float = 1e-3, pre_ids=None, draft_ids=None, is_cyr=None, is_cjk=None,
+                            cyr_rows=None, cjk_rows=None, has_cyr=False, has_cjk=False, require_full=False,
+                            batch1=False):
+        """The whole LM-head scan with its script-gated exit (qo_lm_head_scan_script):
+        (best_val, best_id, chunks_read, active, stopped, has_cyr, has_cjk)."""
+        d, qs, bs = (np.ascontiguousarray(a) for a in q8k)
+        M = qs.shape[0]
+        w = np.ascontiguousarray(w, np.uint8)
+        keep = []
+
+        def arr(a, dt):
+            if a is None:
+                return None, 0
+            a = np.ascontiguousarray(a, dt)
+            keep.append(a)
+            return _ptr(a), a.size
+
+        thr, nthr = arr(thresholds, np.float32)
+        pre, npre = arr(pre_ids, np.uint32)
+        dr, _ = arr(draft_ids, np.uint32)
+        fc, _ = arr(is_cyr, np.uint8)
+        fj, _ = arr(is_cjk, np.uint8)
+        rc_, nc = arr(cyr_rows, np.uint32)
+        rj, nj = arr(cjk_rows, np.uint32)
+        sc = _Script(fc, fj, rc_, nc, rj, nj, int(has_cyr), int(has_cjk), int(require_full), int(batch1))
+        bv = np.empty(M, np.float32)
+        bi = np.empty(M, np.uint32)
+        act, stp = C.c_int(), C.c_int()
+        n = self.lib.qo_lm_head_scan_script(type_id, _ptr(w), vocab_rows, K, M, _ptr(d), _ptr(qs), _ptr(bs),
+                                            chunk_rows, thr, nthr, margin, pre, npre, dr, C.byref(sc), _ptr(bv),
+                                            _ptr(bi), C.byref(act), C.byref(stp))
+        if n < 0:
+            raise ValueError("oracle rejected the scan")
+        return bv, bi, n, act.value, stp.value, bool(sc.has_cyr), bool(sc.has_cjk)
 
     def rmsnorm_q8k_f16(self, x16: np.ndarray, gamma16: np.ndarray):
         """rmsnorm_fp16_rows_fast on fp16 bits: (y16 [M][K], (d, qs, bsum32))."""

@@ -807,3 +807,134 @@ int qo_lm_head_scan(uint32_t type, const uint8_t *w, int vocab_rows, int K, int 
     *stopped_out = stopped;
     return c;
 }
+
+/* run_final_norm_and_lm_head_batch_sdot (E:11107-11262) whole, script rows
+ * included, and at sc->batch1 the batch-1 scan of
+ * run_final_norm_and_lm_head_pipelined (E:9675-9744). */
+int qo_lm_head_scan_script(uint32_t type, const uint8_t *w, int vocab_rows, int K, int M, const float *xd,
+                           const int8_t *xqs, const int32_t *xbs, int chunk_rows, const float *thresholds,
+                           int n_thresholds, float margin, const uint32_t *pre_ids, int n_pre,
+                           const uint32_t *draft_ids, qo_script *sc, float *best_val, uint32_t *best_id,
+                           int *active_out, int *stopped_out) {
+    const size_t rb = (size_t)qo_row_bytes(type, (uint64_t)K);
+    const int nd = (type == QO_TYPE_Q8_0) ? K / 32 : K / 256;
+    float cand[4096];
+    if (M > 4096 || rb == 0 || chunk_rows <= 0 || !sc || (sc->batch1 && (M != 1 || n_pre || draft_ids))) return -1;
+#define QO_DOT(row, p)                                                                                    \
+    qo_dot_row(type, w + (size_t)(row) * rb, K, xd + (size_t)(p) * nd, xqs + (size_t)(p) * K,          \
+               xbs ? xbs + (size_t)(p) * (K / 32) : NULL)
+    /* seeds, end-of-text rows and draft candidates (E:11133-11155) */
+    for (int p = 0; p < M; ++p) {
+        best_val[p] = -1e30f;
+        best_id[p] = 0;
+        cand[p] = -1e30f;
+        for (int i = 0; i < n_pre; ++i) {
+            const uint32_t id = pre_ids[i];
+            const float v = id < (uint32_t)vocab_rows ? QO_DOT(id, p) : -1e30f;
+            if (v > best_val[p]) {
+                best_val[p] = v;
+                best_id[p] = id;
+            }
+        }
+        if (p + 1 < M && draft_ids) {
+            const uint32_t cid = draft_ids[p + 1];
+            const float vc = cid < (uint32_t)vocab_rows ? QO_DOT(cid, p) : -1e30f;
+            cand[p] = vc;
+            if (vc > best_val[p]) {
+                best_val[p] = vc;
+                best_id[p] = cid;
+            }
+        }
+    }
+    int active = M, stopped = 0, c = 0;
+    const int nchunks = (vocab_rows + chunk_rows - 1) / chunk_rows;
+#define QO_PRUNE()                                                                                 \
+    for (int p = 0; p + 1 < active; ++p)                                                           \
+        if (draft_ids && best_id[p] != draft_ids[p + 1] && best_val[p] > cand[p] + margin) {       \
+            active = p + 1;                                                                        \
+            break;                                                                                 \
+        }
+    for (c = 0; c < nchunks; ++c) {
+        const int r0 = c * chunk_rows;
+        const int rows = (r0 + chunk_rows > vocab_rows) ? vocab_rows - r0 : chunk_rows;
+        /* the chunk's fp16 logits, strict > (E:11172-11183, E:9699-9706) */
+        for (int p = 0; p < active; ++p)
+            for (int r = 0; r < rows; ++r) {
+                const float v = qo_fp16_to_f32(qo_f32_to_fp16(QO_DOT(r0 + r, p)));
+                if (v > best_val[p]) {
+                    best_val[p] = v;
+                    best_id[p] = (uint32_t)(r0 + r);
+                }
+            }
+        /* the session's script flags from the best tokens (E:11186-11193, E:9709-9714) */
+        for (int p = 0; p < active; ++p) {
+            const uint32_t bt = best_id[p];
+            if (bt < (uint32_t)vocab_rows && sc->is_cyr && sc->is_cyr[bt]) sc->has_cyr = 1;
+            if (bt < (uint32_t)vocab_rows && sc->is_cjk && sc->is_cjk[bt]) sc->has_cjk = 1;
+        }
+        QO_PRUNE() /* E:11198-11209 */
+        /* chunk 0 of the engine's chunking with a script active: its extended rows (E:11211-11241,
+           E:9716-9733) */
+        if ((sc->has_cyr || sc->has_cjk) && c == 0 && n_thresholds > 0) {
+            for (int s = 0; s < 2; ++s) {
+                const int on = s == 0 ? sc->has_cyr : sc->has_cjk;
+                const uint32_t *ids = s == 0 ? sc->cyr_rows : sc->cjk_rows;
+                const int n = s == 0 ? sc->n_cyr : sc->n_cjk;
+                if (!on) continue;
+                for (int p = 0; p < active; ++p)
+                    for (int i = 0; i < n; ++i) {
+                        const uint32_t id = ids[i];
+                        const float v = id < (uint32_t)vocab_rows ? QO_DOT(id, p) : -1e30f;
+                        if (v > best_val[p]) {
+                            best_val[p] = v;
+                            best_id[p] = id;
+                        }
+                    }
+            }
+            if (sc->batch1) {
+                if (!sc->require_full && best_val[0] >= 10.5f) { /* E:9731-9733 */
+                    stopped = 1;
+                    ++c;
+                    break;
+                }
+            } else {
+                QO_PRUNE() /* E:11226-11231 */
+                int script_ok = 1;
+                for (int p = 0; p < active; ++p) { /* E:11232-11238 */
+                    const uint32_t bt = best_id[p];
+                    const int in_script = bt < (uint32_t)vocab_rows &&
+                                          ((sc->has_cyr && sc->is_cyr && sc->is_cyr[bt]) ||
+                                           (sc->has_cjk && sc->is_cjk && sc->is_cjk[bt]));
+                    const float min_req = in_script ? 11.5f : 20.0f;
+                    if (best_val[p] < min_req) {
+                        script_ok = 0;
+                        break;
+                    }
+                }
+                if (!sc->require_full && script_ok) { /* E:11239-11241 */
+                    stopped = 1;
+                    ++c;
+                    break;
+                }
+            }
+        }
+        /* the checkpoint (E:11243-11256, E:9735-9745) */
+        const float thresh = (c < n_thresholds) ? thresholds[c] : -1e30f;
+        int all_above = 1;
+        for (int p = 0; p < active; ++p)
+            if (best_val[p] < thresh) {
+                all_above = 0;
+                break;
+            }
+        if (n_thresholds > 0 && (!sc->require_full || c >= 6) && all_above) {
+            stopped = 1;
+            ++c;
+            break;
+        }
+    }
+#undef QO_PRUNE
+#undef QO_DOT
+    *active_out = active;
+    *stopped_out = stopped;
+    return c;
+}

@@ -147,6 +147,38 @@ int qo_lm_head_scan(uint32_t type, const uint8_t *w, int vocab_rows, int K, int 
                     const uint32_t *draft_ids, float *best_val, uint32_t *best_id, int *active_out,
                     int *stopped_out);
 
+/* The extended-script state of the LM head (E:9690-9733, E:11185-11241):
+ * the tokenizer's per-token script flags, each script's extended row list,
+ * and the session's sticky flags (read, then updated). */
+typedef struct {
+    const uint8_t *is_cyr;    /* g_token_is_cyrillic [vocab_rows] */
+    const uint8_t *is_cjk;    /* g_token_is_cjk [vocab_rows] */
+    const uint32_t *cyr_rows; /* the Cyrillic extended rows, evaluation order */
+    int n_cyr;
+    const uint32_t *cjk_rows; /* the CJK extended rows */
+    int n_cjk;
+    int has_cyr, has_cjk;     /* g_session_has_cyrillic / _cjk: in and out */
+    int require_full;         /* g_require_full_7chunks: checkpoints from chunk 6, no script exit */
+    int batch1;               /* 1: run_final_norm_and_lm_head_pipelined's rule (M = 1, E:9717-9733);
+                                 0: run_final_norm_and_lm_head_batch_sdot's (E:11194-11241) */
+} qo_script;
+
+/* The whole LM-head scan with its script-gated exit: qo_lm_head_scan's
+ * chunk loop (thresholds present stand for the engine's 24832-row
+ * chunking: checkpoints at every chunk, from chunk 6 with require_full),
+ * plus after each chunk the session flags from the active positions' best
+ * tokens, and after chunk 0, when a script is active, its extended rows
+ * for the active positions (fp32 values, list order, strict >), then the
+ * script exit: batch1, the running best >= 10.5; batched, the pruning
+ * again and every active best >= 11.5 when its token is of an active
+ * script, else >= 20.0. The batch-1 rule has no pre rows and no drafts
+ * (pass none). Returns the chunks read (-1 on bad arguments). */
+int qo_lm_head_scan_script(uint32_t type, const uint8_t *w, int vocab_rows, int K, int M, const float *xd,
+                           const int8_t *xqs, const int32_t *xbs, int chunk_rows, const float *thresholds,
+                           int n_thresholds, float margin, const uint32_t *pre_ids, int n_pre,
+                           const uint32_t *draft_ids, qo_script *sc, float *best_val, uint32_t *best_id,
+                           int *active_out, int *stopped_out);
+
 /* rmsnorm_fp16_rows_fast (E:4264-4314), scalar branch, on fp16 bits:
  * y [M][K] fp16 bits, then the Q8_K of each y row. K % 256 == 0. */
 void qo_rmsnorm_q8k_f16(const uint16_t *x, const uint16_t *gamma, int M, int K, uint16_t *y,

@@ -129,3 +129,107 @@ def test_scan_pruning_freezes_later_positions(oracle):
     # without draft ids nothing is pruned and the chunk-1 rows win
     bv, bi, n, act, stp = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, None)
     assert act == M and [int(i) for i in bi[1:]] == [CH + 10, CH + 20, CH + 30]
+
+
+# ---------------------------------------------------------------------------
+# The script-gated exit (E:9716-9733 at batch 1, E:11185-11241 batched):
+# outcomes fixed by planted logits and script tables.
+def _tables(rows_cyr=(), rows_cjk=()):
+    is_cyr = np.zeros(V, np.uint8)
+    is_cjk = np.zeros(V, np.uint8)
+    is_cyr[list(rows_cyr)] = 1
+    is_cjk[list(rows_cjk)] = 1
+    return is_cyr, is_cjk
+
+
+def test_script_scan_without_a_script_is_the_plain_scan(oracle):
+    M = 3
+    w, q = _scan_setup(oracle, M, 910)
+    draft = np.array([0, 700, 9000], np.uint32)
+    lm_plant.plant(w, oracle, q, [(700, 0, 4.0), (CH + 3, 0, 6.0), (2 * CH + 9, 1, 14.0), (9000, 1, 3.0)], K)
+    is_cyr, is_cjk = _tables()
+    for thr in (lm_plant.CHUNK_THRESH, None):
+        plain = oracle.lm_head_scan(q, w, TYPE_Q6_K, V, K, CH, thr, pre_ids=[V - 3], draft_ids=draft)
+        got = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, thr, pre_ids=[V - 3], draft_ids=draft,
+                                         is_cyr=is_cyr, is_cjk=is_cjk, cyr_rows=[5, 6], cjk_rows=[7])
+        assert np.array_equal(plain[0].view(np.uint32), got[0].view(np.uint32))
+        assert np.array_equal(plain[1], got[1]) and plain[2:] == got[2:5]
+        assert got[5:] == (False, False)
+
+
+def test_script_exit_batched(oracle):
+    M = 1
+    w, q = _scan_setup(oracle, M, 911)
+    ext = [3 * CH + 5, 3 * CH + 6]  # extended rows outside chunk 0
+    is_cyr, is_cjk = _tables(rows_cyr=ext)
+    (v,) = lm_plant.plant(w, oracle, q, [(3 * CH + 6, 0, 12.0)], K)
+    assert 11.5 < v < 13.5
+    kw = dict(is_cyr=is_cyr, is_cjk=is_cjk, cyr_rows=ext)
+    # the session already writes Cyrillic: after chunk 0 the extended rows give 12 on a Cyrillic token,
+    # >= 11.5, so the scan ends after one chunk with that row (fp32 value)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             has_cyr=True, **kw)
+    assert (n, stp, int(bi[0]), hc) == (1, 1, 3 * CH + 6, True) and bv[0] == np.float32(v)
+    # no script in the session: the row is found when chunk 3 is scanned (fp16 value), and chunk 3's
+    # threshold 11.5 ends the scan there; that best token then sets the session's flag (for later
+    # tokens: the extended rows run only after chunk 0)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH, **kw)
+    assert (n, stp, int(bi[0]), hc) == (4, 1, 3 * CH + 6, True) and bv[0] == np.float32(np.float16(v))
+    # the full scan is required: no script exit, and with 5 chunks no checkpoint (they start at chunk 6)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             has_cyr=True, require_full=True, **kw)
+    assert (n, stp, int(bi[0])) == (5, 0, 3 * CH + 6)
+
+
+def test_script_exit_needs_an_in_script_best_or_20(oracle):
+    w, q = _scan_setup(oracle, 1, 912)
+    ext = [4 * CH + 1]
+    is_cyr, is_cjk = _tables(rows_cjk=ext)
+    # chunk 0 holds 15 on a token of no script: the session has CJK (set below by chunk 0's best), so
+    # the extended rows run, but the best is not CJK and 15 < 20: no script exit; 15 < 19.5 and 16,
+    # >= 13.5 at chunk 2
+    (v0, v1) = lm_plant.plant(w, oracle, q, [(900, 0, 15.0), (4 * CH + 1, 0, 11.0)], K)
+    is_cjk[900] = 0
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             is_cyr=is_cyr, is_cjk=is_cjk, cjk_rows=ext,
+                                                             has_cjk=True)
+    assert (n, stp, int(bi[0])) == (3, 1, 900)
+    # chunk 0's best is itself a CJK token: it sets the session's flag, the extended rows run, and
+    # 15 on an in-script token clears 11.5
+    is_cjk[900] = 1
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             is_cyr=is_cyr, is_cjk=is_cjk, cjk_rows=ext)
+    assert (n, stp, int(bi[0]), hj) == (1, 1, 900, True)
+
+
+def test_script_exit_batch1_rule_is_10_5(oracle):
+    w, q = _scan_setup(oracle, 1, 913)
+    ext = [2 * CH + 40]
+    is_cyr, is_cjk = _tables(rows_cyr=ext)
+    (v,) = lm_plant.plant(w, oracle, q, [(2 * CH + 40, 0, 11.0)], K)
+    assert 10.5 < v < 11.5
+    kw = dict(is_cyr=is_cyr, is_cjk=is_cjk, cyr_rows=ext, has_cyr=True)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             batch1=True, **kw)
+    assert (n, stp, int(bi[0])) == (1, 1, 2 * CH + 40) and bv[0] == np.float32(v)
+    # the batched rule wants 11.5 for an in-script token: the scan goes on to chunk 4 (10.5)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH, **kw)
+    assert (n, stp, int(bi[0])) == (5, 1, 2 * CH + 40)
+
+
+def test_script_rows_then_pruning(oracle):
+    M = 3
+    w, q = _scan_setup(oracle, M, 914)
+    ext = [3 * CH + 100]
+    is_cyr, is_cjk = _tables(rows_cyr=ext + [600])
+    draft = np.array([0, 600, 601], np.uint32)
+    # token 0: candidate 600 (Cyrillic, logit 9 in chunk 0: sets the flag, best == candidate, no pruning
+    # after chunk 0); the extended row gives it 12 on another row -> pruned to 1 active position, and
+    # 12 >= 11.5 on a Cyrillic token ends the scan; tokens 1, 2 keep their chunk-0 bests
+    plan = [(600, 0, 9.0), (3 * CH + 100, 0, 12.0), (601, 1, 2.0), (CH + 50, 2, 13.0)]
+    lm_plant.plant(w, oracle, q, plan, K)
+    bv, bi, n, act, stp, hc, hj = oracle.lm_head_scan_script(q, w, TYPE_Q6_K, V, K, CH, lm_plant.CHUNK_THRESH,
+                                                             draft_ids=draft, is_cyr=is_cyr, is_cjk=is_cjk,
+                                                             cyr_rows=ext)
+    assert (n, stp, act, int(bi[0]), hc) == (1, 1, 1, 3 * CH + 100, True)
+    assert int(bi[2]) != CH + 50  # chunk 1 was never scanned
