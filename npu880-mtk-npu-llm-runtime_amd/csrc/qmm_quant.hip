@@ -68,6 +68,26 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
                     round_to_fp16(v.w), lane, blk, o, nb);
 }
 
+// The same for M >= 16, workgroups placed by token tile: workgroup b runs
+// on XCD b mod 8, and the 16 tokens of one token tile (for one quad of
+// blocks, a wave per block) are consecutive workgroups of one XCD, so the
+// tiles and bh sections' lines, which interleave those 16 tokens, are
+// written through one L2 (M = 512, K = 9728: 11.1 -> 9.3 us).
+__global__ __launch_bounds__(256) void quantize_q8k_tiled_kernel(const float *__restrict__ x, int M, int nb, int nq,
+                                                                 int total, Q8KOut o) {
+    const int per = (int(gridDim.x) + 7) / 8;
+    const int lin = int(blockIdx.x % 8u) * per + int(blockIdx.x / 8u);
+    if (lin >= total) return;
+    const int mi = lin & 15, u = lin >> 4;
+    const int t = u / nq, q = u - t * nq;
+    const int m = 16 * t + mi, j = 4 * q + int(threadIdx.x >> 6);
+    if (m >= M || j >= nb) return;
+    const int lane = threadIdx.x & 63;
+    const size_t blk = size_t(m) * size_t(nb) + size_t(j);
+    const float4 v = reinterpret_cast<const float4 *>(x + blk * 256)[lane];
+    store_q8k_block(round_to_fp16(v.x), round_to_fp16(v.y), round_to_fp16(v.z), round_to_fp16(v.w), lane, blk, o, nb);
+}
+
 // Q8_0: 32-value blocks, 8 lanes each, 8 blocks per wave (flattened).
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x,
                                                             size_t nblk32,
@@ -243,6 +263,12 @@ hipError_t launch_quantize_q8k(const float *x, int M, int K, void *out, hipStrea
     if (skip & kSkipQs) o.qs = nullptr;
     if (skip & kSkipH) o.h = nullptr;
     if (skip & kSkipBs) o.bs = nullptr;
+    if (M >= 16) {
+        const int nb = K / 256, nq = (nb + 3) / 4, total = ((M + 15) / 16) * nq * 16;
+        hipLaunchKernelGGL(quantize_q8k_tiled_kernel, dim3(unsigned((total + 7) / 8 * 8)), dim3(256), 0, s, x, M, nb,
+                           nq, total, o);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(quantize_q8k_kernel, dim3(grid), dim3(256), 0, s, x, nblk, o, K / 256);
     return hipGetLastError();
 }

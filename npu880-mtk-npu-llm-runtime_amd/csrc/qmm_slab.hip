@@ -1,8 +1,9 @@
 // qmm_slab.hip — prefill GEMM (M > 64 tokens) over GGUF-packed k-quant rows
 // (Q4_K, Q5_K, Q6_K) with int8 MFMA, gfx950.
 //
-// Workgroup = 4 waves on a slab of R = 16 RW PR weight rows x T = 16 TW PT
-// tokens; wave (pr, pt) owns RW row tiles x TW token tiles of 16 x 16. The K
+// Workgroup = NW (4 or 8) waves on a slab of R = 16 RW PR weight rows x
+// T = 16 TW PT tokens; wave (pr, pt) owns RW row tiles x TW token tiles of
+// 16 x 16. The K
 // loop walks one 256-value block at a time through PD LDS stages, each filled by direct buffer -> LDS
 // transfers (buffer_load ... lds): the slab's packed weight rows, the
 // tokens' codes from the tiles section of the activation buffer (already in
@@ -34,10 +35,12 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <class F, int RW_, int TW_, int PR_, int PD_>
+template <class F, int RW_, int TW_, int PR_, int PD_, int NW_ = 4, int WPS_ = 1>
 struct SlabCfg {
-    static constexpr int RW = RW_, TW = TW_, PR = PR_, PT = 4 / PR_, PD = PD_;
-    static_assert(PR * PT == 4, "4 waves");
+    static constexpr int NW = NW_;    // waves per workgroup
+    static constexpr int WPS = WPS_;  // waves per SIMD the registers must allow (launch bound)
+    static constexpr int RW = RW_, TW = TW_, PR = PR_, PT = NW_ / PR_, PD = PD_;
+    static_assert(PR * PT == NW, "PR x PT waves");
     static constexpr bool MIN = F::kMin;
     static constexpr int R = 16 * RW * PR;  // weight rows per workgroup
     static constexpr int T = 16 * TW * PT;  // tokens per workgroup
@@ -51,14 +54,15 @@ struct SlabCfg {
     static constexpr int NAI = (T / 16) * 4;              // code transfers (4 KB per token tile)
     static constexpr int NBI = MIN ? (T / 16 * 32 + 63) / 64 : 0;  // bh transfers (512 B per token tile)
     static constexpr int NDI = (T + 63) / 64;                        // scales (4-B transfers)
-    static constexpr int NWW = (NWI + 3) / 4, NAW = NAI / 4, NBW = (NBI + 3) / 4, NDW = (NDI + 3) / 4;
+    static constexpr int NWW = (NWI + NW - 1) / NW, NAW = NAI / NW, NBW = (NBI + NW - 1) / NW,
+                         NDW = (NDI + NW - 1) / NW;
     static constexpr int L = NWW + NAW + NBW + NDW;       // transfers per wave and step
     static constexpr int OFF_A = NWI * 1024;
     static constexpr int OFF_B = OFF_A + NAI * 1024;
     static constexpr int OFF_D = OFF_B + NBI * 1024;
     static constexpr int STAGE = OFF_D + NDI * 256;
     static constexpr int OFF_DUMP = PD * STAGE, LDS = OFF_DUMP + 1024;
-    static_assert(NAI % 4 == 0, "token tiles per workgroup: a multiple of 4 code transfers");
+    static_assert(NAI % NW == 0, "code transfers: a multiple of the waves");
     static_assert((PD - 2) * L <= 63, "vmcnt range");
     static_assert(LDS <= 160 * 1024, "LDS");
 };
@@ -116,7 +120,7 @@ __device__ inline void slab_unpack(const uint8_t *blk, int c, SlabB &o) {
 }
 
 template <class C, class F>
-__global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<F>::T x, int ntg) {
+__global__ __launch_bounds__(64 * C::NW, C::WPS) void slab_kernel(MatGroup grp, typename ActOf<F>::T x, int ntg) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int RW = C::RW, TW = C::TW;
     const int lane = threadIdx.x & 63;
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<
     uint32_t wo[C::NWW], wp[C::NWW], ao[C::NAW], bo[C::NBW > 0 ? C::NBW : 1], dof[C::NDW];
 #pragma unroll
     for (int s = 0; s < C::NWW; ++s) {  // unit pc of row `row`: 16 B from the 16-B boundary at or below its step bytes
-        const int p = (s * 4 + wid) * 64 + lane;
+        const int p = (s * C::NW + wid) * 64 + lane;
         const int row = p / C::WCR, pc = p - row * C::WCR;
         wo[s] = row < C::R ? uint32_t(row) * uint32_t(a.row_bytes) + bl : kFar;
         wp[s] = 16u * uint32_t(pc);
@@ -167,18 +171,18 @@ __global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<
     }
 #pragma unroll
     for (int s = 0; s < C::NAW; ++s) {
-        const int i = s * 4 + wid, tt = i >> 2, h = i & 3;  // token tile, 1-KB quarter
+        const int i = s * C::NW + wid, tt = i >> 2, h = i & 3;  // token tile, 1-KB quarter
         const uint32_t tile = uint32_t(m0 / 16 + tt);
         ao[s] = (tile * uint32_t(nbk)) * 4096u + 1024u * uint32_t(h) + 16u * uint32_t(lane);
     }
 #pragma unroll
     for (int s = 0; s < C::NBW; ++s) {
-        const int p = (s * 4 + wid) * 64 + lane, tt = p >> 5, q = p & 31;
+        const int p = (s * C::NW + wid) * 64 + lane, tt = p >> 5, q = p & 31;
         bo[s] = tt < C::T / 16 ? (uint32_t(m0 / 16 + tt) * uint32_t(nbk)) * 512u + 16u * uint32_t(q) : kFar;
     }
 #pragma unroll
     for (int s = 0; s < C::NDW; ++s) {
-        const int p = (s * 4 + wid) * 64 + lane;
+        const int p = (s * C::NW + wid) * 64 + lane;
         dof[s] = p < C::T ? uint32_t(m0 + p) * uint32_t(nbk) * 4u : kFar;
     }
     const uint32_t wrange = uint32_t(rw.z), arange = uint32_t(ra.z), brange = uint32_t(rb.z), drange = uint32_t(rd.z);
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<
         const uint32_t base = lds0 + uint32_t(sg * C::STAGE), dump = lds0 + uint32_t(C::OFF_DUMP);
 #pragma unroll
         for (int s = 0; s < C::NWW; ++s) {
-            const int i = s * 4 + wid;
+            const int i = s * C::NW + wid;
             const uint32_t dst = i < C::NWI ? base + uint32_t(i * 1024) : dump;
             if constexpr (C::ALIGNED) {
                 dma16s(rw, wo[s], live ? uint32_t(st) * uint32_t(C::SB) : wrange, dst);
@@ -199,15 +203,16 @@ __global__ __launch_bounds__(256) void slab_kernel(MatGroup grp, typename ActOf<
         }
 #pragma unroll
         for (int s = 0; s < C::NAW; ++s)
-            dma16s(ra, ao[s], live ? uint32_t(st) * 4096u : arange, base + uint32_t(C::OFF_A + (s * 4 + wid) * 1024));
+            dma16s(ra, ao[s], live ? uint32_t(st) * 4096u : arange,
+                   base + uint32_t(C::OFF_A + (s * C::NW + wid) * 1024));
 #pragma unroll
         for (int s = 0; s < C::NBW; ++s) {
-            const int i = s * 4 + wid;
+            const int i = s * C::NW + wid;
             dma16s(rb, bo[s], live ? uint32_t(st) * 512u : brange, i < C::NBI ? base + uint32_t(C::OFF_B + i * 1024) : dump);
         }
 #pragma unroll
         for (int s = 0; s < C::NDW; ++s) {
-            const int i = s * 4 + wid;
+            const int i = s * C::NW + wid;
             dma4s(rd, dof[s], live ? uint32_t(st) * 4u : drange, i < C::NDI ? base + uint32_t(C::OFF_D + i * 256) : dump);
         }
     };
@@ -339,7 +344,7 @@ static hipError_t launch_slab_t(const MatArgs *tasks, int n, const typename ActO
     const int ntg = (tasks[0].M + C::T - 1) / C::T;
     const int G = g.wg0[n] * ntg;
     const unsigned grid = unsigned((G + 7) / 8 * 8);
-    hipLaunchKernelGGL((slab_kernel<C, F>), dim3(grid), dim3(256), size_t(C::LDS), s, g, x, ntg);
+    hipLaunchKernelGGL((slab_kernel<C, F>), dim3(grid), dim3(64 * C::NW), size_t(C::LDS), s, g, x, ntg);
     return hipGetLastError();
 }
 
@@ -360,16 +365,25 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
         if (aligned && ((reinterpret_cast<uintptr_t>(tasks[i].w) | tasks[i].row_bytes) & 15)) return hipErrorNotSupported;
         if (size_t(tasks[i].N) * tasks[i].row_bytes + 16 >= (size_t(1) << 31)) return hipErrorNotSupported;
     }
-    // 64 rows x 64 tokens, two workgroups per CU (measured best at M = 512
-    // where those slabs give at least two workgroups per CU: gate 9728 x
-    // 2560, QKV 6144 x 2560); 64 x 32 (three or four per CU) where they give
-    // fewer (O 2560 x 4096 at M = 512: 28.5 -> 23.9 us, down 2560 x 9728:
-    // 77.8 -> 75.3 us). Measured slower at M = 512: 32 x 128, 32 x 64, 64 x 16,
-    // 32 x 32, three stages, and two row tiles per wave.
-    int slabs = 0;
-    for (int i = 0; i < n; ++i) slabs += (tasks[i].N + 63) / 64;
-    //                                  RW TW PR PD
-    if (slabs * ((a.M + 63) / 64) < 2 * mfma_cu_count()) return launch_slab_t<SlabCfg<F, 1, 2, 4, 2>, F>(tasks, n, x, s);
+    // 128 rows x 64 tokens in 8 waves where those slabs give at least four
+    // workgroups per CU: two fit a CU (2 x 74 KB of LDS, <= 128 VGPRs), so
+    // four waves per SIMD, and the 64 tokens' codes staged once per 128 rows
+    // (gate + up 2 x 9728 x 2560 at M = 512: 87.5 -> 79.1 us). Else 64 x 64
+    // (two workgroups per CU; QKV 6144 x 2560: 35.7 us against 48.1 for
+    // 128 x 64 on its 384 slabs), and 64 x 32 (three or four per CU) where
+    // 64 x 64 gives fewer than two (O 2560 x 4096 at M = 512: 28.5 -> 23.9 us,
+    // down 2560 x 9728: 77.8 -> 75.3 us). Measured slower at M = 512: 128 x 128
+    // in 8 waves, 128 x 32 in 8 waves, 32 x 128, 32 x 64, 64 x 16, 32 x 32,
+    // three stages, and two row tiles per wave.
+    int slabs = 0, slabs128 = 0;
+    for (int i = 0; i < n; ++i) {
+        slabs += (tasks[i].N + 63) / 64;
+        slabs128 += (tasks[i].N + 127) / 128;
+    }
+    const int tg64 = (a.M + 63) / 64, cus = mfma_cu_count();
+    //                                                         RW TW PR PD NW WPS
+    if (slabs128 * tg64 >= 4 * cus) return launch_slab_t<SlabCfg<F, 1, 4, 8, 2, 8, 4>, F>(tasks, n, x, s);
+    if (slabs * tg64 < 2 * cus) return launch_slab_t<SlabCfg<F, 1, 2, 4, 2>, F>(tasks, n, x, s);
     return launch_slab_t<SlabCfg<F, 1, 4, 4, 2>, F>(tasks, n, x, s);
 }
 

@@ -389,3 +389,38 @@ def test_task_groups_one_launch(ctx, oracle, M):
         check_outputs(ctx.d2h(yb, np.float32, (M, n)), refs[i], f"task {i}")
     for b in [xb] + wbs + ybs + [r for r in rbs if r is not None]:
         ctx.free(b)
+
+
+@pytest.mark.parametrize("M,K,specs,residual", [(512, 2560, (9728, 9728), False), (300, 512, (13200, 13107), True)])
+def test_prefill_eight_wave_slabs(ctx, oracle, M, K, specs, residual):
+    """Task groups with at least four 128 x 64 slabs per CU take the 8-wave
+    prefill workgroups: the FFN's gate + up at M = 512, and ragged tasks
+    (partial row slabs and token groups, a residual) at M = 300; one row of
+    every 16-row tile of each task against the oracle, all tokens."""
+    say(f"prefill 8-wave slabs M={M} K={K} tasks={specs}")
+    x = synth.activations(M, K, seed=3500 + M)
+    xb = ctx.upload(x)
+    bufs, tasks, hosts, res_h = [xb], [], [], []
+    for i, n in enumerate(specs):
+        w = synth.weights(TYPE_Q4_K, n, K, seed=3501 + i + M)
+        wb, yb = ctx.weight_upload(w, TYPE_Q4_K, n, K), ctx.malloc(M * n * 4)
+        rh = synth.activations(M, n, seed=3520 + i) if residual and i == 1 else None
+        rb = ctx.upload(rh) if rh is not None else None
+        bufs += [b for b in (wb, yb, rb) if b is not None]
+        tasks.append(qmm_hip.MatrixTask(wb, TYPE_Q4_K, n, K, yb, n, residual=rb, res_stride=n if rh is not None else 0))
+        hosts.append(w)
+        res_h.append(rh)
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    rbytes = synth.row_bytes(TYPE_Q4_K, K)
+    for t, w, rh in zip(tasks, hosts, res_h):
+        n = t.rows
+        rows = np.array([16 * i + (5 * i) % 16 for i in range(n // 16)] + [n - 1])
+        got = ctx.d2h(t.dst, np.float32, (M, n))[:, rows]
+        sub = w.reshape(n, rbytes)[rows].reshape(-1)
+        ref = oracle.gemm_multi(x, [dict(w=sub, type=TYPE_Q4_K, rows=rows.size)])[0]
+        if rh is not None:
+            ref = ref + rh[:, rows]
+        check_outputs(got, ref, f"8-wave slabs task of {n} rows")
+    for b in bufs:
+        ctx.free(b)
