@@ -719,8 +719,9 @@ def bench_lm_head(ctx, args):
     GEMV, the GEMV with its argmax epilogue, and the chunked scan
     (24832-row chunks, chunk_thresh) on a tensor whose chunk 0 holds a row
     at logit 25 (the scan stops after chunk 0) against the same scan
-    without thresholds and with a threshold at every chunk that no chunk
-    meets (all 7 chunks either way)."""
+    without thresholds (one launch) and with a threshold at every chunk that
+    no chunk meets (chunk 0's launch, then the later chunks in one launch;
+    all 7 chunks either way)."""
     N, K = synth.GEMV_Q6K_LMHEAD["N"], synth.GEMV_Q6K_LMHEAD["K"]
     rb = synth.row_bytes(synth.TYPE_Q6_K, K)
     a = Acts(ctx, 1, K, seed=21)

@@ -250,7 +250,12 @@ typedef struct {
  * position's best reaches the chunk's threshold. A chunk after the stop
  * reads no weights. Chunks after which nothing is decided (no checkpoint,
  * no drafts to prune) share one launch with the chunks that follow them, up
- * to the next deciding chunk: the same results, fewer launches.
+ * to the next deciding chunk: the same results, fewer launches. At M = 1
+ * with three or more such launches, the first runs alone and all later
+ * chunks run as one launch that applies the first's decision before it
+ * reads any weight, then a one-workgroup step decides the later chunks in
+ * order from their bests: the same results (a stop after the first launch
+ * reads nothing more; later checkpoints stop nothing in flight).
  * scan_state (device int32[4]) receives: chunks read,
  * active positions, 1 if the scan stopped early, 0. The script-specific
  * extended rows (E:11194-11240) are the caller's: qmm_eval_rows_argmax. */

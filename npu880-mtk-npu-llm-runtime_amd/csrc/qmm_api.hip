@@ -46,6 +46,7 @@ struct qmm_context {
     size_t act_cap = 0;
     void *lm = nullptr;   // LM-head epilogue scratch: logits | argmax slices | gathered rows
     size_t lm_cap = 0;
+    qmm::ScanFold *fold = nullptr;  // the one-launch scan's state (cleared once, then by every scan's last step)
     bool capturing = false;
     // Instantiated graphs still alive (qmm_graph_end .. qmm_graph_destroy):
     // while any is, a buffer that must grow is replaced but not freed — the
@@ -129,6 +130,22 @@ int ensure_act(qmm_context *ctx, size_t bytes) {
 }
 
 int ensure_lm(qmm_context *ctx, size_t bytes) { return grow(ctx, ctx->lm, ctx->lm_cap, bytes, "LM-head scratch"); }
+
+// the one-launch scan's state: allocated once (outside a capture) and
+// cleared by a kernel on the context's stream; false where it cannot be
+// (the caller then takes the per-chunk launches)
+bool ensure_fold(qmm_context *ctx) {
+    if (ctx->fold) return true;
+    if (ctx->capturing) return false;
+    void *p = nullptr;
+    if (hipMalloc(&p, sizeof(qmm::ScanFold)) != hipSuccess) return false;
+    if (qmm::launch_scan_fold_clear(static_cast<qmm::ScanFold *>(p), ctx->stream) != hipSuccess) {
+        (void)hipFree(p);
+        return false;
+    }
+    ctx->fold = static_cast<qmm::ScanFold *>(p);
+    return true;
+}
 
 void free_retired(qmm_context *ctx) {
     if (ctx->retired.empty()) return;
@@ -543,6 +560,7 @@ int qmm_destroy(qmm_context *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->lm) (void)hipFree(ctx->lm);
+    if (ctx->fold) (void)hipFree(ctx->fold);
     for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
@@ -571,6 +589,7 @@ int qmm_reserve(qmm_context *ctx, int max_M, int max_K) {
     if (!ctx || max_M <= 0 || max_K <= 0) return fail(ctx, QMM_EINVAL, "bad reserve size");
     int rc = use_device(ctx);
     if (rc) return rc;
+    (void)ensure_fold(ctx);  // (small; a later scan retries where this fails)
     return ensure_act(ctx, std::max(qmm::Q8KLayout(max_M, max_K).total + qmm::Q80Layout(max_M, max_K).total,
                                     ffn_scratch_bytes(max_K)));
 }
@@ -1001,10 +1020,10 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
     uint8_t *work = scr + cand_b + cdot_b;
     const uint8_t *wb = static_cast<const uint8_t *>(w_lm);
     PendingStep pend;
+    hipError_t e;
     // At batch 1 with nothing evaluated ahead of the chunks, the first chunk's
     // launch seeds the scan's state (where it takes the fused argmax grid)
     // instead of a launch of its own.
-    hipError_t e;
     {
         qmm::Q8KView xk;
         qmm::Q80View x0;
@@ -1073,7 +1092,55 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
     pend.bufs[0] = work + lm_scratch(M, chunk, rb, false, false).total();
     pend.bufs[1] = static_cast<uint8_t *>(pend.bufs[0]) + part_b;
     qmm::ScanStep last{};
-    for (const auto &gr : groups) {
+    // At batch 1 with three or more launches' worth of groups, the groups
+    // after the first run as one launch (launch_gemv_scan): it applies the
+    // first group's step before any weight request (a stop there ends the
+    // scan, as the per-group launches would), then reads every later chunk,
+    // folding each chunk's best, and one workgroup decides those chunks in
+    // order afterwards — the same results with two launches in place of one
+    // per later group (the later checkpoints stop nothing in flight).
+    const int cf = groups.size() >= 3 ? groups[1].first : ce;  // the folded chunks: [cf, ce)
+    const bool fold_shape = M == 1 && groups.size() >= 3 && ce - cf <= qmm::kFoldChunks &&
+                            params->chunk_rows % (4 * qmm::kScanRows) == 0;
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+        const auto &gr = groups[gi];
+        if (gi == 1 && fold_shape && (!pend.on || pend.nparts <= 1024)) {
+            qmm_matrix_task tf = tc;
+            const int64_t r0 = int64_t(cf) * params->chunk_rows;
+            tf.w_base = wb + size_t(r0) * rb;
+            tf.rows = int(std::min<int64_t>(int64_t(ce) * params->chunk_rows, vocab_rows) - r0);
+            tf.dst_stride = size_t(tf.rows);
+            qmm::ScanPlan plan{};
+            plan.nch = ce - cf;
+            plan.chunk_groups = params->chunk_rows / qmm::kScanRows;
+            plan.row_base = uint32_t(r0);
+            for (int c = cf; c < ce; ++c) {
+                if (params->n_thresholds > 0 && c >= params->first_checkpoint) plan.ckpt |= 1ull << (c - cf);
+                plan.thresh[c - cf] = c < params->n_thresholds ? params->thresholds[c] : -1e30f;  // E:11245-11246
+            }
+            plan.best_val = best_val;
+            plan.best_id = best_id;
+            plan.st = scan_state;
+            plan.c0 = cf;
+            qmm::Q8KView xk;
+            qmm::Q80View x0;
+            act_views(q8k, q80, 1, K, xk, x0);
+            qmm::PrevStep pre{};
+            if (pend.on)
+                pre = qmm::PrevStep{pend.part, pend.nparts, pend.row_base, pend.thresh, pend.checkpoint ? 1 : 0,
+                                    pend.c, best_val, best_id, scan_state};
+            const qmm::MatArgs af = mat_args(tf, 1, K, scan_state);
+            if (qmm::launch_gemv_scan(tf.type, af, xk, pend.x32, pend.gamma, plan, pre, false, ctx->stream) ==
+                    hipSuccess &&
+                ensure_fold(ctx)) {
+                plan.fold = ctx->fold;
+                pend.on = false;
+                e = qmm::launch_gemv_scan(tf.type, af, xk, pend.x32, pend.gamma, plan, pre, true, ctx->stream);
+                if (e != hipSuccess) return hip_fail(ctx, e, "scan launch");
+                e = qmm::launch_scan_fold_final(plan, ctx->stream);
+                return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "scan step launch");
+            }
+        }
         const int c = gr.second;  // the group's last chunk: its threshold and checkpoint
         const int r0 = gr.first * params->chunk_rows;
         qmm_matrix_task t = tc;

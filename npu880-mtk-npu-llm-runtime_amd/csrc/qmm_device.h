@@ -213,6 +213,44 @@ struct AmaxOut {
     uint32_t id_limit;
     PrevStep pre;
 };
+// The batch-1 chunk scan's later chunks in one launch (qmm_lm_head_scan at
+// M = 1 with checkpoints): chunk 0 runs as its own launch, whose step the
+// later chunks' launch applies first (every workgroup, from chunk 0's
+// partials, before any weight request: a stop there ends the scan at
+// once); then each wave contributes its best over its rows of every later
+// chunk (a DPP max over the wave, an LDS max over the workgroup, one
+// device-scope max per workgroup and chunk into one of 16 words, none of
+// them waited for), and one workgroup decides those chunks in order from
+// the word keys (scan_fold_final_kernel): the chunks after chunk 0 are all
+// read, their decisions taken at the end. Cleared (scan_fold_clear_kernel)
+// before first use and by every final step for the next scan.
+constexpr int kFoldChunks = 64;  // chunks per launch at most
+constexpr int kFoldWords = 16;   // words per chunk
+constexpr int kScanRows = 4;     // rows per row group of the batch-1 persistent grid (kGemvR)
+// a key on a 256-B line of its own (the device's atomics serialize per line)
+struct FoldWord {
+    unsigned long long key;  // best key (best_key) of the word's workgroups
+    unsigned int pad[62];
+};
+struct ScanFold {
+    FoldWord wd[kFoldWords][kFoldChunks];  // word w of chunk c; a chunk's words 16 KB apart
+};
+struct ScanPlan {
+    ScanFold *fold;
+    int nch;                   // chunks of the launch
+    int chunk_groups;          // row groups per chunk
+    uint32_t row_base;         // the launch's first row in the tensor (row ids of the result)
+    unsigned long long ckpt;   // bit c: chunk c is a checkpoint
+    float thresh[kFoldChunks];
+    float *best_val;
+    uint32_t *best_id;
+    int32_t *st;
+    int c0;                    // the launch's first chunk in the scan (the state's chunk count)
+};
+hipError_t launch_gemv_scan(uint32_t type, const MatArgs &a, const Q8KView &xk, const float *x32, const float *gamma,
+                            const ScanPlan &plan, const PrevStep &pre, bool launch, hipStream_t s);
+hipError_t launch_scan_fold_final(const ScanPlan &plan, hipStream_t s);
+hipError_t launch_scan_fold_clear(ScanFold *fold, hipStream_t s);
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                               const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
                               const PrevStep &pre = PrevStep{}, bool launch = true, const float *x32 = nullptr,
@@ -385,6 +423,22 @@ __device__ inline Best wave_best(Best b) {
         b = better(b, o);
     }
     return b;
+}
+
+// A Best as a 64-bit key whose unsigned order is better()'s: the value's
+// bits in an order-preserving form above, the row's complement below (an
+// earlier row wins a tie); 0 is the empty Best. NaN never enters.
+__device__ inline unsigned long long best_key(Best b) {
+    if (b.i == kNone) return 0ull;
+    uint32_t u = __builtin_bit_cast(uint32_t, b.v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - b.i);
+}
+__device__ inline Best key_best(unsigned long long k) {
+    if (k == 0ull) return Best{-INFINITY, kNone};
+    uint32_t u = uint32_t(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    return Best{__builtin_bit_cast(float, u), 0xFFFFFFFFu - uint32_t(k & 0xFFFFFFFFu)};
 }
 
 // a scan that has stopped (uniform: every thread reads the same word)

@@ -396,12 +396,41 @@ __global__ __launch_bounds__(256) void gemv_mixed_kernel(MatGroup grp, const flo
 // the row before its RMSNorm, gamma the norm's weights; the workgroup forms
 // the normed fp16 row (rmsnorm_fp16_rows_fast, E:4264-4314, the same values
 // as rmsnorm_q8k_kernel) and quantizes that.
-template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false, bool RMS = false>
+// ------------------------------------- the chunk scan's fold (SCAN mode)
+// the largest key over the wave (returned in every lane): DPP row shifts
+// within each 16-lane row, then the row broadcasts, the result in lane 63
+__device__ inline unsigned long long wave_max_key(unsigned long long k) {
+    uint32_t hi = uint32_t(k >> 32), lo = uint32_t(k);
+    auto step = [&](auto ctrl, auto rows) __attribute__((always_inline)) {
+        constexpr int C = decltype(ctrl)::value, RM = decltype(rows)::value;
+        // lanes with no source (or outside the row mask) see the key 0, the smallest
+        const uint32_t h2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(hi), C, RM, 0xF, false));
+        const uint32_t l2 = uint32_t(__builtin_amdgcn_update_dpp(0, int(lo), C, RM, 0xF, false));
+        const bool take = h2 > hi || (h2 == hi && l2 > lo);
+        hi = take ? h2 : hi;
+        lo = take ? l2 : lo;
+    };
+    using std::integral_constant;
+    step(integral_constant<int, 0x111>{}, integral_constant<int, 0xF>{});  // row_shr:1
+    step(integral_constant<int, 0x112>{}, integral_constant<int, 0xF>{});  // row_shr:2
+    step(integral_constant<int, 0x114>{}, integral_constant<int, 0xF>{});  // row_shr:4
+    step(integral_constant<int, 0x118>{}, integral_constant<int, 0xF>{});  // row_shr:8
+    step(integral_constant<int, 0x142>{}, integral_constant<int, 0xA>{});  // row_bcast:15 into rows 1, 3
+    step(integral_constant<int, 0x143>{}, integral_constant<int, 0xC>{});  // row_bcast:31 into rows 2, 3
+    hi = uint32_t(__builtin_amdgcn_readlane(int(hi), 63));
+    lo = uint32_t(__builtin_amdgcn_readlane(int(lo), 63));
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+template <class F, int R, int U, bool FUSED, int NC, bool AMAX, bool X16 = false, bool RMS = false, bool SCAN = false>
 __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a, const float *__restrict__ x32,
                                                                       Q8KView prek, Q80View pre0, AmaxOut am,
                                                                       int wgi, int nwg,
-                                                                      const float *__restrict__ gamma = nullptr) {
+                                                                      const float *__restrict__ gamma = nullptr,
+                                                                      const ScanPlan *sp = nullptr) {
     static_assert(!RMS || (FUSED && !X16), "the RMSNorm fill takes an fp32 row");
+    static_assert(!(SCAN && AMAX), "the scan folds its chunk bests instead of writing partials");
+    constexpr bool STEP = AMAX || SCAN;  // a scan chunk's launch: the previous chunk's step first
     extern __shared__ __align__(16) uint8_t lds[];
     static_assert(F::kStaged, "the persistent kernel stages its rows in LDS");
     constexpr int G = F::G, SLOTS = 64 / G, NST = stage_chunks<F, U>();
@@ -451,7 +480,7 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     // at batch 1 seeds its state instead (E:11138-11141): nothing in this
     // launch reads it, the next launch does.
     Best pb4[4];
-    if constexpr (AMAX) {
+    if constexpr (STEP) {
         if (am.pre.init && wgi == 0 && threadIdx.x == 0) {
             am.pre.best_val[0] = -1e30f;
             am.pre.best_id[0] = 0;
@@ -486,7 +515,7 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     [[maybe_unused]] XPre gp;
     if constexpr (RMS)
         if (x_has(0, K)) x_load(gamma, K, x_chunk(0, K), gp);
-    if constexpr (AMAX) {
+    if constexpr (STEP) {
         if (am.pre.part) {
             __shared__ Best psh[4];
             __shared__ int pstop;
@@ -530,6 +559,14 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     if constexpr (X16) x16_fill<q80, std::is_same_v<F, FmtQ6K4>>(x16q, K, act);
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
+    // SCAN: the workgroup's per-chunk best and contribution count
+    [[maybe_unused]] __shared__ unsigned long long lkey[SCAN ? kFoldChunks : 1];
+    [[maybe_unused]] __shared__ unsigned lcnt[SCAN ? kFoldChunks : 1];
+    if constexpr (SCAN)
+        if (threadIdx.x < kFoldChunks) {
+            lkey[threadIdx.x] = 0ull;
+            lcnt[threadIdx.x] = 0u;
+        }
     lds_barrier();
     // 3. groups. With 4 lanes per block (R = 1, 2 or 4 rows of 16 / R lane
     // groups each), a row's GPR lane groups take its blocks in consecutive
@@ -545,7 +582,24 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     constexpr int GPR = CHAIN ? SLOTS / R : 1;
     const int bpg = (nb + GPR - 1) / GPR;
     [[maybe_unused]] const int adv = SLOTS % nb;
-    Best wb{-INFINITY, kNone};  // AMAX: the wave's running (max, first row)
+    Best wb{-INFINITY, kNone};  // AMAX: the wave's running (max, first row); SCAN: of the current chunk
+    [[maybe_unused]] int ccur = 0;
+    // SCAN: this wave's contribution to chunk c (its best over its rows of
+    // the chunk, or nothing); the workgroup's fourth folds the workgroup's
+    // best into word wgi % 16 of the chunk (a device-scope max nothing waits
+    // for: the final step reads the words after the launch)
+    [[maybe_unused]] auto contribute = [&](int c) __attribute__((always_inline)) {
+        const unsigned long long k = wave_max_key(best_key(wb));
+        if (lane == 0) {
+            (void)__hip_atomic_fetch_max(&lkey[c], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const unsigned n = __hip_atomic_fetch_add(&lcnt[c], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (n == 3u)
+                (void)__hip_atomic_fetch_max(&sp->fold->wd[wgi % kFoldWords][c].key,
+                                             __hip_atomic_load(&lkey[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        wb = Best{-INFINITY, kNone};
+    };
     for (; gw < ngroups; gw += stride) {
         const int row0 = gw * R;
         const int nrows = min(R, a.N - row0);
@@ -561,6 +615,10 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
         // the next group, in flight during the math (none for a wave's last:
         // a clamped duplicate would cost the address units as much as a new one)
         if (gw + stride < ngroups) stage_load(gw + stride);
+        if constexpr (SCAN) {  // entering a later chunk: the chunks left behind (while the next bytes travel)
+            const int cg = gw / sp->chunk_groups;
+            while (ccur < cg) contribute(ccur++);
+        }
         float acc = 0.0f;
         int orow = lane;  // the row (of the group) this lane's acc belongs to
         bool wr = lane < nrows;
@@ -641,13 +699,15 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
             if (a.res) acc = acc + a.res[row];
             if constexpr (AMAX)
                 if (am.ids && am.ids[row] >= am.id_limit) acc = -1e30f;  // a row past the tensor (E:11150)
-            a.y[row] = acc;
-            if constexpr (AMAX) {
+            if constexpr (!SCAN) a.y[row] = acc;
+            if constexpr (AMAX || SCAN) {
                 const float v = am.round16 ? round_to_fp16(acc) : acc;  // as the argmax kernels compare
                 if (v == v) wb = better(wb, Best{v, uint32_t(row)});
             }
         }
     }
+    if constexpr (SCAN)
+        while (ccur < sp->nch) contribute(ccur++);
     if constexpr (AMAX) {  // one partial per workgroup (per wave was slower: 4x the partials to combine)
         __shared__ Best wsb[4];
         wb = wave_best(wb);
@@ -731,6 +791,21 @@ __global__ __launch_bounds__(256) void gemv_argmax_rms_kernel(MatArgs a, const f
                                                               int(gridDim.x), gamma);
 }
 
+// The batch-1 chunk scan's later chunks in one launch: the persistent
+// argmax GEMV over all the launch's chunks, the previous chunk's step first
+// (pre), each wave folding its chunk bests as it moves on (SCAN mode
+// above); a prequantized row, or (RMS) the row before its norm.
+// (three waves per SIMD: the persistent grid puts up to three workgroups on a CU)
+template <class F, int NC, bool RMS>
+__global__ __launch_bounds__(256, 3) void gemv_scan_kernel(MatArgs a, const float *__restrict__ x32,
+                                                        const float *__restrict__ gamma, Q8KView prek, ScanPlan sp,
+                                                        PrevStep pre) {
+    AmaxOut am{};
+    am.round16 = 1;  // chunk logits compare as fp16 (E:11175)
+    am.pre = pre;
+    gemv_persist_wg<F, kGemvR, 3, RMS, NC, false, false, RMS, true>(a, x32, prek, Q80View{}, am, int(blockIdx.x),
+                                                                    int(gridDim.x), gamma, &sp);
+}
 
 // ------------------------------------------- 2..4 tokens, batch-1 shape
 // The persistent kernel's structure for 2 <= M <= MT <= 4 tokens on a
@@ -966,6 +1041,45 @@ static hipError_t launch_gemv_argmax_t(const MatArgs &a, const Q8KView &xk, cons
             return hipGetLastError();
         });
     return launch_gemv_persist_t<F, R, U, true>(a, nullptr, xk, x0, lds, wgs, s, am);
+}
+
+// The one-launch scan over the persistent grid of launch_gemv_argmax;
+// NotSupported (nothing launched) where that grid does not apply or the
+// chunks do not fall on whole quads of row groups. launch = false: the check
+// alone.
+static_assert(kScanRows == kGemvR, "the scan's chunks are counted in the persistent grid's row groups");
+template <class F>
+static hipError_t launch_gemv_scan_t(const MatArgs &a, const Q8KView &xk, const float *x32, const float *gamma,
+                                     const ScanPlan &sp, const PrevStep &pre, bool launch, hipStream_t s) {
+    constexpr int R = kGemvR, U = 3;
+    const int nb = a.K / F::QK, cus = cu_count();
+    const int wg0 = ((a.N + R - 1) / R + 3) / 4;
+    if (R * nb > (64 / F::G) * U || (gamma && !x32) || (!gamma && !xk.qs)) return hipErrorNotSupported;
+    if (sp.nch < 1 || sp.nch > kFoldChunks || sp.chunk_groups <= 0 || sp.chunk_groups % 4) return hipErrorNotSupported;
+    const int wgs = wg0 < 2 * cus ? wg0 : persist_grid(wg0, cus);
+    if (pre.part && pre.nparts > 1024) return hipErrorNotSupported;  // (the step reads at most 1024 partials)
+    if (!launch) return hipSuccess;
+    const size_t lds = gemv_lds_bytes_t<F, R, U>(a.K);
+    return with_stage_chunks<F, U>(R * nb, [&](auto nc) {
+        constexpr int NC = decltype(nc)::value;
+        if (gamma)
+            hipLaunchKernelGGL((gemv_scan_kernel<F, NC, true>), dim3(unsigned(wgs)), dim3(256), lds, s, a, x32, gamma,
+                               xk, sp, pre);
+        else
+            hipLaunchKernelGGL((gemv_scan_kernel<F, NC, false>), dim3(unsigned(wgs)), dim3(256), lds, s, a, x32, gamma,
+                               xk, sp, pre);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_gemv_scan(uint32_t type, const MatArgs &a, const Q8KView &xk, const float *x32, const float *gamma,
+                            const ScanPlan &plan, const PrevStep &pre, bool launch, hipStream_t s) {
+    switch (type) {
+        case kQ4_K: return launch_gemv_scan_t<FmtQ4K4>(a, xk, x32, gamma, plan, pre, launch, s);
+        case kQ5_K: return launch_gemv_scan_t<FmtQ5K4>(a, xk, x32, gamma, plan, pre, launch, s);
+        case kQ6_K: return launch_gemv_scan_t<FmtQ6K4>(a, xk, x32, gamma, plan, pre, launch, s);
+        default: return hipErrorNotSupported;
+    }
 }
 
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,

@@ -401,3 +401,40 @@ def test_scan_in_a_row(ctx, oracle):
     _same(*_scan(ctx, oracle, 1, 1024, [(2 * 4095 + 7, 0, 14.0)], T, CH=4095), 3, 1, 1)
     _same(*_scan(ctx, oracle, 1, 1025, [(2 * 1024 + 5, 0, 14.0)], T, CH=1024), 3, 1, 1)
     _same(*_scan(ctx, oracle, 1, 1026, [(5, 0, 25.0)], T, V=V2, CH=CH2), 1, 1, 1)
+
+
+def test_scan_full_vocabulary_one_launch(ctx, oracle):
+    """The engine's LM head at batch 1: 151936 Q6_K rows of K = 2560 in
+    chunks of 24832 with chunk_thresh at every chunk (the scan's one launch
+    and its final step). A stop after chunk 0 (a larger row in chunk 1 must
+    not be taken), after chunk 3 (a row at 12 clears its 11.5), and all
+    seven chunks with no threshold met, each against the oracle; the three
+    twice on one context (the fold's state is cleared by every scan's last
+    step)."""
+    Vf, CHf, Kf = 151936, 24832, 2560
+    say("lm scan full vocabulary, one launch")
+    w0 = lm_plant.base_tensor(Vf, Kf, 1030)
+    x = synth.activations(1, Kf, seed=1031)
+    q = oracle.quantize_q8k(x)
+    qb = ctx.malloc(ctx.lib.qmm_q8k_bytes(1, Kf))
+    ctx.write_q8k(qb, *q, x16=oracle.f32_to_fp16(x))
+    wb = ctx.malloc(w0.nbytes)
+    bv, bi, st = ctx.malloc(4), ctx.malloc(4), ctx.upload(np.full(4, -7, np.int32))
+    cases = [("chunk0", [(77, 0, 25.0), (CHf + 5, 0, 60.0)], (1, 1, 1), 77),
+             ("chunk3", [(3 * CHf + 11, 0, 12.0)], (4, 1, 1), 3 * CHf + 11),
+             ("never", [(6 * CHf + 2, 0, 9.0)], (7, 1, 0), 6 * CHf + 2)]
+    for rnd in range(2):
+        for name, plan, want, row in cases:
+            w = w0.copy()
+            lm_plant.plant(w, oracle, q, plan, Kf)
+            ctx.h2d(wb, w)
+            ctx.lm_head_scan(qb, None, 1, Kf, wb, TYPE_Q6_K, Vf, CHf, thresholds=lm_plant.CHUNK_THRESH, best_val=bv,
+                             best_id=bi, scan_state=st)
+            ctx.sync()
+            got = (ctx.d2h(bv, np.float32, (1,)), ctx.d2h(bi, np.uint32, (1,)), ctx.d2h(st, np.int32, (4,)))
+            say(f"  round {rnd} {name}: state {list(got[2])}, best {int(got[1][0])}")
+            exp = oracle.lm_head_scan(q, w, TYPE_Q6_K, Vf, Kf, CHf, lm_plant.CHUNK_THRESH)
+            _same(got, exp, *want)
+            assert int(got[1][0]) == row
+    for b in (qb, wb, bv, bi, st):
+        ctx.free(b)
