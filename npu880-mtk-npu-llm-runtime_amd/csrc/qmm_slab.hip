@@ -332,6 +332,398 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void slab_kernel(MatGroup grp, 
     }
 }
 
+// ------------------------------------------------------------ decoded slabs
+// Prefill GEMM with each weight block decoded once per workgroup into int8
+// MFMA tiles in LDS. The slab's RT row tiles are staged packed (buffer -> LDS
+// transfers, PD stages, two blocks ahead); after block j's MFMAs the waves
+// decode block j + 1 into the other of two decoded buffers (per row tile:
+// the two folded int8 planes of each 64-value chunk in MFMA B-operand order,
+// the mins as fp16, d and dmin per row), each wave HC of the slab's 4 RT
+// chunks. Every wave owns TW token tiles: their codes and sums are loaded
+// from the activation buffer into registers (the codes of block j + 1 once
+// block j's last MFMAs are issued), their block scales staged once per
+// workgroup in LDS; it reads the decoded B operands of all RT row tiles. A
+// block's decoding is thus paid once per 16 NW TW tokens, where the slab
+// kernel pays it once per wave's 16 TW. One barrier per block. Per 16 x 16
+// tile and block the integer sums and the fp32 update are the slab kernel's.
+
+template <class F, int RT_, int NW_, int TW_, int WPS_ = 2, int PD_ = 3>
+struct DsCfg {
+    static constexpr int RT = RT_, NW = NW_, TW = TW_, PD = PD_, WPS = WPS_;
+    static constexpr bool MIN = F::kMin;
+    static constexpr int R = 16 * RT, T = 16 * NW * TW;
+    static constexpr int SB = F::BB;
+    static constexpr bool ALIGNED = SB % 16 == 0;
+    static constexpr int WCR = (ALIGNED ? SB / 16 : (SB + 30) / 16) | 1;  // 16-B units per staged row, odd
+    static constexpr int NWI = (R * WCR + 63) / 64;                       // weight transfers (1 KB) per block
+    static constexpr int NWW = (NWI + NW - 1) / NW;
+    static constexpr int PS = NWI * 1024;                                 // one packed stage
+    static constexpr int HC = 4 * RT / NW;                                // chunks a wave decodes per block
+    static_assert(HC >= 1 && 4 * RT % NW == 0, "chunks per wave");
+    // decoded row tile: planes [chunk][high | low] (1 KB each), mins (512 B), (d, dmin) per row
+    static constexpr int OB_M = 8192, OB_D = MIN ? 8704 : 8192, RTB = OB_D + 128;
+    static constexpr int DB = RT * RTB;  // one decoded buffer (two, as static arrays)
+    // dynamic LDS: packed stages | a scratch KB | the tokens' block scales [T][nbk]
+    static constexpr int OFF_DUMP = PD * PS, OFF_DX = OFF_DUMP + 1024;
+    static constexpr int lds_bytes(int nbk) { return OFF_DX + (T * nbk * 4 + 1023) / 1024 * 1024; }
+    static_assert(PD >= 3, "a block is staged two blocks ahead of its use");
+};
+
+// B operands of chunk h (0..3) of a block for lane k-slice c: the high and low
+// folded planes (the layout of split_b)
+template <class F>
+__device__ inline void ds_fold(const uint8_t *blk, int c, int h, uint4 &o1, uint4 &o2) {
+    if constexpr (std::is_same_v<F, MQ6KS>) {
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        auto rd8 = [&](int dw) __attribute__((always_inline)) {
+            const uint32_t w0 = q[dw], w1 = q[dw + 1], w2 = q[dw + 2];
+            return make_uint2(funnel(w1, w0, sh), funnel(w2, w1, sh));
+        };
+        const int hf = h >> 1, ip = h & 1;
+        const uint2 wa = rd8(16 * hf + 2 * c), wb = rd8(16 * hf + 8 + 2 * c), wq = rd8(32 + 8 * hf + 2 * c);
+        const uint2 sw = rd8(48 + 2 * hf);
+        const int cb = 8 * (c >> 1);
+        uint32_t hi[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = 2 * ip + k;
+            const int sc = __builtin_amdgcn_sbfe(int((i & 2) ? sw.y : sw.x), 16 * (i & 1) + cb, 8);
+            const u16x2 sp = __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(0u, uint32_t(sc), 0x01000100u));
+            const u16x2 cp = sp * u16x2{0xFFE0u, 0xFFE0u} + u16x2{128u, 128u};  // 128 - 32 sc
+            const uint2 src = k ? wb : wa;
+            const int hs = 4 * ip + 2 * k;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t v = e ? src.y : src.x, qv = e ? wq.y : wq.x;
+                const uint32_t q6 = ((v >> (4 * ip)) & 0x0F0F0F0Fu) | (((qv >> hs) & 0x03030303u) << 4);
+                fold4(q6, sp, cp, lo[2 * k + e], hi[2 * k + e]);
+            }
+        }
+        o1 = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        o2 = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    } else {
+        const uint4 hd = ld16(blk);
+        uint32_t scp[2], mp[2];
+        scales_k4_packed(hd.y, hd.z, hd.w, scp, mp);
+        const uint32_t scw = (h >> 1) ? scp[1] : scp[0];  // sub-blocks 2h, 2h + 1: bytes 2 (h & 1), + 1
+        const int b0 = 2 * (h & 1);
+        if constexpr (std::is_same_v<F, MQ4KS>) {
+            const uint2 q = ld8(blk + 16 + 32 * h + 8 * c);
+            const uint32_t shw = (scw >> 3) & 0x07070707u, slw = scw & 0x07070707u;
+            const uint32_t lo0 = q.x & 0x0F0F0F0Fu, lo1 = q.y & 0x0F0F0F0Fu;
+            const uint32_t hi0 = (q.x >> 4) & 0x0F0F0F0Fu, hi1 = (q.y >> 4) & 0x0F0F0F0Fu;
+            const u16x2 sh0 = byte_pair(shw, b0), sl0 = byte_pair(slw, b0);
+            const u16x2 sh1 = byte_pair(shw, b0 + 1), sl1 = byte_pair(slw, b0 + 1);
+            o1 = make_uint4(bytes_times(lo0, sh0), bytes_times(lo1, sh0), bytes_times(hi0, sh1), bytes_times(hi1, sh1));
+            o2 = make_uint4(bytes_times(lo0, sl0), bytes_times(lo1, sl0), bytes_times(hi0, sl1), bytes_times(hi1, sl1));
+        } else {  // Q5_K
+            const uint2 qh = ld8(blk + 16 + 8 * c);
+            const uint2 q = ld8(blk + 48 + 32 * h + 8 * c);
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int u = 2 * h + k;
+                const u16x2 sp = byte_pair(scw, b0 + k);
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t v = e ? q.y : q.x, qv = e ? qh.y : qh.x;
+                    const uint32_t q5 = ((v >> (4 * k)) & 0x0F0F0F0Fu) | (((qv >> u) & 0x01010101u) << 4);
+                    fold4(q5, sp, u16x2{128u, 128u}, lo[2 * k + e], hi[2 * k + e]);
+                }
+            }
+            o1 = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            o2 = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        }
+    }
+}
+
+// the row's d, dmin and the lane's mins (fp16, as mins_f16) of a block
+template <class F>
+__device__ inline void ds_row(const uint8_t *blk, int c, half4v &mh, float &d, float &dmin) {
+    if constexpr (std::is_same_v<F, MQ6KS>) {
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(blk) & 3);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(blk - sh);
+        d = fp16_bits_to_f32((q[52] >> (8 * sh)) & 0xFFFFu);
+        dmin = 0.0f;
+        mh = half4v{0, 0, 0, 0};
+    } else {
+        const uint4 hd = ld16(blk);
+        uint32_t scp[2], mp[2];
+        scales_k4_packed(hd.y, hd.z, hd.w, scp, mp);
+        mh = mins_f16(mp, c);
+        d = fp16_bits_to_f32(hd.x & 0xFFFFu);
+        dmin = fp16_bits_to_f32(hd.x >> 16);
+    }
+}
+
+template <class C, class F>
+__global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp, Q8KView x, int ntg) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    // the decoded buffers as two static arrays: the compiler then knows that
+    // a block's decoding (into one) and the previous block's reads (of the
+    // other) are independent and interleaves them
+    __shared__ __align__(16) uint8_t dbuf0[C::DB], dbuf1[C::DB];
+    constexpr int RT = C::RT, TW = C::TW;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nl = lane & 15, cl = lane >> 4;
+
+    // workgroup -> (row slab, token group): consecutive slots of one XCD
+    // take the token groups of one slab
+    const int G = grp.wg0[grp.n] * ntg;
+    const int per = (G + 7) / 8;
+    const int lin = int(blockIdx.x % 8u) * per + int(blockIdx.x / 8u);
+    if (lin >= G) return;
+    const int rg = lin / ntg, tg = lin - rg * ntg;
+    int bx;
+    const MatArgs a = grp.t[group_task(grp, rg, bx)];
+    if (scan_stopped(a.scan)) return;
+    const int n0 = bx * C::R, m0 = tg * C::T;
+    const int K = a.K;
+    const int nbk = K / 256;
+
+    const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
+    const uint32_t bl = uint32_t(wstart & 15);
+    const int rows_valid = min(C::R, a.N - n0);
+    const v4i32 rw = buf_rsrc(reinterpret_cast<const void *>(wstart - bl),
+                              (bl + uint32_t(rows_valid) * uint32_t(a.row_bytes) + 15u) & ~15u);
+    const int ntile = (a.M + 15) / 16;
+    auto rsrc = [](const void *p, uint32_t bytes) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), short(0), int(bytes), 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t ra = rsrc(x.qt, uint32_t(ntile) * 16u * uint32_t(K));
+    const __amdgpu_buffer_rsrc_t rb = rsrc(C::MIN ? static_cast<const void *>(x.bh) : static_cast<const void *>(x.qt),
+                                           C::MIN ? uint32_t(ntile) * 16u * uint32_t(K / 8) : 0u);
+    const uint32_t lds0 = lds_addr(lds);
+
+    // weight transfers: unit pc of staged row `row` (as the slab kernel)
+    uint32_t wo[C::NWW], wp[C::NWW];
+#pragma unroll
+    for (int s = 0; s < C::NWW; ++s) {
+        const int p = (s * C::NW + wid) * 64 + lane;
+        const int row = p / C::WCR, pc = p - row * C::WCR;
+        wo[s] = row < C::R ? uint32_t(row) * uint32_t(a.row_bytes) + bl : kFar;
+        wp[s] = 16u * uint32_t(pc);
+        if constexpr (C::ALIGNED) wo[s] = row < C::R ? wo[s] + wp[s] : kFar;
+    }
+    // (a block past the row reads zeros: the whole range as the uniform offset)
+    const uint32_t wrange = uint32_t(rw.z);
+    auto issue_w = [&](int st) __attribute__((always_inline)) {
+        const bool live = st < nbk;
+        const uint32_t base = lds0 + uint32_t((st % C::PD) * C::PS), dump = lds0 + uint32_t(C::OFF_DUMP);
+#pragma unroll
+        for (int s = 0; s < C::NWW; ++s) {
+            const int i = s * C::NW + wid;
+            const uint32_t dst = i < C::NWI ? base + uint32_t(i * 1024) : dump;
+            if constexpr (C::ALIGNED) {
+                dma16s(rw, wo[s], live ? uint32_t(st) * uint32_t(C::SB) : wrange, dst);
+            } else {
+                const uint32_t v = ((wo[s] + uint32_t(st) * uint32_t(C::SB)) & ~15u) + wp[s];
+                dma16s(rw, wo[s] != kFar ? v : kFar, live ? 0u : wrange, dst);
+            }
+        }
+    };
+
+    // the wave's token tiles: codes (4 KB per tile and block), sums of 16
+    // codes (512 B), scales of the lane's four tokens; tiles past the input
+    // read zeros
+    uint32_t ao[TW], bo[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+        const int tile = m0 / 16 + wid * TW + t;
+        const bool in = tile < ntile;
+        ao[t] = in ? uint32_t(tile) * uint32_t(nbk) * 4096u + 16u * uint32_t(lane) : kFar;
+        bo[t] = in ? uint32_t(tile) * uint32_t(nbk) * 512u + 8u * uint32_t(lane) : kFar;
+    }
+    // the codes of one block (reloaded once the block's MFMAs are issued);
+    // the sums of two
+    uint4 A[TW][4];
+    half4v BH[2][TW];
+    auto load_codes = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                A[t][h] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, ao[t] + 1024u * uint32_t(h), uint32_t(st) * 4096u, 0));
+    };
+    auto load_sums = [&](auto P, int st) __attribute__((always_inline)) {
+        constexpr int p = decltype(P)::value;
+        if constexpr (C::MIN) {
+#pragma unroll
+            for (int t = 0; t < TW; ++t)
+                BH[p][t] = __builtin_bit_cast(half4v, __builtin_amdgcn_raw_buffer_load_b64(rb, bo[t],
+                                                                                             uint32_t(st) * 512u, 0));
+        }
+    };
+    // the scales of the workgroup's tokens, [T][nbk] (contiguous in the
+    // activation buffer; tokens past the input read zeros), staged once
+    const float *sdx = reinterpret_cast<const float *>(lds + C::OFF_DX);
+    {
+        const v4i32 rdd = buf_rsrc(x.d, uint32_t(a.M) * uint32_t(nbk) * 4u);
+        const int n16 = (C::T * nbk * 4 + 1023) / 1024;  // 1-KB transfers
+        for (int i = wid; i < n16; i += C::NW)
+            dma16s(rdd, uint32_t(i * 1024 + 16 * lane), uint32_t(m0) * uint32_t(nbk) * 4u,
+                   lds0 + uint32_t(C::OFF_DX + i * 1024));
+    }
+
+    // decoding: wave w takes chunks [h0, h0 + HC) of row tile rt
+    const int dchunk = wid * C::HC, drt = dchunk >> 2, dh0 = dchunk & 3;
+    auto decode = [&](auto P, int st) __attribute__((always_inline)) {
+        const uint8_t *stage = lds + (st % C::PD) * C::PS;
+        uint8_t *db = (decltype(P)::value ? dbuf1 : dbuf0) + drt * C::RTB;
+        const int rl = drt * 16 + nl;
+        const uint32_t mis =
+            C::ALIGNED ? 0u : (uint32_t(rl) * uint32_t(a.row_bytes) + bl + uint32_t(st) * uint32_t(C::SB)) & 15u;
+        const uint8_t *blk = stage + rl * (C::WCR * 16) + mis;
+#pragma unroll
+        for (int i = 0; i < C::HC; ++i) {
+            const int h = dh0 + i;
+            uint4 o1, o2;
+            ds_fold<F>(blk, cl, h, o1, o2);
+            *reinterpret_cast<uint4 *>(db + (2 * h) * 1024 + 16 * lane) = o1;
+            *reinterpret_cast<uint4 *>(db + (2 * h + 1) * 1024 + 16 * lane) = o2;
+        }
+        if (dh0 == 0) {
+            half4v mh;
+            float d, dmin;
+            ds_row<F>(blk, cl, mh, d, dmin);
+            if constexpr (C::MIN) *reinterpret_cast<half4v *>(db + C::OB_M + 8 * lane) = mh;
+            if (cl == 0) *reinterpret_cast<float2 *>(db + C::OB_D + 8 * nl) = make_float2(d, dmin);
+        }
+    };
+
+    float acc[RT][TW][4];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[r][t][q] = 0.0f;
+
+    // block st: A its codes, BH[P] and DX[P] its sums and scales, the decoded
+    // buffer (st & 1) its B operands (published by the barrier); stage
+    // (st + 1) % PD has landed. MORE: block st + 1 exists (its activations
+    // are loaded and its weights decoded here, after this block's reads of
+    // the decoded buffer)
+    auto step = [&](auto P, int st, auto MORE) __attribute__((always_inline)) {
+        constexpr int p = decltype(P)::value;
+        constexpr bool more = decltype(MORE)::value;
+        wait_vmcnt<0>();  // this wave's transfers of block st + 1 and activations of st
+        lds_barrier();    // every wave's, and block st decoded; decoded buffer (st + 1) & 1 and stage (st + 2) % PD free
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (more) {
+            issue_w(st + 2);  // zeros past the last block
+            load_sums(std::integral_constant<int, p ^ 1>{}, st + 1);
+        }
+        const uint8_t *db = p ? dbuf1 : dbuf0;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint8_t *dr = db + r * C::RTB;
+            uint4 bb[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bb[i] = ld16(dr + i * 1024 + 16 * lane);
+            const float2 dd = *reinterpret_cast<const float2 *>(dr + C::OB_D + 8 * nl);
+            half4v mh;
+            if constexpr (C::MIN) mh = *reinterpret_cast<const half4v *>(dr + C::OB_M + 8 * lane);
+            int4v D1[TW], D2[TW];
+#pragma unroll
+            for (int t = 0; t < TW; ++t) {
+                D1[t] = int4v{0, 0, 0, 0};
+                D2[t] = int4v{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    D1[t] = mfma16x16x64(A[t][h], bb[2 * h], D1[t]);
+                    D2[t] = mfma16x16x64(A[t][h], bb[2 * h + 1], D2[t]);
+                }
+            if constexpr (more)  // once the block's last MFMAs have their operands
+                if (r == RT - 1) load_codes(st + 1);
+            f32x4v Mb[TW];
+            if constexpr (C::MIN) {
+#pragma unroll
+                for (int t = 0; t < TW; ++t)
+                    Mb[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(BH[p][t], mh, f32x4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < TW; ++t)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int S = (D1[t][q] << F::kShift) + D2[t][q];
+                    const float dx = sdx[((wid * TW + t) * 16 + 4 * cl + q) * nbk + st];
+                    if constexpr (C::MIN)
+                        acc[r][t][q] += dx * (dd.x * (float)S - dd.y * Mb[t][q]);  // E:11026 / E:11063
+                    else
+                        acc[r][t][q] += (dd.x * dx) * (float)S;  // E:11101
+                }
+        }
+        if constexpr (more) decode(std::integral_constant<int, p ^ 1>{}, st + 1);
+    };
+
+    // prologue: blocks 0 and 1 staged, block 0's activations, block 0 decoded
+    issue_w(0);
+    if (nbk > 1) issue_w(1);
+    load_codes(0);
+    load_sums(std::integral_constant<int, 0>{}, 0);
+    wait_vmcnt<0>();
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    decode(std::integral_constant<int, 0>{}, 0);
+    using T0 = std::integral_constant<int, 0>;
+    using T1 = std::integral_constant<int, 1>;
+    using Yes = std::true_type;
+    using No = std::false_type;
+    int st = 0;
+    for (; st + 2 < nbk; st += 2) {
+        step(T0{}, st, Yes{});
+        step(T1{}, st + 1, Yes{});
+    }
+    if (st + 1 < nbk) {
+        step(T0{}, st, Yes{});
+        step(T1{}, st + 1, No{});
+    } else {
+        step(T0{}, st, No{});
+    }
+    wait_vmcnt<0>();
+
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int n = n0 + r * 16 + nl;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int t = 0; t < TW; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int tok = m0 + (wid * TW + t) * 16 + 4 * cl + q;
+                if (tok >= a.M) continue;
+                float v = acc[r][t][q];
+                if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
+                a.y[size_t(tok) * a.ldy + n] = v;
+            }
+    }
+}
+
+template <class C, class F>
+static hipError_t launch_dslab_t(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    MatGroup g{};
+    g.n = n;
+    g.wg0[0] = 0;
+    for (int i = 0; i < n; ++i) {
+        g.t[i] = tasks[i];
+        g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + C::R - 1) / C::R;
+    }
+    const int ntg = (tasks[0].M + C::T - 1) / C::T;
+    const int G = g.wg0[n] * ntg;
+    const unsigned grid = unsigned((G + 7) / 8 * 8);
+    const int lds = C::lds_bytes(tasks[0].K / 256);
+    if (lds + 2 * C::DB > 160 * 1024) return hipErrorNotSupported;
+    hipLaunchKernelGGL((dslab_kernel<C, F>), dim3(grid), dim3(64 * C::NW), size_t(lds), s, g, x, ntg);
+    return hipGetLastError();
+}
+
 template <class C, class F>
 static hipError_t launch_slab_t(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     MatGroup g{};
@@ -375,6 +767,20 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // down 2560 x 9728: 77.8 -> 75.3 us). Measured slower at M = 512: 128 x 128
     // in 8 waves, 128 x 32 in 8 waves, 32 x 128, 32 x 64, 64 x 16, 32 x 32,
     // three stages, and two row tiles per wave.
+    // Q6_K / Q5_K from 128 tokens: decoded slabs (their decoding is costly
+    // next to the epilogue). Measured at M = 128 / 200 / 300 / 512 / 1024:
+    // down 2560 x 9728 (16 rows x 128 tokens) 34.4 / 42.6 / 43.5 / 58.4 /
+    // 103.8 us against 39.0 / 56.6 / 57.5 / 77.8 / 126.3 (slab kernel); QKV
+    // 6144 x 2560 (32 x 128) 16.8 / 22.5 / 33.1 / 33.9 / 59.0 against 18.7 /
+    // 24.0 / 31.2 / 37.2 / 63.1. Q4_K stays on the slab kernel (gate + up and
+    // O at M = 512: 86.5 and 29.0 us against 78.9 and 28.0): its epilogue
+    // outweighs its decoding, and the slab kernel fits more waves per SIMD.
+    if (a.M >= 128) {
+        hipError_t e = hipErrorNotSupported;
+        if constexpr (std::is_same_v<F, MQ6KS>) e = launch_dslab_t<DsCfg<F, 1, 4, 2>, F>(tasks, n, x, s);
+        if constexpr (std::is_same_v<F, MQ5KS>) e = launch_dslab_t<DsCfg<F, 2, 4, 2>, F>(tasks, n, x, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     int slabs = 0, slabs128 = 0;
     for (int i = 0; i < n; ++i) {
         slabs += (tasks[i].N + 63) / 64;

@@ -424,3 +424,37 @@ def test_prefill_eight_wave_slabs(ctx, oracle, M, K, specs, residual):
         check_outputs(got, ref, f"8-wave slabs task of {n} rows")
     for b in bufs:
         ctx.free(b)
+
+
+@pytest.mark.parametrize("type_id,M,K,specs,res_task", [
+    (TYPE_Q5_K, 256, 2560, (2048, 512, 528), 1),
+    (TYPE_Q5_K, 333, 1024, (100, 37), 0),
+    (TYPE_Q6_K, 384, 1024, (300, 45), 1),
+    (TYPE_Q6_K, 129, 4352, (2560,), None),
+])
+def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task):
+    """Q5_K / Q6_K from 128 tokens take the decoded-slab workgroups: task
+    groups over their concatenated row slabs (partial slabs at each task's
+    end), partial token groups, a residual; every row of every task, all
+    tokens, against the oracle."""
+    say(f"prefill decoded slabs {NAMES[type_id]} M={M} K={K} tasks={specs}")
+    x = synth.activations(M, K, seed=3600 + M)
+    xb = ctx.upload(x)
+    bufs, tasks, hosts, res_h = [xb], [], [], []
+    for i, n in enumerate(specs):
+        w = synth.weights(type_id, n, K, seed=3601 + i + M)
+        wb, yb = ctx.weight_upload(w, type_id, n, K), ctx.malloc(M * n * 4)
+        rh = synth.activations(M, n, seed=3620 + i) if res_task == i else None
+        rb = ctx.upload(rh) if rh is not None else None
+        bufs += [b for b in (wb, yb, rb) if b is not None]
+        tasks.append(qmm_hip.MatrixTask(wb, type_id, n, K, yb, n, residual=rb, res_stride=n if rh is not None else 0))
+        hosts.append(w)
+        res_h.append(rh)
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=type_id, rows=t.rows, **({"residual": rh} if rh is not None else {}))
+                                 for t, w, rh in zip(tasks, hosts, res_h)])
+    for i, t in enumerate(tasks):
+        check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"decoded slabs task {i}")
+    for b in bufs:
+        ctx.free(b)
