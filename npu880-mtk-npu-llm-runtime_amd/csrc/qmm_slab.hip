@@ -346,27 +346,42 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void slab_kernel(MatGroup grp, 
 // block's decoding is thus paid once per 16 NW TW tokens, where the slab
 // kernel pays it once per wave's 16 TW. One barrier per block. Per 16 x 16
 // tile and block the integer sums and the fp32 update are the slab kernel's.
+// With KS > 1 (few tokens, long K) the waves form KS groups that walk the
+// blocks g, g + KS, ... side by side, each with its own stages and decoded
+// buffers; each step every group writes its fp32 terms to LDS and group 0
+// adds the step's KS terms in block order behind the barrier, so every sum
+// is still the reference's, in its order.
 
-template <class F, int RT_, int NW_, int TW_, int WPS_ = 2, int PD_ = 3>
+template <class F, int RT_, int NW_, int TW_, int WPS_ = 2, int PD_ = 3, int KS_ = 1>
 struct DsCfg {
     static constexpr int RT = RT_, NW = NW_, TW = TW_, PD = PD_, WPS = WPS_;
+    // KS > 1: the waves form KS groups; group g takes blocks g, g + KS, ...
+    // (its own stages and decoded buffers), and group 0 adds the groups'
+    // fp32 terms of each KS blocks in block order (through LDS)
+    static constexpr int KS = KS_, NWG = NW_ / KS_;
+    static_assert(NWG * KS == NW, "KS groups of waves");
     static constexpr bool MIN = F::kMin;
-    static constexpr int R = 16 * RT, T = 16 * NW * TW;
+    static constexpr int R = 16 * RT, T = 16 * NWG * TW;
     static constexpr int SB = F::BB;
     static constexpr bool ALIGNED = SB % 16 == 0;
     static constexpr int WCR = (ALIGNED ? SB / 16 : (SB + 30) / 16) | 1;  // 16-B units per staged row, odd
     static constexpr int NWI = (R * WCR + 63) / 64;                       // weight transfers (1 KB) per block
-    static constexpr int NWW = (NWI + NW - 1) / NW;
+    static constexpr int NWW = (NWI + NWG - 1) / NWG;                     // of them per wave of a group
     static constexpr int PS = NWI * 1024;                                 // one packed stage
-    static constexpr int HC = 4 * RT / NW;                                // chunks a wave decodes per block
-    static_assert(HC >= 1 && 4 * RT % NW == 0, "chunks per wave");
+    static constexpr int HC = 4 * RT / NWG;                               // chunks a wave decodes per block
+    static_assert(HC >= 1 && 4 * RT % NWG == 0, "chunks per wave");
     // decoded row tile: planes [chunk][high | low] (1 KB each), mins (512 B), (d, dmin) per row
     static constexpr int OB_M = 8192, OB_D = MIN ? 8704 : 8192, RTB = OB_D + 128;
-    static constexpr int DB = RT * RTB;  // one decoded buffer (two, as static arrays)
-    // dynamic LDS: packed stages | a scratch KB | the tokens' block scales [T][nbk]
-    static constexpr int OFF_DUMP = PD * PS, OFF_DX = OFF_DUMP + 1024;
+    static constexpr int DB = RT * RTB;  // a group's decoded buffer (two per group, as static arrays)
+    // dynamic LDS: packed stages [group][PD] | a scratch KB | the groups'
+    // terms [2][KS][NWG][RT][TW][64 lanes] float4 (group 0's are written and
+    // never read: a store without a branch on the group between the MFMAs and
+    // their epilogue) | the tokens' block scales [T][nbk]
+    static constexpr int OFF_DUMP = KS * PD * PS, OFF_TM = OFF_DUMP + 1024;
+    static constexpr int TMB = KS > 1 ? KS * NWG * RT * TW * 1024 : 0;  // one terms buffer
+    static constexpr int OFF_DX = OFF_TM + 2 * TMB;
     static constexpr int lds_bytes(int nbk) { return OFF_DX + (T * nbk * 4 + 1023) / 1024 * 1024; }
-    static_assert(PD >= 3, "a block is staged two blocks ahead of its use");
+    static_assert(PD >= 3, "a block is staged two steps ahead of its use");
 };
 
 // B operands of chunk h (0..3) of a block for lane k-slice c: the high and low
@@ -463,10 +478,11 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     // the decoded buffers as two static arrays: the compiler then knows that
     // a block's decoding (into one) and the previous block's reads (of the
     // other) are independent and interleaves them
-    __shared__ __align__(16) uint8_t dbuf0[C::DB], dbuf1[C::DB];
-    constexpr int RT = C::RT, TW = C::TW;
+    __shared__ __align__(16) uint8_t dbuf0[C::KS * C::DB], dbuf1[C::KS * C::DB];
+    constexpr int RT = C::RT, TW = C::TW, KS = C::KS;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = wid / C::NWG, lw = wid - g * C::NWG;  // K group, wave in the group
     const int nl = lane & 15, cl = lane >> 4;
 
     // workgroup -> (row slab, token group): consecutive slots of one XCD
@@ -482,6 +498,7 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     const int n0 = bx * C::R, m0 = tg * C::T;
     const int K = a.K;
     const int nbk = K / 256;
+    const int nsteps = (nbk + KS - 1) / KS;  // group g's block at step s: s KS + g
 
     const uintptr_t wstart = reinterpret_cast<uintptr_t>(a.w) + size_t(n0) * a.row_bytes;
     const uint32_t bl = uint32_t(wstart & 15);
@@ -497,11 +514,12 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
                                            C::MIN ? uint32_t(ntile) * 16u * uint32_t(K / 8) : 0u);
     const uint32_t lds0 = lds_addr(lds);
 
-    // weight transfers: unit pc of staged row `row` (as the slab kernel)
+    // weight transfers of the group's block: unit pc of staged row `row` (as
+    // the slab kernel)
     uint32_t wo[C::NWW], wp[C::NWW];
 #pragma unroll
     for (int s = 0; s < C::NWW; ++s) {
-        const int p = (s * C::NW + wid) * 64 + lane;
+        const int p = (s * C::NWG + lw) * 64 + lane;
         const int row = p / C::WCR, pc = p - row * C::WCR;
         wo[s] = row < C::R ? uint32_t(row) * uint32_t(a.row_bytes) + bl : kFar;
         wp[s] = 16u * uint32_t(pc);
@@ -509,29 +527,30 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     }
     // (a block past the row reads zeros: the whole range as the uniform offset)
     const uint32_t wrange = uint32_t(rw.z);
-    auto issue_w = [&](int st) __attribute__((always_inline)) {
-        const bool live = st < nbk;
-        const uint32_t base = lds0 + uint32_t((st % C::PD) * C::PS), dump = lds0 + uint32_t(C::OFF_DUMP);
+    auto stage_of = [&](int s) __attribute__((always_inline)) { return (g * C::PD + s % C::PD) * C::PS; };
+    auto issue_w = [&](int s) __attribute__((always_inline)) {
+        const int j = s * KS + g;
+        const bool live = j < nbk;
+        const uint32_t base = lds0 + uint32_t(stage_of(s)), dump = lds0 + uint32_t(C::OFF_DUMP);
 #pragma unroll
-        for (int s = 0; s < C::NWW; ++s) {
-            const int i = s * C::NW + wid;
+        for (int t = 0; t < C::NWW; ++t) {
+            const int i = t * C::NWG + lw;
             const uint32_t dst = i < C::NWI ? base + uint32_t(i * 1024) : dump;
             if constexpr (C::ALIGNED) {
-                dma16s(rw, wo[s], live ? uint32_t(st) * uint32_t(C::SB) : wrange, dst);
+                dma16s(rw, wo[t], live ? uint32_t(j) * uint32_t(C::SB) : wrange, dst);
             } else {
-                const uint32_t v = ((wo[s] + uint32_t(st) * uint32_t(C::SB)) & ~15u) + wp[s];
-                dma16s(rw, wo[s] != kFar ? v : kFar, live ? 0u : wrange, dst);
+                const uint32_t v = ((wo[t] + uint32_t(j) * uint32_t(C::SB)) & ~15u) + wp[t];
+                dma16s(rw, wo[t] != kFar ? v : kFar, live ? 0u : wrange, dst);
             }
         }
     };
 
     // the wave's token tiles: codes (4 KB per tile and block), sums of 16
-    // codes (512 B), scales of the lane's four tokens; tiles past the input
-    // read zeros
+    // codes (512 B); tiles past the input read zeros
     uint32_t ao[TW], bo[TW];
 #pragma unroll
     for (int t = 0; t < TW; ++t) {
-        const int tile = m0 / 16 + wid * TW + t;
+        const int tile = m0 / 16 + lw * TW + t;
         const bool in = tile < ntile;
         ao[t] = in ? uint32_t(tile) * uint32_t(nbk) * 4096u + 16u * uint32_t(lane) : kFar;
         bo[t] = in ? uint32_t(tile) * uint32_t(nbk) * 512u + 8u * uint32_t(lane) : kFar;
@@ -540,21 +559,22 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     // the sums of two
     uint4 A[TW][4];
     half4v BH[2][TW];
-    auto load_codes = [&](int st) __attribute__((always_inline)) {
+    auto load_codes = [&](int s) __attribute__((always_inline)) {
+        const uint32_t j = uint32_t(s * KS + g);
 #pragma unroll
         for (int t = 0; t < TW; ++t)
 #pragma unroll
             for (int h = 0; h < 4; ++h)
                 A[t][h] = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, ao[t] + 1024u * uint32_t(h), uint32_t(st) * 4096u, 0));
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, ao[t] + 1024u * uint32_t(h), j * 4096u, 0));
     };
-    auto load_sums = [&](auto P, int st) __attribute__((always_inline)) {
+    auto load_sums = [&](auto P, int s) __attribute__((always_inline)) {
         constexpr int p = decltype(P)::value;
         if constexpr (C::MIN) {
+            const uint32_t j = uint32_t(s * KS + g);
 #pragma unroll
             for (int t = 0; t < TW; ++t)
-                BH[p][t] = __builtin_bit_cast(half4v, __builtin_amdgcn_raw_buffer_load_b64(rb, bo[t],
-                                                                                             uint32_t(st) * 512u, 0));
+                BH[p][t] = __builtin_bit_cast(half4v, __builtin_amdgcn_raw_buffer_load_b64(rb, bo[t], j * 512u, 0));
         }
     };
     // the scales of the workgroup's tokens, [T][nbk] (contiguous in the
@@ -568,14 +588,16 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
                    lds0 + uint32_t(C::OFF_DX + i * 1024));
     }
 
-    // decoding: wave w takes chunks [h0, h0 + HC) of row tile rt
-    const int dchunk = wid * C::HC, drt = dchunk >> 2, dh0 = dchunk & 3;
-    auto decode = [&](auto P, int st) __attribute__((always_inline)) {
-        const uint8_t *stage = lds + (st % C::PD) * C::PS;
-        uint8_t *db = (decltype(P)::value ? dbuf1 : dbuf0) + drt * C::RTB;
+    // decoding: wave lw of group g takes chunks [h0, h0 + HC) of row tile rt
+    // of the group's block
+    const int dchunk = lw * C::HC, drt = dchunk >> 2, dh0 = dchunk & 3;
+    auto decode = [&](auto P, int s) __attribute__((always_inline)) {
+        const int j = s * KS + g;
+        const uint8_t *stage = lds + stage_of(s);
+        uint8_t *db = (decltype(P)::value ? dbuf1 : dbuf0) + g * C::DB + drt * C::RTB;
         const int rl = drt * 16 + nl;
         const uint32_t mis =
-            C::ALIGNED ? 0u : (uint32_t(rl) * uint32_t(a.row_bytes) + bl + uint32_t(st) * uint32_t(C::SB)) & 15u;
+            C::ALIGNED ? 0u : (uint32_t(rl) * uint32_t(a.row_bytes) + bl + uint32_t(j) * uint32_t(C::SB)) & 15u;
         const uint8_t *blk = stage + rl * (C::WCR * 16) + mis;
 #pragma unroll
         for (int i = 0; i < C::HC; ++i) {
@@ -595,77 +617,121 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     };
 
     float acc[RT][TW][4];
+    [[maybe_unused]] float d0[RT][TW][4];  // group 0's terms of the last step, added behind the previous step's
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int t = 0; t < TW; ++t)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[r][t][q] = 0.0f;
-
-    // block st: A its codes, BH[P] and DX[P] its sums and scales, the decoded
-    // buffer (st & 1) its B operands (published by the barrier); stage
-    // (st + 1) % PD has landed. MORE: block st + 1 exists (its activations
-    // are loaded and its weights decoded here, after this block's reads of
-    // the decoded buffer)
-    auto step = [&](auto P, int st, auto MORE) __attribute__((always_inline)) {
-        constexpr int p = decltype(P)::value;
-        constexpr bool more = decltype(MORE)::value;
-        wait_vmcnt<0>();  // this wave's transfers of block st + 1 and activations of st
-        lds_barrier();    // every wave's, and block st decoded; decoded buffer (st + 1) & 1 and stage (st + 2) % PD free
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (more) {
-            issue_w(st + 2);  // zeros past the last block
-            load_sums(std::integral_constant<int, p ^ 1>{}, st + 1);
-        }
-        const uint8_t *db = p ? dbuf1 : dbuf0;
+            for (int q = 0; q < 4; ++q) acc[r][t][q] = d0[r][t][q] = 0.0f;
+    // the terms of group gg (>= 1) of the wave's tiles in terms buffer b
+    auto term_slot = [&](int b, int gg, int r, int t) __attribute__((always_inline)) {
+        return reinterpret_cast<float4 *>(lds + C::OFF_TM + b * C::TMB) +
+               (((gg * C::NWG + lw) * RT + r) * TW + t) * 64 + lane;
+    };
+    // group 0: step s's blocks in order (its own terms, then those of the
+    // groups whose block is inside K), published by the barrier after them
+    auto add_step = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const uint8_t *dr = db + r * C::RTB;
-            uint4 bb[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) bb[i] = ld16(dr + i * 1024 + 16 * lane);
-            const float2 dd = *reinterpret_cast<const float2 *>(dr + C::OB_D + 8 * nl);
-            half4v mh;
-            if constexpr (C::MIN) mh = *reinterpret_cast<const half4v *>(dr + C::OB_M + 8 * lane);
-            int4v D1[TW], D2[TW];
+        for (int r = 0; r < RT; ++r)
 #pragma unroll
             for (int t = 0; t < TW; ++t) {
-                D1[t] = int4v{0, 0, 0, 0};
-                D2[t] = int4v{0, 0, 0, 0};
-            }
+                float v[4] = {d0[r][t][0], d0[r][t][1], d0[r][t][2], d0[r][t][3]};
 #pragma unroll
-            for (int h = 0; h < 4; ++h)
-#pragma unroll
-                for (int t = 0; t < TW; ++t) {
-                    D1[t] = mfma16x16x64(A[t][h], bb[2 * h], D1[t]);
-                    D2[t] = mfma16x16x64(A[t][h], bb[2 * h + 1], D2[t]);
+                for (int q = 0; q < 4; ++q) acc[r][t][q] += v[q];
+                for (int gg = 1; gg < KS && s * KS + gg < nbk; ++gg) {
+                    const float4 w = *term_slot(s & 1, gg, r, t);
+                    acc[r][t][0] += w.x;
+                    acc[r][t][1] += w.y;
+                    acc[r][t][2] += w.z;
+                    acc[r][t][3] += w.w;
                 }
-            if constexpr (more)  // once the block's last MFMAs have their operands
-                if (r == RT - 1) load_codes(st + 1);
-            f32x4v Mb[TW];
-            if constexpr (C::MIN) {
-#pragma unroll
-                for (int t = 0; t < TW; ++t)
-                    Mb[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(BH[p][t], mh, f32x4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             }
-#pragma unroll
-            for (int t = 0; t < TW; ++t)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int S = (D1[t][q] << F::kShift) + D2[t][q];
-                    const float dx = sdx[((wid * TW + t) * 16 + 4 * cl + q) * nbk + st];
-                    if constexpr (C::MIN)
-                        acc[r][t][q] += dx * (dd.x * (float)S - dd.y * Mb[t][q]);  // E:11026 / E:11063
-                    else
-                        acc[r][t][q] += (dd.x * dx) * (float)S;  // E:11101
-                }
-        }
-        if constexpr (more) decode(std::integral_constant<int, p ^ 1>{}, st + 1);
     };
 
-    // prologue: blocks 0 and 1 staged, block 0's activations, block 0 decoded
+    // step s: the group's block j = s KS + g: A its codes, BH[P] its sums,
+    // the group's decoded buffer (s & 1) its B operands (published by the
+    // barrier); stage (s + 1) % PD has landed. MORE: step s + 1 exists (its
+    // activations are loaded and its weights decoded here, after this step's
+    // reads of the decoded buffer)
+    auto step = [&](auto P, int s, auto MORE) __attribute__((always_inline)) {
+        constexpr int p = decltype(P)::value;
+        constexpr bool more = decltype(MORE)::value;
+        const int j = s * KS + g;
+        wait_vmcnt<0>();  // this wave's transfers of step s + 1 and activations of step s
+        lds_barrier();    // every wave's, and step s decoded; decoded buffers (s + 1) & 1 and stages (s + 2) % PD free
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (more) {
+            issue_w(s + 2);  // zeros past the last block
+            load_sums(std::integral_constant<int, p ^ 1>{}, s + 1);
+        }
+        if constexpr (KS > 1)
+            if (g == 0 && s > 0) add_step(s - 1);
+        const uint8_t *db = (p ? dbuf1 : dbuf0) + g * C::DB;
+        if (KS == 1 || j < nbk) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const uint8_t *dr = db + r * C::RTB;
+                uint4 bb[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) bb[i] = ld16(dr + i * 1024 + 16 * lane);
+                const float2 dd = *reinterpret_cast<const float2 *>(dr + C::OB_D + 8 * nl);
+                half4v mh;
+                if constexpr (C::MIN) mh = *reinterpret_cast<const half4v *>(dr + C::OB_M + 8 * lane);
+                int4v D1[TW], D2[TW];
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    D1[t] = int4v{0, 0, 0, 0};
+                    D2[t] = int4v{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+#pragma unroll
+                    for (int t = 0; t < TW; ++t) {
+                        D1[t] = mfma16x16x64(A[t][h], bb[2 * h], D1[t]);
+                        D2[t] = mfma16x16x64(A[t][h], bb[2 * h + 1], D2[t]);
+                    }
+                if constexpr (more)  // once the block's last MFMAs have their operands
+                    if (r == RT - 1) load_codes(s + 1);
+                f32x4v Mb[TW];
+                if constexpr (C::MIN) {
+#pragma unroll
+                    for (int t = 0; t < TW; ++t)
+                        Mb[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(BH[p][t], mh, f32x4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
+                                                                      0);
+                }
+#pragma unroll
+                for (int t = 0; t < TW; ++t) {
+                    float v[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int S = (D1[t][q] << F::kShift) + D2[t][q];
+                        const float dx = sdx[((lw * TW + t) * 16 + 4 * cl + q) * nbk + j];
+                        if constexpr (C::MIN)
+                            v[q] = dx * (dd.x * (float)S - dd.y * Mb[t][q]);  // E:11026 / E:11063
+                        else
+                            v[q] = (dd.x * dx) * (float)S;  // E:11101
+                    }
+                    if constexpr (KS == 1) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc[r][t][q] += v[q];
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) d0[r][t][q] = v[q];
+                        *term_slot(s & 1, g, r, t) = make_float4(v[0], v[1], v[2], v[3]);
+                    }
+                }
+            }
+        } else if constexpr (more) {
+            load_codes(s + 1);
+        }
+        if constexpr (more) decode(std::integral_constant<int, p ^ 1>{}, s + 1);
+    };
+
+    // prologue: the groups' first two blocks staged, their first block's
+    // activations, the first block decoded
     issue_w(0);
-    if (nbk > 1) issue_w(1);
+    if (nsteps > 1) issue_w(1);
     load_codes(0);
     load_sums(std::integral_constant<int, 0>{}, 0);
     wait_vmcnt<0>();
@@ -676,18 +742,23 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
     using T1 = std::integral_constant<int, 1>;
     using Yes = std::true_type;
     using No = std::false_type;
-    int st = 0;
-    for (; st + 2 < nbk; st += 2) {
-        step(T0{}, st, Yes{});
-        step(T1{}, st + 1, Yes{});
+    int s = 0;
+    for (; s + 2 < nsteps; s += 2) {
+        step(T0{}, s, Yes{});
+        step(T1{}, s + 1, Yes{});
     }
-    if (st + 1 < nbk) {
-        step(T0{}, st, Yes{});
-        step(T1{}, st + 1, No{});
+    if (s + 1 < nsteps) {
+        step(T0{}, s, Yes{});
+        step(T1{}, s + 1, No{});
     } else {
-        step(T0{}, st, No{});
+        step(T0{}, s, No{});
     }
     wait_vmcnt<0>();
+    if constexpr (KS > 1) {  // the last step's terms
+        lds_barrier();
+        if (g != 0) return;
+        add_step(nsteps - 1);
+    }
 
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
@@ -697,7 +768,7 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
         for (int t = 0; t < TW; ++t)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int tok = m0 + (wid * TW + t) * 16 + 4 * cl + q;
+                const int tok = m0 + (lw * TW + t) * 16 + 4 * cl + q;
                 if (tok >= a.M) continue;
                 float v = acc[r][t][q];
                 if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
@@ -719,7 +790,7 @@ static hipError_t launch_dslab_t(const MatArgs *tasks, int n, const Q8KView &x, 
     const int G = g.wg0[n] * ntg;
     const unsigned grid = unsigned((G + 7) / 8 * 8);
     const int lds = C::lds_bytes(tasks[0].K / 256);
-    if (lds + 2 * C::DB > 160 * 1024) return hipErrorNotSupported;
+    if (lds + 2 * C::KS * C::DB > 160 * 1024) return hipErrorNotSupported;
     hipLaunchKernelGGL((dslab_kernel<C, F>), dim3(grid), dim3(64 * C::NW), size_t(lds), s, g, x, ntg);
     return hipGetLastError();
 }
@@ -742,9 +813,10 @@ static hipError_t launch_slab_t(const MatArgs *tasks, int n, const typename ActO
 
 int mfma_cu_count();
 
-// hipErrorNotSupported (nothing launched) where the slab kernel does not
+// hipErrorNotSupported (nothing launched) where the slab kernels do not
 // apply: K not a multiple of 256, operand sections missing, rows of an
-// aligned format not 16-B aligned, or offsets past the 32-bit buffer range.
+// aligned format not 16-B aligned, offsets past the 32-bit buffer range, 64
+// tokens or fewer other than Q6_K, or a decoded slab's LDS over the CU's.
 template <class F>
 hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     const MatArgs &a = tasks[0];
@@ -767,6 +839,15 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // down 2560 x 9728: 77.8 -> 75.3 us). Measured slower at M = 512: 128 x 128
     // in 8 waves, 128 x 32 in 8 waves, 32 x 128, 32 x 64, 64 x 16, 32 x 32,
     // three stages, and two row tiles per wave.
+    // Q6_K at 33..64 tokens: decoded slabs of 16 rows x 64 tokens in 16
+    // waves, four K groups of four (down 2560 x 9728 at M = 48 / 64: 20.4 /
+    // 21.8 us against 23 / 27.1 for the 16 x 16 K-split tiles, which decode
+    // each block once per 16 tokens). Fewer tokens, and Q4_K / Q5_K, measured
+    // slower than the small-M kernels.
+    if (a.M <= 64) {
+        if constexpr (std::is_same_v<F, MQ6KS>) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4>, F>(tasks, n, x, s);
+        return hipErrorNotSupported;
+    }
     // Q6_K / Q5_K from 128 tokens: decoded slabs (their decoding is costly
     // next to the epilogue). Measured at M = 128 / 200 / 300 / 512 / 1024:
     // down 2560 x 9728 (16 rows x 128 tokens) 34.4 / 42.6 / 43.5 / 58.4 /

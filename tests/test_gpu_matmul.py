@@ -458,3 +458,36 @@ def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task
         check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"decoded slabs task {i}")
     for b in bufs:
         ctx.free(b)
+
+
+@pytest.mark.parametrize("M,K,specs,res_task", [
+    (64, 9728, (2560,), None),
+    (48, 4352, (300, 45), 1),
+    (33, 9728, (130,), 0),
+])
+def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
+    """Q6_K at 33..64 tokens over long K: decoded slabs whose four K groups
+    walk every fourth block and meet in block order; task groups, partial
+    row slabs, a residual, K not a multiple of 4 blocks (17 and 38 blocks);
+    every row of every task, all tokens, against the oracle."""
+    say(f"small-M Q6_K K-split decoded slabs M={M} K={K} tasks={specs}")
+    x = synth.activations(M, K, seed=3700 + M)
+    xb = ctx.upload(x)
+    bufs, tasks, hosts, res_h = [xb], [], [], []
+    for i, n in enumerate(specs):
+        w = synth.weights(TYPE_Q6_K, n, K, seed=3701 + i + M)
+        wb, yb = ctx.weight_upload(w, TYPE_Q6_K, n, K), ctx.malloc(M * n * 4)
+        rh = synth.activations(M, n, seed=3720 + i) if res_task == i else None
+        rb = ctx.upload(rh) if rh is not None else None
+        bufs += [b for b in (wb, yb, rb) if b is not None]
+        tasks.append(qmm_hip.MatrixTask(wb, TYPE_Q6_K, n, K, yb, n, residual=rb, res_stride=n if rh is not None else 0))
+        hosts.append(w)
+        res_h.append(rh)
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=TYPE_Q6_K, rows=t.rows, **({"residual": rh} if rh is not None else {}))
+                                 for t, w, rh in zip(tasks, hosts, res_h)])
+    for i, t in enumerate(tasks):
+        check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"K-split decoded slabs task {i}")
+    for b in bufs:
+        ctx.free(b)
