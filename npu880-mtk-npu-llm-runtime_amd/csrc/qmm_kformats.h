@@ -307,14 +307,13 @@ __device__ inline void scales_k4_packed(uint32_t s0, uint32_t s1, uint32_t s2, u
     m[1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
 }
 
-// a * b + c on 24-bit signed operands (|a|, |b| < 2^23) as one v_mad_i32_i24:
-// written out, the compiler reassociates a sum of such products into separate
-// multiplies and adds
-__device__ inline int mad_i24(int a, int b, int c) {
-    int d;
-    asm("v_mad_i32_i24 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
+// a * b + c on 24-bit signed operands (|a|, |b| < 2^23), exact in int32 (the
+// compiler may reassociate a sum of such products: integer, so any order
+// gives the same sum). Plain code, not inline assembly: b is often an MFMA
+// result, and the compiler places the wait states an MFMA result needs before
+// its VALU readers only for readers it can see (an inline-assembly reader
+// read stale results a few cycles after the MFMA, depending on timing).
+__device__ inline int mad_i24(int a, int b, int c) { return c + __mul24(a, b); }
 
 __device__ inline int4v mfma16x16x32_acc(uint2 a, uint2 b, int4v c) {
     const long av = (long)(((uint64_t)a.y << 32) | a.x);

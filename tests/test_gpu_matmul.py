@@ -491,3 +491,42 @@ def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
         check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"K-split decoded slabs task {i}")
     for b in bufs:
         ctx.free(b)
+
+
+@pytest.mark.parametrize("type_id,M,K,specs,res_task", [
+    (TYPE_Q4_K, 8, 2560, (9728,), None),
+    (TYPE_Q4_K, 3, 2560, (9728,), 0),
+    (TYPE_Q4_K, 16, 512, (4096, 1000), 1),
+    (TYPE_Q5_K, 5, 3072, (6144,), None),
+    (TYPE_Q5_K, 16, 2560, (4100, 33), 0),
+])
+def test_resident_tiles_groups(ctx, oracle, type_id, M, K, specs, res_task):
+    """Q4_K / Q5_K groups at 3..16 tokens with more row tiles than CUs take
+    the resident-tile kernel (two or three row tiles per workgroup); x with
+    codes at +-127 and an all-zero block; every row of every task, all
+    tokens, against the oracle. Run three times: an MFMA result read too
+    early gave wrong values in random tiles from run to run."""
+    say(f"resident tiles {NAMES[type_id]} M={M} K={K} tasks={specs}")
+    x = synth.activations(M, K, seed=3800 + M)
+    x[:, ::11] *= 30.0  # codes at +-127
+    x[1 % M, 256:512] = 0.0  # an all-zero block (d = 0)
+    xb = ctx.upload(x)
+    bufs, tasks, hosts, res_h = [xb], [], [], []
+    for i, n in enumerate(specs):
+        w = synth.weights(type_id, n, K, seed=3801 + i + M)
+        wb, yb = ctx.weight_upload(w, type_id, n, K), ctx.malloc(M * n * 4)
+        rh = synth.activations(M, n, seed=3820 + i) if res_task == i else None
+        rb = ctx.upload(rh) if rh is not None else None
+        bufs += [b for b in (wb, yb, rb) if b is not None]
+        tasks.append(qmm_hip.MatrixTask(wb, type_id, n, K, yb, n, residual=rb, res_stride=n if rh is not None else 0))
+        hosts.append(w)
+        res_h.append(rh)
+    refs = oracle.gemm_multi(x, [dict(w=w, type=type_id, rows=t.rows, **({"residual": rh} if rh is not None else {}))
+                                 for t, w, rh in zip(tasks, hosts, res_h)])
+    for run in range(3):
+        ctx.gemm_multi_dispatch(xb, M, K, tasks)
+        ctx.sync()
+        for i, t in enumerate(tasks):
+            check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"resident tiles task {i}, run {run}")
+    for b in bufs:
+        ctx.free(b)
