@@ -253,8 +253,8 @@ typedef struct {
  * to the next deciding chunk: the same results, fewer launches. At M = 1
  * with three or more such launches, the first runs alone and all later
  * chunks run as one launch that applies the first's decision before it
- * reads any weight, then a one-workgroup step decides the later chunks in
- * order from their bests: the same results (a stop after the first launch
+ * reads any weight, and whose last workgroup to finish decides the later
+ * chunks in order from their bests: the same results (a stop after the first launch
  * reads nothing more; later checkpoints stop nothing in flight).
  * scan_state (device int32[4]) receives: chunks read,
  * active positions, 1 if the scan stopped early, 0. The script-specific

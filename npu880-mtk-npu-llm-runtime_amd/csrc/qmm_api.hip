@@ -1096,9 +1096,9 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
     // after the first run as one launch (launch_gemv_scan): it applies the
     // first group's step before any weight request (a stop there ends the
     // scan, as the per-group launches would), then reads every later chunk,
-    // folding each chunk's best, and one workgroup decides those chunks in
-    // order afterwards — the same results with two launches in place of one
-    // per later group (the later checkpoints stop nothing in flight).
+    // folding each chunk's best, and its last workgroup to finish decides
+    // those chunks in order — the same results with one launch in place of
+    // one per later group (the later checkpoints stop nothing in flight).
     const int cf = groups.size() >= 3 ? groups[1].first : ce;  // the folded chunks: [cf, ce)
     const bool fold_shape = M == 1 && groups.size() >= 3 && ce - cf <= qmm::kFoldChunks &&
                             params->chunk_rows % (4 * qmm::kScanRows) == 0;
@@ -1136,9 +1136,7 @@ static int lm_scan(qmm_context *ctx, const void *q8k, const void *q80, const flo
                 plan.fold = ctx->fold;
                 pend.on = false;
                 e = qmm::launch_gemv_scan(tf.type, af, xk, pend.x32, pend.gamma, plan, pre, true, ctx->stream);
-                if (e != hipSuccess) return hip_fail(ctx, e, "scan launch");
-                e = qmm::launch_scan_fold_final(plan, ctx->stream);
-                return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "scan step launch");
+                return e == hipSuccess ? QMM_OK : hip_fail(ctx, e, "scan launch");
             }
         }
         const int c = gr.second;  // the group's last chunk: its threshold and checkpoint

@@ -220,9 +220,10 @@ struct AmaxOut {
 // once); then each wave contributes its best over its rows of every later
 // chunk (a DPP max over the wave, an LDS max over the workgroup, one
 // device-scope max per workgroup and chunk into one of 16 words, none of
-// them waited for), and one workgroup decides those chunks in order from
-// the word keys (scan_fold_final_kernel): the chunks after chunk 0 are all
-// read, their decisions taken at the end. Cleared (scan_fold_clear_kernel)
+// them waited for), and the last workgroup to finish decides those chunks
+// in order from the word keys (scan_fold_decide, after the workgroups have
+// counted themselves in on the arrival word): the chunks after chunk 0 are
+// all read, their decisions taken at the end. Cleared (scan_fold_clear_kernel)
 // before first use and by every final step for the next scan.
 constexpr int kFoldChunks = 64;  // chunks per launch at most
 constexpr int kFoldWords = 16;   // words per chunk
@@ -234,6 +235,8 @@ struct FoldWord {
 };
 struct ScanFold {
     FoldWord wd[kFoldWords][kFoldChunks];  // word w of chunk c; a chunk's words 16 KB apart
+    unsigned int arrived;                  // workgroups of the launch done (on a line of its own)
+    unsigned int apad[63];
 };
 struct ScanPlan {
     ScanFold *fold;
@@ -249,7 +252,6 @@ struct ScanPlan {
 };
 hipError_t launch_gemv_scan(uint32_t type, const MatArgs &a, const Q8KView &xk, const float *x32, const float *gamma,
                             const ScanPlan &plan, const PrevStep &pre, bool launch, hipStream_t s);
-hipError_t launch_scan_fold_final(const ScanPlan &plan, hipStream_t s);
 hipError_t launch_scan_fold_clear(ScanFold *fold, hipStream_t s);
 hipError_t launch_gemv_argmax(uint32_t type, const MatArgs &a, const Q8KView &xk, const Q80View &x0, bool round16,
                               const uint32_t *ids, uint32_t id_limit, void *part, int *nparts, hipStream_t s,
@@ -448,6 +450,59 @@ __device__ inline bool scan_stopped(const int32_t *st) {
 __device__ inline int scan_active(const int32_t *st, int M) {
     return st ? __builtin_amdgcn_readfirstlane(st[kScanActive]) : M;
 }
+// the fold's keys and arrival count to zero (one workgroup)
+__device__ inline void fold_clear(ScanFold *f) {
+    for (int i = int(threadIdx.x); i < kFoldWords * kFoldChunks; i += int(blockDim.x))
+        __hip_atomic_store(&f->wd[i / kFoldChunks][i % kFoldChunks].key, 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(&f->arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The later chunks' last step (one 256-thread workgroup, every word key of
+// the launch performed): from the running best chunk 0's step left, the
+// chunks in order — each chunk's best is the largest of its word keys,
+// taken when strictly greater (E:11177) — to the first checkpoint whose
+// threshold the running best reaches (E:11248-11256); then the best, the
+// state, and the keys and arrival count cleared for the next scan.
+__device__ inline void scan_fold_decide(const ScanPlan &sp) {
+    ScanFold *f = sp.fold;
+    __shared__ unsigned long long ck[kFoldChunks];
+    if (threadIdx.x < kFoldChunks) ck[threadIdx.x] = 0ull;
+    __syncthreads();
+    // every word key read at once, one per thread, folded per chunk in LDS
+    for (int i = int(threadIdx.x); i < kFoldWords * sp.nch; i += int(blockDim.x))
+        (void)__hip_atomic_fetch_max(&ck[i % sp.nch],
+                                     __hip_atomic_load(&f->wd[i / sp.nch][i % sp.nch].key, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT),
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float rv = sp.best_val[0];
+        uint32_t ri = sp.best_id[0];
+        int c = 0, stop = 0;
+        for (; c < sp.nch; ++c) {
+            const Best cb = key_best(ck[c]);
+            if (cb.i != kNone && cb.v > rv) {
+                rv = cb.v;
+                ri = sp.row_base + cb.i;
+            }
+            if (((sp.ckpt >> c) & 1ull) && !(rv < sp.thresh[c])) {
+                stop = 1;
+                ++c;
+                break;
+            }
+        }
+        sp.best_val[0] = rv;
+        sp.best_id[0] = ri;
+        sp.st[kScanChunks] = sp.c0 + c;
+        sp.st[kScanActive] = 1;
+        sp.st[kScanStopped] = stop;
+        sp.st[kScanPad] = 0;
+    }
+    __syncthreads();  // (the keys are read above before they are cleared)
+    fold_clear(f);
+}
+
 // the best of a 256-thread workgroup (sh: 4 entries of LDS)
 __device__ inline Best block_best(Best b, Best *sh) {
     b = wave_best(b);

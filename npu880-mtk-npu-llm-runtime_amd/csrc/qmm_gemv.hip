@@ -562,14 +562,10 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     if constexpr (X16) x16_fill<q80, std::is_same_v<F, FmtQ6K4>>(x16q, K, act);
     else if constexpr (FUSED) x_fill<q80, std::is_same_v<F, FmtQ6K4>>(xp, x32, K, act);
     else cpre_fill<q80, std::is_same_v<F, FmtQ6K4>>(cp, pq, pd, pb, K, act);
-    // SCAN: the workgroup's per-chunk best and contribution count
+    // SCAN: the workgroup's per-chunk best
     [[maybe_unused]] __shared__ unsigned long long lkey[SCAN ? kFoldChunks : 1];
-    [[maybe_unused]] __shared__ unsigned lcnt[SCAN ? kFoldChunks : 1];
     if constexpr (SCAN)
-        if (threadIdx.x < kFoldChunks) {
-            lkey[threadIdx.x] = 0ull;
-            lcnt[threadIdx.x] = 0u;
-        }
+        if (threadIdx.x < kFoldChunks) lkey[threadIdx.x] = 0ull;
     lds_barrier();
     // 3. groups. With 4 lanes per block (R = 1, 2 or 4 rows of 16 / R lane
     // groups each), a row's GPR lane groups take its blocks in consecutive
@@ -588,19 +584,10 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
     Best wb{-INFINITY, kNone};  // AMAX: the wave's running (max, first row); SCAN: of the current chunk
     [[maybe_unused]] int ccur = 0;
     // SCAN: this wave's contribution to chunk c (its best over its rows of
-    // the chunk, or nothing); the workgroup's fourth folds the workgroup's
-    // best into word wgi % 16 of the chunk (a device-scope max nothing waits
-    // for: the final step reads the words after the launch)
+    // the chunk, or nothing), into the workgroup's best of the chunk in LDS
     [[maybe_unused]] auto contribute = [&](int c) __attribute__((always_inline)) {
         const unsigned long long k = wave_max_key(best_key(wb));
-        if (lane == 0) {
-            (void)__hip_atomic_fetch_max(&lkey[c], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            const unsigned n = __hip_atomic_fetch_add(&lcnt[c], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (n == 3u)
-                (void)__hip_atomic_fetch_max(&sp->fold->wd[wgi % kFoldWords][c].key,
-                                             __hip_atomic_load(&lkey[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (lane == 0) (void)__hip_atomic_fetch_max(&lkey[c], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         wb = Best{-INFINITY, kNone};
     };
     for (; gw < ngroups; gw += stride) {
@@ -709,8 +696,34 @@ __device__ __attribute__((always_inline)) inline void gemv_persist_wg(MatArgs a,
             }
         }
     }
-    if constexpr (SCAN)
+    if constexpr (SCAN) {
         while (ccur < sp->nch) contribute(ccur++);
+        // one thread folds the workgroup's chunk bests into word wgi % 16 of
+        // each chunk (device-scope maxima, performed where every XCD's
+        // atomics meet), waits until they are done, and counts the workgroup
+        // in on the arrival word; workgroup 0 first releases its state
+        // writes (the one L2 write-back of the launch: one per workgroup
+        // measured 17 us slower). The workgroup that completes the count
+        // takes the launch's final step. (A workgroup that returned above
+        // found the scan stopped, as every workgroup of the launch then does:
+        // nothing counts, and nothing is left to decide.)
+        __syncthreads();
+        __shared__ int last;
+        if (threadIdx.x == 0) {
+            for (int c = 0; c < sp->nch; ++c)
+                (void)__hip_atomic_fetch_max(&sp->fold->wd[wgi % kFoldWords][c].key, lkey[c], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+            if (wgi == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            else wait_vmcnt<0>();
+            last = __hip_atomic_fetch_add(&sp->fold->arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   unsigned(nwg - 1);
+        }
+        __syncthreads();
+        if (last) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            scan_fold_decide(*sp);
+        }
+    }
     if constexpr (AMAX) {  // one partial per workgroup (per wave was slower: 4x the partials to combine)
         __shared__ Best wsb[4];
         wb = wave_best(wb);

@@ -167,66 +167,7 @@ __global__ __launch_bounds__(256) void scan_final_kernel(const Best *__restrict_
     if (checkpoint && all_above) st[kScanStopped] = 1;  // E:11254-11256
 }
 
-// the fold's keys to zero (one workgroup)
-__device__ inline void fold_clear(ScanFold *f) {
-    for (int i = int(threadIdx.x); i < kFoldWords * kFoldChunks; i += int(blockDim.x))
-        __hip_atomic_store(&f->wd[i / kFoldChunks][i % kFoldChunks].key, 0ull, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The later chunks' last step (one workgroup), after their launch: from the
-// running best chunk 0's step left, the chunks in order — each chunk's best
-// is the largest of its word keys (every atomic of the launch performed),
-// taken when strictly greater (E:11177) — to the first checkpoint whose
-// threshold the running best reaches (E:11248-11256); then the best, the
-// state, and the keys cleared for the next scan. A scan chunk 0's step
-// stopped is left as it is.
-__global__ __launch_bounds__(256) void scan_fold_final_kernel(ScanPlan sp) {
-    if (scan_stopped(sp.st)) return;  // (the launch ran nothing either: the keys are clear)
-    ScanFold *f = sp.fold;
-    __shared__ unsigned long long ck[kFoldChunks];
-    if (threadIdx.x < kFoldChunks) ck[threadIdx.x] = 0ull;
-    __syncthreads();
-    // every word key read at once, one per thread, folded per chunk in LDS
-    for (int i = int(threadIdx.x); i < kFoldWords * sp.nch; i += int(blockDim.x))
-        (void)__hip_atomic_fetch_max(&ck[i % sp.nch],
-                                     __hip_atomic_load(&f->wd[i / sp.nch][i % sp.nch].key, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT),
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float rv = sp.best_val[0];
-        uint32_t ri = sp.best_id[0];
-        int c = 0, stop = 0;
-        for (; c < sp.nch; ++c) {
-            const Best cb = key_best(ck[c]);
-            if (cb.i != kNone && cb.v > rv) {
-                rv = cb.v;
-                ri = sp.row_base + cb.i;
-            }
-            if (((sp.ckpt >> c) & 1ull) && !(rv < sp.thresh[c])) {
-                stop = 1;
-                ++c;
-                break;
-            }
-        }
-        sp.best_val[0] = rv;
-        sp.best_id[0] = ri;
-        sp.st[kScanChunks] = sp.c0 + c;
-        sp.st[kScanActive] = 1;
-        sp.st[kScanStopped] = stop;
-        sp.st[kScanPad] = 0;
-    }
-    __syncthreads();  // (the keys are read above before they are cleared)
-    fold_clear(f);
-}
-
 __global__ __launch_bounds__(256) void scan_fold_clear_kernel(ScanFold *f) { fold_clear(f); }
-
-hipError_t launch_scan_fold_final(const ScanPlan &plan, hipStream_t s) {
-    hipLaunchKernelGGL(scan_fold_final_kernel, dim3(1), dim3(256), 0, s, plan);
-    return hipGetLastError();
-}
 
 hipError_t launch_scan_fold_clear(ScanFold *fold, hipStream_t s) {
     hipLaunchKernelGGL(scan_fold_clear_kernel, dim3(1), dim3(256), 0, s, fold);
