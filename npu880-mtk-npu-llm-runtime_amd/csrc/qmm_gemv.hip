@@ -755,8 +755,9 @@ __global__ __launch_bounds__(256) void gemv_persist_kernel(MatArgs a, const floa
 // output equals the one-task launch's, bit for bit.
 // RMS: x32 is the row before its RMSNorm (gamma: the norm's weights), every
 // task a k-quant one; each workgroup normalizes the row itself.
-template <bool FUSED, int D, bool RMS = false>
-__global__ __launch_bounds__(256) void gemv_mixed_persist_kernel(MatGroup grp, const float *__restrict__ x32,
+// OCC: waves per SIMD the registers are held to (3: <= 168 VGPRs).
+template <bool FUSED, int D, bool RMS = false, int OCC = 1>
+__global__ __launch_bounds__(256, OCC) void gemv_mixed_persist_kernel(MatGroup grp, const float *__restrict__ x32,
                                                                  Q8KView prek, Q80View pre0,
                                                                  const float *__restrict__ gamma) {
     int bx = 0;
@@ -1296,18 +1297,26 @@ static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const f
             default: break;
         }
     }
+    // At D = 1 without F32 / F16 tasks the merged bodies are held to three
+    // waves per SIMD (168 VGPRs, no spills; at D = 2 they fit anyway), so the
+    // grid reaches three workgroups per CU: one format's {gate, up} Q4_K
+    // 2 x 9728 x 2560 7.71 -> 7.15 us, {Q5_K 8192, Q4_K 4096} 6.42 -> 6.28 us.
+    // With float tasks the k-quant grid then loses their workgroups' share
+    // of the CUs (the {Q5_K 8192, Q4_K 4096, F32, F32} group 6.40 -> 6.82
+    // us): the unconstrained bodies there.
+    const bool occ3 = fw == 0;
     if (rms) {
         if (dd == 2) return run(gemv_mixed_persist_kernel<true, 2, true>);
-        if (dd == 1) return run(gemv_mixed_persist_kernel<true, 1, true>);
+        if (dd == 1) return run(gemv_mixed_persist_kernel<true, 1, true, 3>);
         return run(gemv_mixed_persist_kernel<true, 0, true>);
     }
     if (x32) {
         if (dd == 2) return run(gemv_mixed_persist_kernel<true, 2>);
-        if (dd == 1) return run(gemv_mixed_persist_kernel<true, 1>);
+        if (dd == 1) return occ3 ? run(gemv_mixed_persist_kernel<true, 1, false, 3>) : run(gemv_mixed_persist_kernel<true, 1>);
         return run(gemv_mixed_persist_kernel<true, 0>);
     }
     if (dd == 2) return run(gemv_mixed_persist_kernel<false, 2>);
-    if (dd == 1) return run(gemv_mixed_persist_kernel<false, 1>);
+    if (dd == 1) return occ3 ? run(gemv_mixed_persist_kernel<false, 1, false, 3>) : run(gemv_mixed_persist_kernel<false, 1>);
     return run(gemv_mixed_persist_kernel<false, 0>);
 }
 
