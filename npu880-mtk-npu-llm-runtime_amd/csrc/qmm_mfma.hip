@@ -600,7 +600,7 @@ struct PartCfg {
 
 template <class F, int TT, int NBK>
 __device__ __attribute__((always_inline)) inline void part_wg(const MatArgs &a, int bx, const Q8KView &x,
-                                                              const ResArgs &ra) {
+                                                              const ResArgs &ra, int m0 = 0) {
     using C = PartCfg<F, TT, NBK>;
     using P = typename C::P;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -638,25 +638,30 @@ __device__ __attribute__((always_inline)) inline void part_wg(const MatArgs &a, 
     // are exact (codes issued first would make its wait for the last code
     // also wait for every younger transfer).
     // Blocks past the part repeat its last block; token slots past M hold
-    // stray codes whose outputs are not kept.
+    // stray codes whose outputs are not kept (token tiles past the tiles
+    // section's last repeat it).
+    const int tlast = (M + 15) / 16 - 1;
     uint4 av[NBK][TT][4];
 #pragma unroll
     for (int jb = 0; jb < NBK; ++jb) {
         const int j = j0 + min(jb, max(nbk - 1, 0));
 #pragma unroll
-        for (int t = 0; t < TT; ++t)
+        for (int t = 0; t < TT; ++t) {
+            const size_t tt = size_t(min(m0 / 16 + t, tlast));
 #pragma unroll
             for (int h = 0; h < 4; ++h)
-                av[jb][t][h] = ld16(x.qt + ((size_t(t) * size_t(nb) + size_t(j)) * 4 + size_t(h)) * 1024 + 16 * lane);
+                av[jb][t][h] = ld16(x.qt + ((tt * size_t(nb) + size_t(j)) * 4 + size_t(h)) * 1024 + 16 * lane);
+        }
     }
     wait_vmcnt<0>();                  // this wave's transfers and codes
     __builtin_amdgcn_s_barrier();     // everyone's scales
-    // scales transposed to [block][64 tokens] (tokens past M repeat M - 1),
-    // so a lane reads its 4 tokens' scales of a block as one float4
+    // scales of tokens m0 .. m0 + 63 transposed to [block][64 tokens]
+    // (tokens past M repeat M - 1), so a lane reads its 4 tokens' scales of
+    // a block as one float4
     float *dxt = reinterpret_cast<float *>(lds + ra.off_d + (M * nb + 63) / 64 * 256);
     for (int e = int(threadIdx.x); e < nb * 64; e += 256) {
         const int j = e >> 6, tok = e & 63;
-        dxt[e] = reinterpret_cast<const float *>(lds + ra.off_d)[min(tok, M - 1) * nb + j];
+        dxt[e] = reinterpret_cast<const float *>(lds + ra.off_d)[min(m0 + tok, M - 1) * nb + j];
     }
     lds_barrier();
 
@@ -766,7 +771,7 @@ __device__ __attribute__((always_inline)) inline void part_wg(const MatArgs &a, 
             for (int jb = 0; jb < NBK; ++jb)
                 if (jb < nbp) v = v + xs[p][jb];
         }
-        const int tok = 16 * t + 4 * cl + kp;
+        const int tok = m0 + 16 * t + 4 * cl + kp;
         if (tok < M && n < a.N) {
             if (a.res) v = v + a.res[size_t(tok) * a.ldr + n];
             a.y[size_t(tok) * a.ldy + n] = v;
@@ -774,11 +779,12 @@ __device__ __attribute__((always_inline)) inline void part_wg(const MatArgs &a, 
     }
 }
 
+// workgroup (bx, by): row tile bx, tokens 16 TT by ..
 template <class F, int TT, int NBK>
 __global__ __launch_bounds__(256) void part_kernel(MatGroup grp, Q8KView x, ResArgs ra) {
     int bx = 0;
     const MatArgs a = grp.t[group_task(grp, int(blockIdx.x), bx)];
-    part_wg<F, TT, NBK>(a, bx, x, ra);
+    part_wg<F, TT, NBK>(a, bx, x, ra, int(blockIdx.y) * 16 * TT);
 }
 
 // ================================================== F32 / F16 weight rows
@@ -992,7 +998,8 @@ static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hip
         g.t[i] = tasks[i];
         g.wg0[i + 1] = g.wg0[i] + (tasks[i].N + 15) / 16;
     }
-    hipLaunchKernelGGL((part_kernel<F, TT, NBK>), dim3(unsigned(tiles)), dim3(256), size_t(ra.lds), s, g, x, ra);
+    const dim3 grid(unsigned(tiles), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
+    hipLaunchKernelGGL((part_kernel<F, TT, NBK>), grid, dim3(256), size_t(ra.lds), s, g, x, ra);
     return hipGetLastError();
 }
 
@@ -1064,7 +1071,15 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
         if (a.M <= 16 || (a.M <= 32 ? wg < cus : 8 * wg < 5 * cus))
             return launch_tile_t<TileCfg<G, 1, 1, 1, 1, 4, 16, 2, 100 * 1024>, G>(tasks, n, x, s);
     }
-    // up to 32 tokens over K <= 3072: the resident-tile kernel
+    // up to 64 tokens over K <= 3072: the resident-tile and part kernels.
+    // Past 16 tokens the part kernel's workgroups each take a group of 16
+    // or 32 tokens (a grid row per group): at 17..32 tokens groups of 16
+    // where the row tiles are no more than the CUs (else all 32 tokens per
+    // workgroup), at 33..48 groups of 16, at 49..64 groups of 32. Measured
+    // (Q4_K 9728 x 2560 / Q5_K 4096 x 2560, M = 24, 40, 48, 64): 10.22 /
+    // 6.60, 13.37 / 7.79, 12.93 / 7.87, 14.02 / 8.70 us against one
+    // workgroup per row tile (Q4_K past 32 tokens: the 64 x 32 tiles) 10.22
+    // / 7.28, 14.90 / 8.33, 14.94 / 8.28, 15.32 / 9.27.
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
         if (a.K <= 3072) {
@@ -1074,11 +1089,12 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
                 if (group_tiles(tasks, n) > mfma_cu_count()) e = launch_res<F, 1>(tasks, n, x, s);
                 if (e == hipErrorNotSupported) e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 32) {
-                e = launch_part<G, 2>(tasks, n, x, s);
+                e = group_tiles(tasks, n) <= mfma_cu_count() ? launch_part<F, 1>(tasks, n, x, s)
+                                                             : launch_part<G, 2>(tasks, n, x, s);
             } else if (a.M <= 48) {
-                e = launch_part<G, 3>(tasks, n, x, s);
+                e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 64) {
-                e = launch_part<G, 4>(tasks, n, x, s);
+                e = launch_part<G, 2>(tasks, n, x, s);
             }
         }
         if (e != hipErrorNotSupported) return e;

@@ -169,6 +169,16 @@ def test_tree_verify_q5k_qkv(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, M, seed=2100 + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q6_K, 3000, 2560, 20, False), (TYPE_Q5_K, 4096, 2560, 33, True),
+                                                    (TYPE_Q4_K, 5000, 3072, 29, False), (TYPE_Q6_K, 1000, 1024, 57, True),
+                                                    (TYPE_Q4_K, 300, 2560, 47, True), (TYPE_Q5_K, 4000, 768, 64, False)])
+def test_part_token_groups(ctx, oracle, type_id, N, K, M, residual):
+    """17..64 tokens over K <= 3072: part-kernel workgroups on groups of 16
+    or 32 tokens (a last group holding 1..31 of them), or all 32 tokens
+    where the row tiles outnumber the CUs."""
+    _run(ctx, oracle, type_id, N, K, M, seed=2300 + N + M, residual=residual)
+
+
 def _extreme_weights(type_id, N, K, seed):
     """Random blocks pushed to the ends of the integer ranges: all 6-bit
     scales and mins 63 (Q4_K / Q5_K) or int8 scales cycling through -128,
