@@ -932,7 +932,9 @@ PMC_WORKLOADS = [
     ("tree_q5k_m16", synth.TYPE_Q5_K, 4096, 2560, 16),
     ("tree_q5k_m32", synth.TYPE_Q5_K, 4096, 2560, 32),
     ("tree_q5k_m64", synth.TYPE_Q5_K, 4096, 2560, 64),
+    ("tree_q6k_m8", synth.TYPE_Q6_K, 2560, 9728, 8),
     ("tree_q6k_m16", synth.TYPE_Q6_K, 2560, 9728, 16),
+    ("tree_q6k_m32", synth.TYPE_Q6_K, 2560, 9728, 32),
     ("tree_q6k_m64", synth.TYPE_Q6_K, 2560, 9728, 64),
     ("prefill_qkv", synth.TYPE_Q5_K, 6144, 2560, 512),
     ("prefill_o", synth.TYPE_Q4_K, 2560, 4096, 512),
