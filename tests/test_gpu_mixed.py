@@ -138,12 +138,15 @@ def test_mixed_group_large_k(ctx, oracle):
     ([(TYPE_Q5_K, 8192), (TYPE_F32, 32)], 2560, False),
     ([(TYPE_F16, 40), (TYPE_Q4_K, 8192), (TYPE_Q5_K, 2048), (TYPE_Q6_K, 1000)], 3072, False),
     ([(TYPE_Q6_K, 6144), (TYPE_Q4_K, 2048), (TYPE_Q5_K, 8)], 2560, True),
+    ([(TYPE_Q5_K, 8192), (TYPE_Q4_K, 4096)], 2560, True),
+    ([(TYPE_Q4_K, 3000), (TYPE_Q5_K, 8192), (TYPE_Q4_K, 1111)], 2560, False),
 ])
 def test_mixed_groups_persistent_grid(ctx, oracle, specs, K, pre):
     """Batch-1 groups with enough k-quant row groups for the persistent grid
     (every k-quant task on its own slice of it, F32 / F16 rows one per wave):
     each format's stage-load count, fused and prequantized input, ragged
-    row counts, a task smaller than one workgroup's row groups."""
+    row counts, a task smaller than one workgroup's row groups, groups
+    without float tasks (the bodies held to three waves per SIMD)."""
     say(f"mixed persistent {[(qmm_hip.TYPE_NAMES[t], n) for t, n in specs]} K={K} prequantized={pre}")
     _check(_run_group(ctx, oracle, specs, 1, K, seed=360 + K + len(specs), prequantized=pre),
            f"mixed persistent K={K}")
