@@ -407,9 +407,9 @@ def sweep_write(dirs):
     print("# floor at 9728 x {1, 2, 4, 8} rows of K = 2560, weights rotated over >= 512 MB of")
     print("# replicas, every dispatch launched directly (16 per size and kernel). Command (run from")
     print("# /tmp with TMPDIR=/tmp; paths relative to the repository root):")
-    print("#   rocprofv3 --kernel-trace --stats -d gpurun_out/sweep_trace -o run --output-format csv \\")
+    print("#   rocprofv3 --kernel-trace --stats -d prof/sweep_trace -o run --output-format csv \\")
     print("#     -- python3 bench.py --sweep-run")
-    print(f"#   python3 bench.py --sweep-summarize gpurun_out/sweep_trace > {os.path.relpath(SWEEP_PROFILE, ROOT)}")
+    print(f"#   python3 bench.py --sweep-summarize prof/sweep_trace > {os.path.relpath(SWEEP_PROFILE, ROOT)}")
     print("# Each traced dispatch runs alone (its own ramp-up and drain under the profiler's completion")
     print("# signal), so a duration here is the graph-timed step's time plus a fixed per-dispatch cost;")
     print("# the fit T = t0 + bytes / BW puts that cost into t0, and its slope (the marginal rate) is")
@@ -1014,11 +1014,11 @@ def pmc_write(dirs):
     print("# rotated over >= 512 MB of replicas; 8 dispatches each, launched directly, one at a time under")
     print("# the profiler). Passes (run from /tmp with TMPDIR=/tmp; paths relative to the repository root):")
     print("#   rocprofv3 --pmc SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES \\")
-    print("#     SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_WAVES GRBM_GUI_ACTIVE -d gpurun_out/gpmc1 -o run \\")
+    print("#     SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_WAVES GRBM_GUI_ACTIVE -d prof/gpmc1 -o run \\")
     print("#     --output-format csv -- python3 bench.py --pmc-run")
-    print("#   rocprofv3 --pmc FETCH_SIZE -d gpurun_out/gpmc2 ... ; rocprofv3 --pmc WRITE_SIZE -d gpurun_out/gpmc3 ...")
+    print("#   rocprofv3 --pmc FETCH_SIZE -d prof/gpmc2 ... ; rocprofv3 --pmc WRITE_SIZE -d prof/gpmc3 ...")
     print("#   rocprofv3 --pmc SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS \\")
-    print("#     SQ_VALU_MFMA_COEXEC_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 -d gpurun_out/gpmc4 ...")
+    print("#     SQ_VALU_MFMA_COEXEC_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 -d prof/gpmc4 ...")
     print(f"# summary: {cmd}")
     print("# derived: mfma_busy_frac = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs * 1024 SIMDs)")
     print("#   (rocprof's MfmaUtil); valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA; int8_ops_executed =")
