@@ -838,12 +838,30 @@ int qmm_gemm_multi_dispatch(qmm_context *ctx, const float *x, int M, int K, qmm_
     if (!aligned(x, 16)) return fail(ctx, QMM_EALIGN, "x must be 16-B aligned");
     if ((rc = use_device(ctx))) return rc;
     if (M == 1) return run_tasks(ctx, x, nullptr, nullptr, M, K, tasks, n_tasks);
+    hipError_t e;
+    // 2..4 tokens, one k-quant task in the batch-1 GEMV's shape: the kernel
+    // quantizes the rows in its fill (no quantizer launch), as at batch 1
+    if (M <= 4) {
+        int live = -1, nlive = 0;
+        for (int t = 0; t < n_tasks; ++t)
+            if (tasks[t].rows > 0) {
+                live = t;
+                ++nlive;
+            }
+        if (nlive == 1 && !need_q80 && !is_float(tasks[live].type)) {
+            const qmm::MatArgs a = mat_args(tasks[live], M, K);
+            if (qmm::gemv_mt_shape(a)) {
+                e = qmm::launch_gemv_mt(tasks[live].type, &a, 1, qmm::Q8KView{}, ctx->stream, x);
+                if (e == hipSuccess) return QMM_OK;
+                if (e != hipErrorNotSupported) return hip_fail(ctx, e, "matmul launch");
+            }
+        }
+    }
     const size_t k_bytes = need_q8k ? qmm::Q8KLayout(M, K).total : 0;
     const size_t z_bytes = need_q80 ? qmm::Q80Layout(M, K).total : 0;
     if ((rc = ensure_act(ctx, k_bytes + z_bytes))) return rc;
     void *q8k = need_q8k ? ctx->act : nullptr;
     void *q80 = need_q80 ? static_cast<uint8_t *>(ctx->act) + k_bytes : nullptr;
-    hipError_t e;
     if (need_q8k && (e = qmm::launch_quantize_q8k(x, M, K, q8k, ctx->stream, q8k_skip(M, tasks, n_tasks))) !=
                         hipSuccess)
         return hip_fail(ctx, e, "quantize_q8k launch");

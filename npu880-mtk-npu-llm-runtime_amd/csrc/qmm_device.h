@@ -290,7 +290,12 @@ hipError_t launch_gemv_x16(uint32_t type, const MatArgs &a, const uint16_t *x16,
 // 2 <= M <= 4 tokens of one Q4_K / Q5_K / Q6_K task on a prequantized input
 // (its codes, scales and 32-code sums) in the batch-1 GEMV's shape, else
 // hipErrorNotSupported (nothing launched)
-hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s);
+// one task at 2 tokens, or at 3..4 on a tensor tall enough that the MFMA
+// kernels need several rounds of workgroups: the batch-1 GEMV's shape
+bool gemv_mt_shape(const MatArgs &a);
+// x32 non-null: the tokens' fp32 rows, quantized in the kernel's fill (xk unused)
+hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s,
+                          const float *x32 = nullptr);
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 

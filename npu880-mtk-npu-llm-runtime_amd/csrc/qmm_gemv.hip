@@ -834,8 +834,11 @@ __global__ __launch_bounds__(256, 3) void gemv_scan_kernel(MatArgs a, const floa
 // the block terms (the batch-1 expression) and sum them in block order
 // along each row's lane groups in registers. Each output equals the batch-1
 // GEMV of its token, bit for bit. 4 lanes per block, R = 1, 2 or 4.
-template <class F, int R, int U, int NC, int MT>
-__global__ __launch_bounds__(256) void gemv_mt_kernel(MatArgs a, Q8KView prek) {
+// FUSED: x32 holds the tokens' fp32 rows, which every workgroup quantizes
+// into its LDS rows itself (the batch-1 fill per token: the quantizer's
+// launch saved); the rows are requested before the weights.
+template <class F, int R, int U, int NC, int MT, bool FUSED = false>
+__global__ __launch_bounds__(256) void gemv_mt_kernel(MatArgs a, Q8KView prek, const float *__restrict__ x32) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int G = F::G, SLOTS = 64 / G, GPR = SLOTS / R;
     static_assert(G == 4 && SLOTS % R == 0 && F::kStaged, "4 lanes per block, whole rows per DPP rows");
@@ -863,19 +866,36 @@ __global__ __launch_bounds__(256) void gemv_mt_kernel(MatArgs a, Q8KView prek) {
     // 1. the tokens' rows requested, then the first group's bytes; the rows into LDS
     int gw = int(blockIdx.x) * 4 + wid;
     const int stride = int(gridDim.x) * 4;
-    CPre cp[MT];
+    if constexpr (FUSED) {
+        XPre xp[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-        if (t < M)
-            cpre_load<false, false>(prek.qs + size_t(t) * K, prek.d + size_t(t) * nb, nullptr, K, cp[t]);
-    __builtin_amdgcn_sched_barrier(0);
-    stage_load(min(gw, ngroups - 1));
-    __builtin_amdgcn_sched_barrier(0);
+        for (int t = 0; t < MT; ++t)
+            if (t < M && x_has(0, K)) x_load(x32 + size_t(t) * K, K, x_chunk(0, K), xp[t]);
+        wait_vmcnt<0>();  // the rows before the weights (as the batch-1 fill)
+        __builtin_amdgcn_sched_barrier(0);
+        stage_load(min(gw, ngroups - 1));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-        if (t < M)
-            cpre_fill<false, std::is_same_v<F, FmtQ6K4>, true>(cp[t], prek.qs + size_t(t) * K, prek.d + size_t(t) * nb,
-                                                                nullptr, K, gemv_act_view(lds + t * act_bytes, false, K));
+        for (int t = 0; t < MT; ++t)
+            if (t < M)
+                x_fill<false, std::is_same_v<F, FmtQ6K4>>(xp[t], x32 + size_t(t) * K, K,
+                                                          gemv_act_view(lds + t * act_bytes, false, K));
+    } else {
+        CPre cp[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            if (t < M)
+                cpre_load<false, false>(prek.qs + size_t(t) * K, prek.d + size_t(t) * nb, nullptr, K, cp[t]);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_load(min(gw, ngroups - 1));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            if (t < M)
+                cpre_fill<false, std::is_same_v<F, FmtQ6K4>, true>(cp[t], prek.qs + size_t(t) * K,
+                                                                    prek.d + size_t(t) * nb, nullptr, K,
+                                                                    gemv_act_view(lds + t * act_bytes, false, K));
+    }
     lds_barrier();
 
     // 2. groups (as the batch-1 persistent kernel's register row sums)
@@ -1390,7 +1410,7 @@ hipError_t launch_gemv(uint32_t type, const MatArgs *tasks, int n, const float *
 }
 
 template <class F, int R, int U, int MT>
-static hipError_t launch_gemv_mt_r(const MatArgs &a, const Q8KView &xk, hipStream_t s) {
+static hipError_t launch_gemv_mt_r(const MatArgs &a, const Q8KView &xk, const float *x32, hipStream_t s) {
     const int nb = a.K / F::QK;
     if (R * nb > (64 / F::G) * U) return hipErrorNotSupported;
     const int cus = cu_count();
@@ -1400,32 +1420,50 @@ static hipError_t launch_gemv_mt_r(const MatArgs &a, const Q8KView &xk, hipStrea
     if (lds > 160 * 1024) return hipErrorNotSupported;
     return with_stage_chunks<F, U>(R * nb, [&](auto nc) {
         constexpr int NC = decltype(nc)::value;
-        hipLaunchKernelGGL((gemv_mt_kernel<F, R, U, NC, MT>), dim3(unsigned(wgs)), dim3(256), lds, s, a, xk);
+        if constexpr (MT == 2) {  // (the fused fill is taken at 2 tokens only)
+            if (x32) {
+                hipLaunchKernelGGL((gemv_mt_kernel<F, R, U, NC, MT, true>), dim3(unsigned(wgs)), dim3(256), lds, s, a,
+                                   xk, x32);
+                return hipGetLastError();
+            }
+        }
+        hipLaunchKernelGGL((gemv_mt_kernel<F, R, U, NC, MT>), dim3(unsigned(wgs)), dim3(256), lds, s, a, xk, x32);
         return hipGetLastError();
     });
 }
 
 template <class F, int U>
-static hipError_t launch_gemv_mt_t(const MatArgs &a, const Q8KView &xk, hipStream_t s) {
+static hipError_t launch_gemv_mt_t(const MatArgs &a, const Q8KView &xk, const float *x32, hipStream_t s) {
     // rows per wave as for a batch-1 launch of the same tensor
     const int R = a.N >= 4096 ? kGemvR : a.K <= 4096 ? 2 : 1;
     if (a.M <= 2) {
-        if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 2>(a, xk, s);
-        if (R == 2) return launch_gemv_mt_r<F, 2, U, 2>(a, xk, s);
-        return launch_gemv_mt_r<F, 1, U, 2>(a, xk, s);
+        if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 2>(a, xk, x32, s);
+        if (R == 2) return launch_gemv_mt_r<F, 2, U, 2>(a, xk, x32, s);
+        return launch_gemv_mt_r<F, 1, U, 2>(a, xk, x32, s);
     }
-    if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 4>(a, xk, s);
-    if (R == 2) return launch_gemv_mt_r<F, 2, U, 4>(a, xk, s);
-    return launch_gemv_mt_r<F, 1, U, 4>(a, xk, s);
+    if (R == kGemvR) return launch_gemv_mt_r<F, kGemvR, U, 4>(a, xk, x32, s);
+    if (R == 2) return launch_gemv_mt_r<F, 2, U, 4>(a, xk, x32, s);
+    return launch_gemv_mt_r<F, 1, U, 4>(a, xk, x32, s);
 }
 
-hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s) {
+hipError_t launch_gemv_mt(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, hipStream_t s,
+                          const float *x32) {
     const MatArgs &a = tasks[0];
-    if (n != 1 || a.M < 2 || a.M > 4 || a.K % 256 || a.K > 16384 || !xk.qs || !xk.d) return hipErrorNotSupported;
+    if (n != 1 || a.M < 2 || a.M > 4 || a.K % 256 || a.K > 16384) return hipErrorNotSupported;
+    if (!x32 && (!xk.qs || !xk.d)) return hipErrorNotSupported;
+    // the fill quantizes the rows where that beats the quantizer's launch:
+    // 2 tokens, one fill round (K <= 4096), at most four quads of row groups
+    // per CU (measured: Q4_K 9728 x 2560 8.49 -> 6.57 us; slower at K = 9728,
+    // Q6_K 2560 x 9728 11.3 -> 12.4, and on the 151936-row LM head, 60.6 ->
+    // 66.3; even at 3..4 tokens)
+    if (x32) {
+        const int R = a.N >= 4096 ? kGemvR : a.K <= 4096 ? 2 : 1;
+        if (a.M != 2 || a.K > 4096 || ((a.N + R - 1) / R + 3) / 4 > 4 * cu_count()) return hipErrorNotSupported;
+    }
     switch (type) {
-        case kQ4_K: return launch_gemv_mt_t<FmtQ4K4, 3>(a, xk, s);
-        case kQ5_K: return launch_gemv_mt_t<FmtQ5K4, 3>(a, xk, s);
-        case kQ6_K: return launch_gemv_mt_t<FmtQ6K4, 3>(a, xk, s);
+        case kQ4_K: return launch_gemv_mt_t<FmtQ4K4, 3>(a, xk, x32, s);
+        case kQ5_K: return launch_gemv_mt_t<FmtQ5K4, 3>(a, xk, x32, s);
+        case kQ6_K: return launch_gemv_mt_t<FmtQ6K4, 3>(a, xk, x32, s);
         default: return hipErrorNotSupported;
     }
 }

@@ -1199,6 +1199,8 @@ int mfma_cu_count() {
     return cus[dev];
 }
 
+bool gemv_mt_shape(const MatArgs &a) { return a.M == 2 || (a.M >= 3 && a.M <= 4 && a.N >= 96 * mfma_cu_count()); }
+
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,
                        hipStream_t s) {
     if (n < 1 || n > kMaxGroup) return hipErrorInvalidValue;
@@ -1207,7 +1209,7 @@ hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView
     // shape (measured, M = 2: Q4_K 9728 x 2560 7.75 -> 6.16 us, Q6_K 2560 x
     // 9728 13.57 -> 9.00, Q6_K 151936 x 2560 111 -> 62; M = 4: Q6_K 151936 x
     // 2560 111 -> 93, while Q4_K 9728 x 2560 went 7.73 -> 8.58)
-    if (n == 1 && (tasks[0].M == 2 || (tasks[0].M <= 4 && tasks[0].N >= 96 * mfma_cu_count()))) {
+    if (n == 1 && gemv_mt_shape(tasks[0])) {
         const hipError_t e = launch_gemv_mt(type, tasks, n, xk, s);
         if (e != hipErrorNotSupported) return e;
     }

@@ -169,6 +169,17 @@ def test_tree_verify_q5k_qkv(ctx, oracle, M):
     _run(ctx, oracle, TYPE_Q5_K, 4096, 2560, M, seed=2100 + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 2560, 2, False), (TYPE_Q6_K, 6000, 2560, 2, True),
+                                                    (TYPE_Q5_K, 333, 4096, 2, False), (TYPE_Q6_K, 2560, 9728, 2, True),
+                                                    (TYPE_Q6_K, 24832, 2560, 3, False), (TYPE_Q4_K, 24600, 1024, 4, True)])
+def test_few_tokens_fp32_input(ctx, oracle, type_id, N, K, M, residual):
+    """2..4 tokens in the batch-1 GEMV's shape on fp32 input: at 2 tokens
+    and K <= 4096 the kernel quantizes the tokens' rows in its fill (ragged
+    row counts, residuals); past that the quantizer's launch first. Bit-exact
+    against the oracle."""
+    _run(ctx, oracle, type_id, N, K, M, seed=2400 + N + M, residual=residual)
+
+
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q6_K, 3000, 2560, 20, False), (TYPE_Q5_K, 4096, 2560, 33, True),
                                                     (TYPE_Q4_K, 5000, 3072, 29, False), (TYPE_Q6_K, 1000, 1024, 57, True),
                                                     (TYPE_Q4_K, 300, 2560, 47, True), (TYPE_Q5_K, 4000, 768, 64, False)])
