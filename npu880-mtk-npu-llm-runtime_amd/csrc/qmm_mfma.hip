@@ -960,13 +960,12 @@ static hipError_t launch_res_r(const MatArgs *tasks, int n, const Q8KView &x, in
 }
 
 // Part-kernel launch if the parts, scales and terms fit one CU's LDS;
-// returns hipErrorNotSupported (nothing launched) otherwise. One tile per
-// workgroup. Up to 32 tokens a workgroup needs few enough registers for
-// three per CU, so any number of tiles runs as one wave of workgroups; past
-// 32 tokens only one fits a CU, and the tiles must not outnumber the CUs
-// (several tiles per workgroup in sequence, one wave per SIMD, measured
-// slower than the chunked tile kernel: Q4_K 9728 x 2560, M = 64, 21.9
-// against 17.6 us).
+// returns hipErrorNotSupported (nothing launched) otherwise. One tile and
+// one group of 16 TT tokens per workgroup (grid rows: the token groups).
+// Up to 32 tokens a workgroup needs few enough registers for three per CU,
+// so any number of tiles runs as one wave of workgroups; past 32 tokens
+// (three or four token tiles, as the mixed-group kernel uses) only one fits
+// a CU, and the tiles must not outnumber the CUs.
 // LDS offsets of the part-kernel body of format F for (M, K)
 template <class F, int TT>
 static ResArgs part_args(int M, int K) {
