@@ -351,10 +351,18 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void slab_kernel(MatGroup grp, 
 // buffers; each step every group writes its fp32 terms to LDS and group 0
 // adds the step's KS terms in block order behind the barrier, so every sum
 // is still the reference's, in its order.
+// Step s waits for its own wave's loads, then the barrier. Plain form: every
+// load issued before (the weights of step s + 1 and the codes of step s, both
+// issued one step earlier), so a step lasts at least one memory round trip.
+// DEEP form: the weights are issued three steps ahead and the codes and sums
+// two (a second register set of codes), every wave issues the same LPS loads
+// per step (past the last block they read zeros), and step s waits until only
+// the previous step's LPS are outstanding: two steps per round trip.
 
-template <class F, int RT_, int NW_, int TW_, int WPS_ = 2, int PD_ = 3, int KS_ = 1>
+template <class F, int RT_, int NW_, int TW_, int WPS_ = 2, int PD_ = 3, int KS_ = 1, bool DEEP_ = false>
 struct DsCfg {
     static constexpr int RT = RT_, NW = NW_, TW = TW_, PD = PD_, WPS = WPS_;
+    static constexpr bool DEEP = DEEP_;
     // KS > 1: the waves form KS groups; group g takes blocks g, g + KS, ...
     // (its own stages and decoded buffers), and group 0 adds the groups'
     // fp32 terms of each KS blocks in block order (through LDS)
@@ -368,6 +376,8 @@ struct DsCfg {
     static constexpr int NWI = (R * WCR + 63) / 64;                       // weight transfers (1 KB) per block
     static constexpr int NWW = (NWI + NWG - 1) / NWG;                     // of them per wave of a group
     static constexpr int PS = NWI * 1024;                                 // one packed stage
+    static constexpr int LPS = NWW + 4 * TW + (F::kMin ? TW : 0);         // loads per wave and step (DEEP)
+    static_assert(!DEEP || LPS <= 63, "vmcnt range");
     static constexpr int HC = 4 * RT / NWG;                               // chunks a wave decodes per block
     static_assert(HC >= 1 && 4 * RT % NWG == 0, "chunks per wave");
     // decoded row tile: planes [chunk][high | low] (1 KB each), mins (512 B), (d, dmin) per row
@@ -555,17 +565,19 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
         ao[t] = in ? uint32_t(tile) * uint32_t(nbk) * 4096u + 16u * uint32_t(lane) : kFar;
         bo[t] = in ? uint32_t(tile) * uint32_t(nbk) * 512u + 8u * uint32_t(lane) : kFar;
     }
-    // the codes of one block (reloaded once the block's MFMAs are issued);
-    // the sums of two
-    uint4 A[TW][4];
+    // the codes of one block (two with DEEP; reloaded once the block's MFMAs
+    // are issued); the sums of two
+    constexpr bool DEEP = C::DEEP;
+    uint4 A[DEEP ? 2 : 1][TW][4];
     half4v BH[2][TW];
-    auto load_codes = [&](int s) __attribute__((always_inline)) {
+    auto load_codes = [&](auto Q, int s) __attribute__((always_inline)) {
+        constexpr int q = decltype(Q)::value;
         const uint32_t j = uint32_t(s * KS + g);
 #pragma unroll
         for (int t = 0; t < TW; ++t)
 #pragma unroll
             for (int h = 0; h < 4; ++h)
-                A[t][h] = __builtin_bit_cast(
+                A[q][t][h] = __builtin_bit_cast(
                     uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, ao[t] + 1024u * uint32_t(h), j * 4096u, 0));
     };
     auto load_sums = [&](auto P, int s) __attribute__((always_inline)) {
@@ -607,12 +619,15 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
             *reinterpret_cast<uint4 *>(db + (2 * h) * 1024 + 16 * lane) = o1;
             *reinterpret_cast<uint4 *>(db + (2 * h + 1) * 1024 + 16 * lane) = o2;
         }
-        if (dh0 == 0) {
+        // the row scales: by the wave holding the row tile's chunk 0; without
+        // mins by every wave and lane (the same value to the same word), so
+        // the decoding has no branch to schedule around
+        if (!C::MIN || dh0 == 0) {
             half4v mh;
             float d, dmin;
             ds_row<F>(blk, cl, mh, d, dmin);
             if constexpr (C::MIN) *reinterpret_cast<half4v *>(db + C::OB_M + 8 * lane) = mh;
-            if (cl == 0) *reinterpret_cast<float2 *>(db + C::OB_D + 8 * nl) = make_float2(d, dmin);
+            if (!C::MIN || cl == 0) *reinterpret_cast<float2 *>(db + C::OB_D + 8 * nl) = make_float2(d, dmin);
         }
     };
 
@@ -649,26 +664,39 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
             }
     };
 
-    // step s: the group's block j = s KS + g: A its codes, BH[P] its sums,
-    // the group's decoded buffer (s & 1) its B operands (published by the
-    // barrier); stage (s + 1) % PD has landed. MORE: step s + 1 exists (its
-    // activations are loaded and its weights decoded here, after this step's
-    // reads of the decoded buffer)
+    // step s: the group's block j = s KS + g: A[ap] its codes, BH[P] its
+    // sums, the group's decoded buffer (s & 1) its B operands (published by
+    // the barrier); stage (s + 1) % PD has landed. MORE: step s + 1 exists
+    // (its weights are decoded here, after this step's reads of the decoded
+    // buffer; plain form: its activations are loaded here too)
+    using T0c = std::integral_constant<int, 0>;
     auto step = [&](auto P, int s, auto MORE) __attribute__((always_inline)) {
         constexpr int p = decltype(P)::value;
+        constexpr int ap = DEEP ? p : 0;  // the code registers of this step
+        using AP = std::integral_constant<int, ap>;
         constexpr bool more = decltype(MORE)::value;
         const int j = s * KS + g;
-        wait_vmcnt<0>();  // this wave's transfers of step s + 1 and activations of step s
-        lds_barrier();    // every wave's, and step s decoded; decoded buffers (s + 1) & 1 and stages (s + 2) % PD free
+        // plain: this wave's transfers of step s + 1 and activations of step s;
+        // DEEP: all but the previous step's LPS loads (the transfers of step
+        // s + 1 and the activations of step s were issued two steps ago)
+        wait_vmcnt<DEEP ? C::LPS : 0>();
+        lds_barrier();  // every wave's, and step s decoded; decoded buffers (s + 1) & 1 free, and the
+                        // stage written next ((s + 2) % PD plain, s % PD DEEP)
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (more) {
+        if constexpr (DEEP) {
+            issue_w(s + 3);  // zeros past the last block
+        } else if constexpr (more) {
             issue_w(s + 2);  // zeros past the last block
             load_sums(std::integral_constant<int, p ^ 1>{}, s + 1);
         }
         if constexpr (KS > 1)
             if (g == 0 && s > 0) add_step(s - 1);
         const uint8_t *db = (p ? dbuf1 : dbuf0) + g * C::DB;
-        if (KS == 1 || j < nbk) {
+        // DEEP: a group's block past K is computed too (zeros staged, its term
+        // never added: group 0's block is inside K, add_step skips the rest),
+        // so no load sits behind a branch (the compiler would wait for it to
+        // copy registers where the paths join)
+        if (KS == 1 || DEEP || j < nbk) {
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const uint8_t *dr = db + r * C::RTB;
@@ -688,17 +716,25 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
                 for (int h = 0; h < 4; ++h)
 #pragma unroll
                     for (int t = 0; t < TW; ++t) {
-                        D1[t] = mfma16x16x64(A[t][h], bb[2 * h], D1[t]);
-                        D2[t] = mfma16x16x64(A[t][h], bb[2 * h + 1], D2[t]);
+                        D1[t] = mfma16x16x64(A[ap][t][h], bb[2 * h], D1[t]);
+                        D2[t] = mfma16x16x64(A[ap][t][h], bb[2 * h + 1], D2[t]);
                     }
-                if constexpr (more)  // once the block's last MFMAs have their operands
-                    if (r == RT - 1) load_codes(s + 1);
+                // once the block's last MFMAs have their operands: the next
+                // codes, then the next block's decoding (independent of the
+                // MFMAs in flight, ahead of the epilogue that waits for them)
+                if (r == RT - 1) {
+                    if constexpr (DEEP) load_codes(AP{}, s + 2);
+                    else if constexpr (more) load_codes(T0c{}, s + 1);
+                    if constexpr (more) decode(std::integral_constant<int, p ^ 1>{}, s + 1);
+                }
                 f32x4v Mb[TW];
                 if constexpr (C::MIN) {
 #pragma unroll
                     for (int t = 0; t < TW; ++t)
                         Mb[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(BH[p][t], mh, f32x4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0,
                                                                       0);
+                    if constexpr (DEEP)
+                        if (r == RT - 1) load_sums(P, s + 2);
                 }
 #pragma unroll
                 for (int t = 0; t < TW; ++t) {
@@ -723,18 +759,29 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
                 }
             }
         } else if constexpr (more) {
-            load_codes(s + 1);
+            load_codes(T0c{}, s + 1);
+            decode(std::integral_constant<int, p ^ 1>{}, s + 1);
         }
-        if constexpr (more) decode(std::integral_constant<int, p ^ 1>{}, s + 1);
     };
 
-    // prologue: the groups' first two blocks staged, their first block's
-    // activations, the first block decoded
-    issue_w(0);
-    if (nsteps > 1) issue_w(1);
-    load_codes(0);
-    load_sums(std::integral_constant<int, 0>{}, 0);
-    wait_vmcnt<0>();
+    // prologue: the groups' first two (DEEP: three) blocks staged, their
+    // first (two) blocks' activations, the first block decoded
+    if constexpr (DEEP) {
+        issue_w(0);
+        issue_w(1);
+        load_codes(T0c{}, 0);
+        load_sums(T0c{}, 0);
+        load_codes(std::integral_constant<int, 1>{}, 1);
+        load_sums(std::integral_constant<int, 1>{}, 1);
+        issue_w(2);
+        wait_vmcnt<C::NWW>();  // all but the third block's transfers
+    } else {
+        issue_w(0);
+        if (nsteps > 1) issue_w(1);
+        load_codes(T0c{}, 0);
+        load_sums(T0c{}, 0);
+        wait_vmcnt<0>();
+    }
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     decode(std::integral_constant<int, 0>{}, 0);
@@ -840,12 +887,12 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // in 8 waves, 128 x 32 in 8 waves, 32 x 128, 32 x 64, 64 x 16, 32 x 32,
     // three stages, and two row tiles per wave.
     // Q6_K at 33..64 tokens: decoded slabs of 16 rows x 64 tokens in 16
-    // waves, four K groups of four (down 2560 x 9728 at M = 48 / 64: 20.4 /
-    // 21.8 us against 23 / 27.1 for the 16 x 16 K-split tiles, which decode
-    // each block once per 16 tokens). Fewer tokens, and Q4_K / Q5_K, measured
-    // slower than the small-M kernels.
+    // waves, four K groups of four, steps two deep (down 2560 x 9728 at M =
+    // 48 / 64: 20.1 / 20.8 us; one deep 21.9 / 22.2; 23 / 27.1 for the 16 x 16
+    // K-split tiles, which decode each block once per 16 tokens). Fewer
+    // tokens, and Q4_K / Q5_K, measured slower than the small-M kernels.
     if (a.M <= 64) {
-        if constexpr (std::is_same_v<F, MQ6KS>) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4>, F>(tasks, n, x, s);
+        if constexpr (std::is_same_v<F, MQ6KS>) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
         return hipErrorNotSupported;
     }
     // Q6_K / Q5_K from 128 tokens: decoded slabs (their decoding is costly
