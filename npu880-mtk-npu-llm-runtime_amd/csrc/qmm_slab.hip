@@ -889,10 +889,19 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // Q6_K at 33..64 tokens: decoded slabs of 16 rows x 64 tokens in 16
     // waves, four K groups of four, steps two deep (down 2560 x 9728 at M =
     // 48 / 64: 20.1 / 20.8 us; one deep 21.9 / 22.2; 23 / 27.1 for the 16 x 16
-    // K-split tiles, which decode each block once per 16 tokens). Fewer
-    // tokens, and Q4_K / Q5_K, measured slower than the small-M kernels.
+    // K-split tiles, which decode each block once per 16 tokens). At 17..32
+    // tokens, where the row tiles are no more than the CUs, 16 x 32 in 8 waves
+    // (M = 24 / 32: 17.3 / 17.3 us against 18.7 / 18.6 on the K-split tiles).
+    // At 9..16 tokens (16.9 against 13.2 us), and Q4_K / Q5_K, slower than
+    // the small-M kernels.
     if (a.M <= 64) {
-        if constexpr (std::is_same_v<F, MQ6KS>) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
+        if constexpr (std::is_same_v<F, MQ6KS>) {
+            if (a.M > 32) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
+            int tiles = 0;
+            for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
+            if (a.M > 16 && tiles <= mfma_cu_count())
+                return launch_dslab_t<DsCfg<F, 1, 8, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
+        }
         return hipErrorNotSupported;
     }
     // Q6_K / Q5_K from 128 tokens: decoded slabs (their decoding is costly

@@ -485,12 +485,16 @@ def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task
     (64, 9728, (2560,), None),
     (48, 4352, (300, 45), 1),
     (33, 9728, (130,), 0),
+    (32, 9728, (2560,), None),
+    (24, 4352, (300, 45), 1),
+    (17, 9728, (130,), 0),
 ])
 def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
-    """Q6_K at 33..64 tokens over long K: decoded slabs whose four K groups
-    walk every fourth block and meet in block order; task groups, partial
-    row slabs, a residual, K not a multiple of 4 blocks (17 and 38 blocks);
-    every row of every task, all tokens, against the oracle."""
+    """Q6_K at 17..64 tokens over long K (16 x 32 slabs up to 32 tokens,
+    16 x 64 past): decoded slabs whose four K groups walk every fourth block
+    and meet in block order, steps two deep; task groups, partial row slabs,
+    a residual, K not a multiple of 4 blocks (17 and 38 blocks); every row
+    of every task, all tokens, against the oracle."""
     say(f"small-M Q6_K K-split decoded slabs M={M} K={K} tasks={specs}")
     x = synth.activations(M, K, seed=3700 + M)
     xb = ctx.upload(x)
