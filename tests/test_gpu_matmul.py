@@ -488,13 +488,15 @@ def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task
     (32, 9728, (2560,), None),
     (24, 4352, (300, 45), 1),
     (17, 9728, (130,), 0),
+    (20, 3328, (200,), None),
 ])
 def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
     """Q6_K at 17..64 tokens over long K (16 x 32 slabs up to 32 tokens,
     16 x 64 past): decoded slabs whose four K groups walk every fourth block
     and meet in block order, steps two deep; task groups, partial row slabs,
-    a residual, K not a multiple of 4 blocks (17 and 38 blocks); every row
-    of every task, all tokens, against the oracle."""
+    a residual, K not a multiple of 4 blocks (13, 17 and 38 blocks: four
+    to ten steps, the transfers issued past the last block reading zeros);
+    every row of every task, all tokens, against the oracle."""
     say(f"small-M Q6_K K-split decoded slabs M={M} K={K} tasks={specs}")
     x = synth.activations(M, K, seed=3700 + M)
     xb = ctx.upload(x)
