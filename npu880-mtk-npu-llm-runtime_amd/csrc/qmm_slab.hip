@@ -697,6 +697,7 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
         // so no load sits behind a branch (the compiler would wait for it to
         // copy registers where the paths join)
         if (KS == 1 || DEEP || j < nbk) {
+            const int jd = min(j, nbk - 1);  // (a DEEP block past K reads block nbk - 1's scales)
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const uint8_t *dr = db + r * C::RTB;
@@ -742,7 +743,7 @@ __global__ __launch_bounds__(64 * C::NW, C::WPS) void dslab_kernel(MatGroup grp,
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int S = (D1[t][q] << F::kShift) + D2[t][q];
-                        const float dx = sdx[((lw * TW + t) * 16 + 4 * cl + q) * nbk + j];
+                        const float dx = sdx[((lw * TW + t) * 16 + 4 * cl + q) * nbk + jd];
                         if constexpr (C::MIN)
                             v[q] = dx * (dd.x * (float)S - dd.y * Mb[t][q]);  // E:11026 / E:11063
                         else
