@@ -118,3 +118,38 @@ def test_gemm_sweep(ctx, oracle, case):
     if res is not None:
         task["residual"] = res
     check_outputs(y, oracle.gemm_multi(x, [task])[0], f"sweep {NAMES[t]} N={N} K={K} M={M}")
+
+
+def _small_m_cases(n, seed):
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        t = int(g.choice([TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0]))
+        M = int(g.choice([int(g.integers(2, 5)), int(g.integers(5, 17)), int(g.integers(17, 33)), int(g.integers(33, 65))]))
+        K = int(g.choice([256, 768, 2560, 3072, 3328, 4352, 9728]))
+        if t == TYPE_Q8_0:
+            K = int(g.choice([32, 288, 1024, 2560, 4096]))
+        hi = 10000 if K <= 3072 else 3200  # (keeps the oracle's share of the sweep to seconds)
+        N = int(g.choice([int(g.integers(1, 700)), int(g.integers(2000, 3000)), int(g.integers(3000, hi))]))
+        out.append((t, M, N, K, bool(g.integers(0, 2)), int(g.integers(0, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _small_m_cases(24, 13),
+                         ids=lambda c: f"{NAMES[c[0]]}-M{c[1]}-N{c[2]}-K{c[3]}-r{int(c[4])}")
+def test_gemm_small_m_sweep(ctx, oracle, case):
+    """2..64 tokens: whichever kernel the dispatcher picks for the shape
+    (the batch-1 shape for a few tokens, resident tiles, part tiles on token
+    groups, chunked tiles, decoded slabs split over K), bit for bit."""
+    t, M, N, K, residual, seed = case
+    say(f"small-M sweep {NAMES[t]} M={M} N={N} K={K} residual={residual}")
+    w = synth.weights(t, N, K, seed=seed)
+    x = synth.activations(M, K, seed=seed + 1)
+    res = synth.activations(M, N, seed=seed + 2) if residual else None
+    wb = ctx.weight_upload(w, t, N, K)
+    y = ctx.gemm(t, wb, N, K, x, res)
+    ctx.free(wb)
+    task = dict(w=w, type=t, rows=N)
+    if res is not None:
+        task["residual"] = res
+    check_outputs(y, oracle.gemm_multi(x, [task])[0], f"small-M sweep {NAMES[t]} M={M} N={N} K={K}")
