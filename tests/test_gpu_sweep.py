@@ -153,3 +153,36 @@ def test_gemm_small_m_sweep(ctx, oracle, case):
     if res is not None:
         task["residual"] = res
     check_outputs(y, oracle.gemm_multi(x, [task])[0], f"small-M sweep {NAMES[t]} M={M} N={N} K={K}")
+
+
+def _prefill_cases(n, seed):
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        t = int(g.choice([TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0]))
+        M = int(g.integers(65, 300))
+        K = int(g.choice([256, 1280, 2560, 3072, 4352, 9728]))
+        if t == TYPE_Q8_0:
+            K = int(g.choice([64, 1024, 2560, 4096]))
+        N = int(g.integers(1, 1500 if K <= 3072 else 500))
+        out.append((t, M, N, K, bool(g.integers(0, 2)), int(g.integers(0, 1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _prefill_cases(12, 17),
+                         ids=lambda c: f"{NAMES[c[0]]}-M{c[1]}-N{c[2]}-K{c[3]}-r{int(c[4])}")
+def test_gemm_prefill_sweep(ctx, oracle, case):
+    """65..300 tokens on ragged shapes: the slab kernels (packed or decoded,
+    each slab shape the launcher picks) and the Q8_0 tiles, bit for bit."""
+    t, M, N, K, residual, seed = case
+    say(f"prefill sweep {NAMES[t]} M={M} N={N} K={K} residual={residual}")
+    w = synth.weights(t, N, K, seed=seed)
+    x = synth.activations(M, K, seed=seed + 1)
+    res = synth.activations(M, N, seed=seed + 2) if residual else None
+    wb = ctx.weight_upload(w, t, N, K)
+    y = ctx.gemm(t, wb, N, K, x, res)
+    ctx.free(wb)
+    task = dict(w=w, type=t, rows=N)
+    if res is not None:
+        task["residual"] = res
+    check_outputs(y, oracle.gemm_multi(x, [task])[0], f"prefill sweep {NAMES[t]} M={M} N={N} K={K}")
