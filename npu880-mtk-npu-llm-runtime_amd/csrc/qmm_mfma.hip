@@ -1120,8 +1120,17 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
             return launch_tile_t<TileCfg<F, 1, 3, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
         else if constexpr (F::kSplit)
             return launch_tile_t<TileCfg<F, 1, 4, 4, 1, 1, 16, 2, 76 * 1024>, F>(tasks, n, x, s);
-        else  // Q8_0: a fp32 term per 32 values; smaller tiles, 3 workgroups per CU
+        else {  // Q8_0: a fp32 term per 32 values; smaller tiles, 3 workgroups per CU
+            // 64 x 32 tiles; 64 x 16 where the 64 x 32 tiles number at most 1.5
+            // per CU (2560 x 2560 at M = 65 / 128 / 256: 20.4 / 20.5 / 23.4 ->
+            // 15.0 / 16.9 / 20.4 us; 6144 x 2560 at M = 128: 24.0 -> 21.6; at
+            // 1.56 per CU and above slower: 2560 x 2560 at M = 320 23.7 -> 29.2)
+            int wg = 0;
+            for (int i = 0; i < n; ++i) wg += (tasks[i].N + 63) / 64 * ((a.M + 31) / 32);
+            if (2 * wg <= 3 * mfma_cu_count())
+                return launch_tile_t<TileCfg<F, 1, 1, 4, 1, 1, 16, 2, 52 * 1024>, F>(tasks, n, x, s);
             return launch_tile_t<TileCfg<F, 1, 2, 4, 1, 1, 16, 2, 52 * 1024>, F>(tasks, n, x, s);
+        }
     }
 }
 

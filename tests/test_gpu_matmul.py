@@ -304,6 +304,34 @@ def test_prefill_task_group(ctx, oracle):
         ctx.free(b)
 
 
+@pytest.mark.parametrize("M,specs", [(200, (2560, 130, 64)), (400, (2560, 70))])
+def test_prefill_q8_0_tile_shapes(ctx, oracle, M, specs):
+    """Q8_0 past 64 tokens in task groups: 64 x 16 tiles where the 64 x 32
+    tiles would number at most 1.5 per CU (M = 200), else 64 x 32 (M = 400),
+    the first task with a residual."""
+    K = 2560
+    say(f"prefill Q8_0 tiles M={M} tasks={specs}")
+    x = synth.activations(M, K, seed=3500 + M)
+    ws = [synth.weights(TYPE_Q8_0, n, K, seed=3501 + i) for i, n in enumerate(specs)]
+    res = synth.activations(M, specs[0], seed=3510 + M)
+    xb = ctx.upload(x)
+    rb = ctx.upload(res)
+    wbs = [ctx.weight_upload(w, TYPE_Q8_0, n, K) for w, n in zip(ws, specs)]
+    ybs = [ctx.malloc(M * n * 4) for n in specs]
+    tasks = [qmm_hip.MatrixTask(wb, TYPE_Q8_0, n, K, yb, n, residual=rb if i == 0 else None,
+                                res_stride=specs[0] if i == 0 else 0)
+             for i, (wb, yb, n) in enumerate(zip(wbs, ybs, specs))]
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    tdicts = [dict(w=w, type=TYPE_Q8_0, rows=n) for w, n in zip(ws, specs)]
+    tdicts[0]["residual"] = res
+    refs = oracle.gemm_multi(x, tdicts)
+    for i, (n, yb) in enumerate(zip(specs, ybs)):
+        check_outputs(ctx.d2h(yb, np.float32, (M, n)), refs[i], f"Q8_0 group task {i}")
+    for b in [xb, rb] + wbs + ybs:
+        ctx.free(b)
+
+
 # ---------------------------------------------------------------- dispatch
 @pytest.mark.parametrize("M", [1, 6])
 def test_multi_task_dispatch_mixed_types(ctx, oracle, M):
