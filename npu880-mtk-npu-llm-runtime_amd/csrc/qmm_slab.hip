@@ -877,16 +877,14 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
         if (aligned && ((reinterpret_cast<uintptr_t>(tasks[i].w) | tasks[i].row_bytes) & 15)) return hipErrorNotSupported;
         if (size_t(tasks[i].N) * tasks[i].row_bytes + 16 >= (size_t(1) << 31)) return hipErrorNotSupported;
     }
-    // 128 rows x 64 tokens in 8 waves where those slabs give at least four
-    // workgroups per CU: two fit a CU (2 x 74 KB of LDS, <= 128 VGPRs), so
-    // four waves per SIMD, and the 64 tokens' codes staged once per 128 rows
-    // (gate + up 2 x 9728 x 2560 at M = 512: 87.5 -> 79.1 us). Else 64 x 64
-    // (two workgroups per CU; QKV 6144 x 2560: 35.7 us against 48.1 for
-    // 128 x 64 on its 384 slabs), and 64 x 32 (three or four per CU) where
-    // 64 x 64 gives fewer than two (O 2560 x 4096 at M = 512: 28.5 -> 23.9 us,
-    // down 2560 x 9728: 77.8 -> 75.3 us). Measured slower at M = 512: 128 x 128
-    // in 8 waves, 128 x 32 in 8 waves, 32 x 128, 32 x 64, 64 x 16, 32 x 32,
-    // three stages, and two row tiles per wave.
+    // Packed slabs (the shape is chosen at the end): 128 rows x 64 tokens in
+    // 8 waves, two per CU (2 x 74 KB of LDS, <= 128 VGPRs), so four waves per
+    // SIMD and the 64 tokens' codes staged once per 128 rows (gate + up 2 x
+    // 9728 x 2560 at M = 512: 87.5 -> 79.1 us); 64 x 64 (two per CU); 64 x 32
+    // (three or four per CU: O 2560 x 4096 at M = 512: 28.5 -> 23.9 us).
+    // Measured slower at M = 512: 128 x 128 in 8 waves, 128 x 32 in 8 waves,
+    // 32 x 128, 32 x 64, 64 x 16, 32 x 32, three stages, and two row tiles
+    // per wave.
     // Q6_K at 33..64 tokens: decoded slabs of 16 rows x 64 tokens in 16
     // waves, four K groups of four, steps two deep (down 2560 x 9728 at M =
     // 48 / 64: 20.1 / 20.8 us; one deep 21.9 / 22.2; 23 / 27.1 for the 16 x 16
@@ -913,11 +911,22 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // 24.0 / 31.2 / 37.2 / 63.1. Q4_K stays on the slab kernel (gate + up and
     // O at M = 512: 86.5 and 29.0 us against 78.9 and 28.0): its epilogue
     // outweighs its decoding, and the slab kernel fits more waves per SIMD.
-    if (a.M >= 128) {
-        hipError_t e = hipErrorNotSupported;
-        if constexpr (std::is_same_v<F, MQ6KS>) e = launch_dslab_t<DsCfg<F, 1, 4, 2>, F>(tasks, n, x, s);
-        if constexpr (std::is_same_v<F, MQ5KS>) e = launch_dslab_t<DsCfg<F, 2, 4, 2>, F>(tasks, n, x, s);
-        if (e != hipErrorNotSupported) return e;
+    // Q6_K from 65 tokens (the tokens padded to 128): faster than the packed
+    // slabs at every height measured (down 2560 x 9728 at M = 65..127 38.6 ->
+    // 33.1 us; 1024 x 9728 38.6 -> 32.7, 1024 x 2560 12.9 -> 11.6, 4096 x
+    // 2560 13.0 -> 11.9 at M = 65..512). Q5_K where its workgroups number at
+    // least 5/8 of the CUs (QKV 6144 x 2560 at M = 65..127 17.4 -> 16.1 us;
+    // 4096 x 2560 at M = 128 12.8 against 16.2, 1024 x 2560 12.3 against 15.8
+    // on the packed slabs: there they stay).
+    if constexpr (std::is_same_v<F, MQ6KS> || std::is_same_v<F, MQ5KS>) {
+        int wgs = 0;
+        for (int i = 0; i < n; ++i) wgs += (tasks[i].N + 31) / 32;
+        if (std::is_same_v<F, MQ6KS> || 8 * wgs * ((a.M + 127) / 128) >= 5 * mfma_cu_count()) {
+            hipError_t e = hipErrorNotSupported;
+            if constexpr (std::is_same_v<F, MQ6KS>) e = launch_dslab_t<DsCfg<F, 1, 4, 2>, F>(tasks, n, x, s);
+            if constexpr (std::is_same_v<F, MQ5KS>) e = launch_dslab_t<DsCfg<F, 2, 4, 2>, F>(tasks, n, x, s);
+            if (e != hipErrorNotSupported) return e;
+        }
     }
     int slabs = 0, slabs128 = 0;
     for (int i = 0; i < n; ++i) {
@@ -925,10 +934,17 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
         slabs128 += (tasks[i].N + 127) / 128;
     }
     const int tg64 = (a.M + 63) / 64, cus = mfma_cu_count();
+    const int w128 = slabs128 * tg64, w64 = slabs * tg64;  // workgroups of the 128 x 64 / 64 x 64 shapes
+    // 128 x 64 in 8 waves where those workgroups number at least 1.5 per CU;
+    // 64 x 64 where they make one round of two per CU (1.75..2 per CU); else
+    // 64 x 32. Measured (Q4_K, M = 65..512, K = 2560, kernel alone): 19456
+    // rows at M = 65 / 128 / 384 32.5 / 33.5 / 72.5 -> 23.0 / 30.0 / 59.8 us,
+    // 9728 rows at M = 256 33.2 -> 28.0, 6144 rows at M = 384 32.2 -> 27.0;
+    // M = 512 of gate + up and O unchanged (128 x 64 and 64 x 32).
     //                                                         RW TW PR PD NW WPS
-    if (slabs128 * tg64 >= 4 * cus) return launch_slab_t<SlabCfg<F, 1, 4, 8, 2, 8, 4>, F>(tasks, n, x, s);
-    if (slabs * tg64 < 2 * cus) return launch_slab_t<SlabCfg<F, 1, 2, 4, 2>, F>(tasks, n, x, s);
-    return launch_slab_t<SlabCfg<F, 1, 4, 4, 2>, F>(tasks, n, x, s);
+    if (2 * w128 >= 3 * cus) return launch_slab_t<SlabCfg<F, 1, 4, 8, 2, 8, 4>, F>(tasks, n, x, s);
+    if (4 * w64 >= 7 * cus && w64 <= 2 * cus) return launch_slab_t<SlabCfg<F, 1, 4, 4, 2>, F>(tasks, n, x, s);
+    return launch_slab_t<SlabCfg<F, 1, 2, 4, 2>, F>(tasks, n, x, s);
 }
 
 template hipError_t launch_slab<MQ4KS>(const MatArgs *, int, const Q8KView &, hipStream_t);

@@ -278,6 +278,14 @@ def test_prefill_tails(ctx, oracle, type_id, N, K, M):
     _run(ctx, oracle, type_id, N, K, M, seed=3200 + N + M + type_id)
 
 
+@pytest.mark.parametrize("M", [65, 100])
+def test_prefill_q5k_decoded_slabs_under_128(ctx, oracle, M):
+    """Q5_K past 64 tokens on a tensor whose 32-row decoded slabs number at
+    least 5/8 of the CUs: the decoded slabs with the tokens padded to 128
+    (below that height the packed slabs), with a residual."""
+    _run(ctx, oracle, TYPE_Q5_K, 5200, 2560, M, seed=3600 + M, residual=True)
+
+
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0])
 def test_prefill_residual(ctx, oracle, type_id):
     _run(ctx, oracle, type_id, 150, 2560, 140, seed=3300 + type_id, residual=True)
