@@ -1042,8 +1042,9 @@ template <class F>
 static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     const MatArgs &a = tasks[0];
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
-        // (Q6_K at 17..64 tokens over K > 3072: the decoded slabs split over K)
-        if (a.M > 64 || (std::is_same_v<F, MQ6KS> && a.M > 16 && a.K > 3072)) {
+        // (Q6_K at 17..64 tokens over K > 3072, Q4_K / Q5_K at 33..64 over
+        // K >= 8192: the decoded slabs split over K, where the launcher takes them)
+        if (a.M > 64 || (a.M > 16 && a.K > 3072 && (std::is_same_v<F, MQ6KS> || (a.M > 32 && a.K >= 8192)))) {
             const hipError_t e = launch_slab<typename Folded<F>::T>(tasks, n, x, s);
             if (e != hipErrorNotSupported) return e;
         }

@@ -891,9 +891,20 @@ hipError_t launch_slab(const MatArgs *tasks, int n, const typename ActOf<F>::T &
     // K-split tiles, which decode each block once per 16 tokens). At 17..32
     // tokens, where the row tiles are no more than the CUs, 16 x 32 in 8 waves
     // (M = 24 / 32: 17.3 / 17.3 us against 18.7 / 18.6 on the K-split tiles).
-    // At 9..16 tokens (16.9 against 13.2 us), and Q4_K / Q5_K, slower than
-    // the small-M kernels.
+    // At 9..16 tokens (16.9 against 13.2 us) slower than the small-M kernels.
+    // Q4_K / Q5_K at 33..64 tokens over K >= 8192 where the 16 x 16 K-split
+    // tiles would take more than two per CU (Q4_K 4096 x 9728 at M = 48 / 64:
+    // 21.6 / 26.2 -> 18.3 / 19.1 us, 2560 x 9728 at M = 64: 21.1 -> 18.9);
+    // over K = 4096, or within two per CU, the tiles stay (2560 x 9728 at
+    // M = 48: 15.5 against 18.0 us decoded).
     if (a.M <= 64) {
+        if constexpr (!std::is_same_v<F, MQ6KS>) {
+            int tiles = 0;
+            for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
+            const int cus = mfma_cu_count();
+            if (a.M > 32 && a.K >= 8192 && tiles <= cus && tiles * ((a.M + 15) / 16) > 2 * cus)
+                return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
+        }
         if constexpr (std::is_same_v<F, MQ6KS>) {
             if (a.M > 32) return launch_dslab_t<DsCfg<F, 1, 16, 1, 4, 3, 4, true>, F>(tasks, n, x, s);
             int tiles = 0;

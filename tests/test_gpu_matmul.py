@@ -557,6 +557,39 @@ def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
 
 
 @pytest.mark.parametrize("type_id,M,K,specs,res_task", [
+    (TYPE_Q4_K, 64, 9728, (2560,), None),
+    (TYPE_Q5_K, 48, 8192, (4096,), 0),
+    (TYPE_Q4_K, 40, 8448, (3000, 900), 1),
+])
+def test_small_m_q4k_q5k_decoded_slabs_long_k(ctx, oracle, type_id, M, K, specs, res_task):
+    """Q4_K / Q5_K at 33..64 tokens over K >= 8192 where the K-split tiles
+    would take more than two per CU: the decoded slabs in four K groups (the
+    mins as fp16 sums against fp16 mins), task groups, a residual, K of 33
+    blocks; every row of every task, all tokens, against the oracle."""
+    say(f"small-M {NAMES[type_id]} K-split decoded slabs M={M} K={K} tasks={specs}")
+    x = synth.activations(M, K, seed=3800 + M)
+    xb = ctx.upload(x)
+    bufs, tasks, hosts, res_h = [xb], [], [], []
+    for i, n in enumerate(specs):
+        w = synth.weights(type_id, n, K, seed=3801 + i + M)
+        wb, yb = ctx.weight_upload(w, type_id, n, K), ctx.malloc(M * n * 4)
+        rh = synth.activations(M, n, seed=3820 + i) if res_task == i else None
+        rb = ctx.upload(rh) if rh is not None else None
+        bufs += [b for b in (wb, yb, rb) if b is not None]
+        tasks.append(qmm_hip.MatrixTask(wb, type_id, n, K, yb, n, residual=rb, res_stride=n if rh is not None else 0))
+        hosts.append(w)
+        res_h.append(rh)
+    ctx.gemm_multi_dispatch(xb, M, K, tasks)
+    ctx.sync()
+    refs = oracle.gemm_multi(x, [dict(w=w, type=type_id, rows=t.rows, **({"residual": rh} if rh is not None else {}))
+                                 for t, w, rh in zip(tasks, hosts, res_h)])
+    for i, t in enumerate(tasks):
+        check_outputs(ctx.d2h(t.dst, np.float32, (M, t.rows)), refs[i], f"long-K decoded slabs task {i}")
+    for b in bufs:
+        ctx.free(b)
+
+
+@pytest.mark.parametrize("type_id,M,K,specs,res_task", [
     (TYPE_Q4_K, 8, 2560, (9728,), None),
     (TYPE_Q4_K, 3, 2560, (9728,), 0),
     (TYPE_Q4_K, 16, 512, (4096, 1000), 1),
