@@ -1074,27 +1074,32 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // up to 64 tokens over K <= 3072: the resident-tile and part kernels.
     // Past 16 tokens the part kernel's workgroups each take a group of 16
     // or 32 tokens (a grid row per group): at 17..32 tokens groups of 16
-    // where the row tiles are no more than the CUs (else all 32 tokens per
-    // workgroup), at 33..48 groups of 16, at 49..64 groups of 32. Measured
-    // (Q4_K 9728 x 2560 / Q5_K 4096 x 2560, M = 24, 40, 48, 64): 10.22 /
-    // 6.60, 13.37 / 7.79, 12.93 / 7.87, 14.02 / 8.70 us against one
-    // workgroup per row tile (Q4_K past 32 tokens: the 64 x 32 tiles) 10.22
-    // / 7.28, 14.90 / 8.33, 14.94 / 8.28, 15.32 / 9.27.
+    // where the row tiles are at most two per CU (else all 32 tokens per
+    // workgroup), at 33..48 groups of 16, at 49..64 groups of 32 (of 16
+    // where those would leave half the CUs idle). Measured (Q4_K 9728 x
+    // 2560 / Q5_K 4096 x 2560, M = 24, 40, 48, 64): 10.22 / 6.60, 13.37 /
+    // 7.79, 12.93 / 7.87, 14.02 / 8.70 us against one workgroup per row
+    // tile (Q4_K past 32 tokens: the 64 x 32 tiles) 10.22 / 7.28, 14.90 /
+    // 8.33, 14.94 / 8.28, 15.32 / 9.27; from a sweep of six tensors at
+    // M = 5..64: Q4_K 19456 x 2560 at M = 5..16 13.5..14.4 -> 11.0..11.1
+    // (one tile per workgroup past three tiles per CU), Q5_K 6144 x 2560 at
+    // M = 24 / 32 9.3 -> 8.1 / 8.3, Q5_K 1024 x 2560 at M = 64 6.8 -> 5.3.
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
         if (a.K <= 3072) {
+            const int tiles = group_tiles(tasks, n), cus = mfma_cu_count();
             if (a.M <= 16) {
                 // several resident tiles per CU where the tiles outnumber
-                // the CUs (measured faster there), else one per workgroup
-                if (group_tiles(tasks, n) > mfma_cu_count()) e = launch_res<F, 1>(tasks, n, x, s);
+                // the CUs up to three per CU (measured faster there), else
+                // one per workgroup
+                if (tiles > cus && tiles <= 3 * cus) e = launch_res<F, 1>(tasks, n, x, s);
                 if (e == hipErrorNotSupported) e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 32) {
-                e = group_tiles(tasks, n) <= mfma_cu_count() ? launch_part<F, 1>(tasks, n, x, s)
-                                                             : launch_part<G, 2>(tasks, n, x, s);
+                e = tiles <= 2 * cus ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             } else if (a.M <= 48) {
                 e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 64) {
-                e = launch_part<G, 2>(tasks, n, x, s);
+                e = 2 * tiles < cus ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             }
         }
         if (e != hipErrorNotSupported) return e;
