@@ -967,9 +967,9 @@ static hipError_t launch_res_r(const MatArgs *tasks, int n, const Q8KView &x, in
 // (three or four token tiles, as the mixed-group kernel uses) only one fits
 // a CU, and the tiles must not outnumber the CUs.
 // LDS offsets of the part-kernel body of format F for (M, K)
-template <class F, int TT>
+template <class F, int TT, int NBK = 3>
 static ResArgs part_args(int M, int K) {
-    using C = PartCfg<F, TT, 3>;
+    using C = PartCfg<F, TT, NBK>;
     using P = typename C::P;
     const int nb = K / 256;
     ResArgs ra{};
@@ -979,15 +979,14 @@ static ResArgs part_args(int M, int K) {
     return ra;
 }
 
-template <class F, int TT>
-static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
-    constexpr int NBK = 3;
+template <class F, int TT, int NBK>
+static hipError_t launch_part_n(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
     const MatArgs &a = tasks[0];
     const int nb = a.K / 256;
     int tiles = 0;
     for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
     if (nb > 4 * NBK || !x.qt || (TT > 2 && tiles > mfma_cu_count())) return hipErrorNotSupported;
-    ResArgs ra = part_args<F, TT>(a.M, a.K);
+    ResArgs ra = part_args<F, TT, NBK>(a.M, a.K);
     ra.tiles = tiles;
     if (ra.lds > 160 * 1024) return hipErrorNotSupported;
     MatGroup g{};
@@ -1000,6 +999,13 @@ static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hip
     const dim3 grid(unsigned(tiles), unsigned((a.M + 16 * TT - 1) / (16 * TT)));
     hipLaunchKernelGGL((part_kernel<F, TT, NBK>), grid, dim3(256), size_t(ra.lds), s, g, x, ra);
     return hipGetLastError();
+}
+
+// up to 3 blocks per K part (K <= 3072), else 4 (K <= 4096)
+template <class F, int TT>
+static hipError_t launch_part(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
+    if (tasks[0].K <= 3072) return launch_part_n<F, TT, 3>(tasks, n, x, s);
+    return launch_part_n<F, TT, 4>(tasks, n, x, s);
 }
 
 static int group_tiles(const MatArgs *tasks, int n) {
@@ -1086,7 +1092,11 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // M = 24 / 32 9.3 -> 8.1 / 8.3, Q5_K 1024 x 2560 at M = 64 6.8 -> 5.3.
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
-        if (a.K <= 3072) {
+        // (K up to 4096 from 17 tokens, on the tensors the K-split tiles
+        // above leave: Q4_K 9728 x 4096 at M = 24 / 48 / 64 16.0 / 21.6 /
+        // 21.8 -> 14.4 / 18.2 / 20.3 us against the chunked tiles, 6144 x
+        // 3584 at M = 48 14.3 -> 12.1; at 8 tokens or fewer mixed, not taken)
+        if (a.K <= 3072 || (a.K <= 4096 && a.M > 16)) {
             const int tiles = group_tiles(tasks, n), cus = mfma_cu_count();
             if (a.M <= 16) {
                 // several resident tiles per CU where the tiles outnumber

@@ -153,11 +153,13 @@ def test_mfma_wide_tiles_long_k(ctx, oracle, type_id, N, K, M):
 
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 13000, 2560, 8, True), (TYPE_Q5_K, 12400, 1536, 16, False),
                                                     (TYPE_Q5_K, 1000, 2560, 60, True), (TYPE_Q6_K, 2000, 768, 49, False),
-                                                    (TYPE_Q5_K, 6144, 2560, 24, False)])
+                                                    (TYPE_Q5_K, 6144, 2560, 24, False), (TYPE_Q4_K, 9728, 4096, 24, True),
+                                                    (TYPE_Q5_K, 6144, 3584, 48, False), (TYPE_Q6_K, 9000, 3328, 64, True)])
 def test_small_m_token_group_bounds(ctx, oracle, type_id, N, K, M, residual):
     """The part kernel where the resident tiles would hold more than three
     per CU (M <= 16), 16-token groups at 49..64 tokens on few row tiles and
-    at 17..32 on up to two tiles per CU."""
+    at 17..32 on up to two tiles per CU, and over K up to 4096 (4 blocks per
+    K part) from 17 tokens on tall tensors."""
     _run(ctx, oracle, type_id, N, K, M, seed=4100 + N + M, residual=residual)
 
 
