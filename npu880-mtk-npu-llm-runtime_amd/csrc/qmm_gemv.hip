@@ -1177,7 +1177,9 @@ static hipError_t launch_gemv_mixed_persist(const MatArgs *tasks, int n, const f
 // Rows per wave by the launch's total rows and K (measured per shape): the
 // k-quants take 4 from 4096 rows, else 2 up to K = 4096, else 1 (the 2560-row
 // K = 9728 down projection: 12.4 -> 8.9 us with 1); Q8_0 (34-B blocks, 5
-// wave steps per batch) takes 4 from 8192 rows, 2 from 4096, else 1.
+// wave steps per batch) takes 1 at every size (4096x2560: 6.3 -> 4.9 us,
+// 9728x2560: 9.9 -> 7.9, 19456x2560: 14.0 -> 13.2, 8192x4096: 14.3 -> 13.4
+// against the 2 / 4 rows it took from 4096 / 8192 rows).
 template <class F, int U>
 static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32, const Q8KView &xk,
                                    const Q80View &x0, hipStream_t s) {
@@ -1189,9 +1191,10 @@ static hipError_t launch_gemv_rows(const MatArgs *tasks, int n, const float *x32
                 return e;
     int64_t rows = 0;
     for (int i = 0; i < n; ++i) rows += tasks[i].N;
-    const bool q80 = IsQ80<F>::v;
-    if (rows >= (q80 ? 8192 : 4096)) return launch_gemv_t<F, kGemvR, U>(tasks, n, x32, xk, x0, s);
-    if (q80 ? rows >= 4096 : tasks[0].K <= 4096) return launch_gemv_t<F, 2, U>(tasks, n, x32, xk, x0, s);
+    if constexpr (!IsQ80<F>::v) {
+        if (rows >= 4096) return launch_gemv_t<F, kGemvR, U>(tasks, n, x32, xk, x0, s);
+        if (tasks[0].K <= 4096) return launch_gemv_t<F, 2, U>(tasks, n, x32, xk, x0, s);
+    }
     return launch_gemv_t<F, 1, U>(tasks, n, x32, xk, x0, s);
 }
 

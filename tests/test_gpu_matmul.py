@@ -62,6 +62,15 @@ def test_gemv_two_group_grid(ctx, oracle, type_id, N, K, residual):
     _run(ctx, oracle, type_id, N, K, 1, seed=1200 + N + type_id, residual=residual)
 
 
+@pytest.mark.parametrize("N,K,residual", [(4096, 2560, False), (9731, 2560, True), (8192, 4096, False),
+                                          (19456, 2560, True)])
+def test_gemv_q8_0_one_row_per_wave(ctx, oracle, N, K, residual):
+    """Q8_0 at one token takes one row per wave at every size: the shapes
+    that took 2 (from 4096 rows) and 4 (from 8192 rows) before, on the
+    persistent grid, with a ragged row count."""
+    _run(ctx, oracle, TYPE_Q8_0, N, K, 1, seed=1250 + N, residual=residual)
+
+
 def test_gemv_two_group_grid_unaligned_base(ctx, oracle):
     """The same grid on a weight pointer 8 B past a 16-B boundary: rows
     1..N of an uploaded N + 1 (840-B Q6_K rows)."""
