@@ -1019,13 +1019,13 @@ static int group_tiles(const MatArgs *tasks, int n) {
     return tiles;
 }
 
+// The resident tiles three to a workgroup, where the row tiles number more
+// than two and at most three per CU; hipErrorNotSupported (nothing
+// launched) elsewhere.
 template <class F, int TT>
 static hipError_t launch_res(const MatArgs *tasks, int n, const Q8KView &x, hipStream_t s) {
-    int tiles = 0;
-    for (int i = 0; i < n; ++i) tiles += (tasks[i].N + 15) / 16;
-    const int cus = mfma_cu_count();
-    if (tiles <= cus) return launch_res_r<F, TT, 3, 1>(tasks, n, x, tiles, s);
-    if (tiles <= 2 * cus) return launch_res_r<F, TT, 3, 2>(tasks, n, x, tiles, s);
+    const int tiles = group_tiles(tasks, n), cus = mfma_cu_count();
+    if (tiles <= 2 * cus || tiles > 3 * cus) return hipErrorNotSupported;
     return launch_res_r<F, TT, 3, 3>(tasks, n, x, tiles, s);
 }
 
@@ -1104,13 +1104,20 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
         if (a.K <= 3072 || (a.K <= 4096 && a.M > 16)) {
             const int tiles = group_tiles(tasks, n), cus = mfma_cu_count();
             if (a.M <= 16) {
-                // several resident tiles per CU where the tiles outnumber
-                // the CUs up to three per CU (measured faster there), else
-                // one per workgroup
-                if (tiles > cus && tiles <= 3 * cus) e = launch_res<F, 1>(tasks, n, x, s);
+                // one tile per workgroup, but for Q4_K at 8 tokens or fewer
+                // on more than two row tiles per CU (up to three): there the
+                // resident tiles, three per workgroup, measure level or
+                // faster (9728 x 2560 at M = 5: 7.97 -> 7.78 us); elsewhere
+                // the part kernel is faster (Q5_K / Q6_K 6144 x 2560 at
+                // M = 16: 7.57 / 9.02 -> 6.90 / 8.18 us)
+                if (std::is_same_v<F, MQ4K> && a.M <= 8) e = launch_res<F, 1>(tasks, n, x, s);
                 if (e == hipErrorNotSupported) e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 32) {
-                e = tiles <= 2 * cus ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
+                // Q6_K (the costlier unpacking) takes all 32 tokens per
+                // workgroup from more than half a tile per CU (2560 x 2560
+                // at M = 24: 7.32 -> 6.99 us, 1024 x 2560: 5.99 against 6.75)
+                const bool g16 = tiles <= 2 * cus && !(std::is_same_v<F, MQ6KS> && 2 * tiles > cus);
+                e = g16 ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             } else if (a.M <= 48) {
                 e = launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 64) {

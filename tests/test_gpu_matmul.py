@@ -163,22 +163,34 @@ def test_mfma_wide_tiles_long_k(ctx, oracle, type_id, N, K, M):
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 13000, 2560, 8, True), (TYPE_Q5_K, 12400, 1536, 16, False),
                                                     (TYPE_Q5_K, 1000, 2560, 60, True), (TYPE_Q6_K, 2000, 768, 49, False),
                                                     (TYPE_Q5_K, 6144, 2560, 24, False), (TYPE_Q4_K, 9728, 4096, 24, True),
-                                                    (TYPE_Q5_K, 6144, 3584, 48, False), (TYPE_Q6_K, 9000, 3328, 64, True)])
+                                                    (TYPE_Q5_K, 6144, 3584, 48, False), (TYPE_Q6_K, 9000, 3328, 64, True),
+                                                    (TYPE_Q6_K, 2560, 2560, 24, True), (TYPE_Q6_K, 1024, 2560, 20, False),
+                                                    (TYPE_Q6_K, 2050, 2560, 32, False)])
 def test_small_m_token_group_bounds(ctx, oracle, type_id, N, K, M, residual):
     """The part kernel where the resident tiles would hold more than three
     per CU (M <= 16), 16-token groups at 49..64 tokens on few row tiles and
-    at 17..32 on up to two tiles per CU, and over K up to 4096 (4 blocks per
+    at 17..32 on up to two tiles per CU (Q6_K: up to half a tile per CU,
+    else all 32 tokens per workgroup), and over K up to 4096 (4 blocks per
     K part) from 17 tokens on tall tensors."""
     _run(ctx, oracle, type_id, N, K, M, seed=4100 + N + M, residual=residual)
 
 
+@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 9728, 2560, 8), (TYPE_Q4_K, 12288, 2560, 5),
+                                           (TYPE_Q4_K, 8500, 3072, 7), (TYPE_Q4_K, 8211, 768, 6)])
+def test_resident_tile_layouts(ctx, oracle, type_id, N, K, M):
+    """Q4_K at 8 tokens or fewer on two to three row tiles per CU: three
+    16-row tiles resident per workgroup, 12 blocks per row, a partial last
+    tile."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
+
+
 @pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q4_K, 6144, 2560, 8), (TYPE_Q6_K, 13000, 1024, 3),
                                            (TYPE_Q5_K, 300, 3072, 16), (TYPE_Q4_K, 4111, 768, 11),
-                                           (TYPE_Q6_K, 3000, 2560, 7)])
-def test_resident_tile_layouts(ctx, oracle, type_id, N, K, M):
-    """M <= 16, K <= 3072: one workgroup per CU with one, two or three
-    16-row tiles resident (and more workgroups than CUs past three tiles
-    per CU), 12 blocks per row, a partial last tile."""
+                                           (TYPE_Q6_K, 3000, 2560, 7), (TYPE_Q5_K, 6144, 2560, 12),
+                                           (TYPE_Q6_K, 6144, 2560, 16), (TYPE_Q4_K, 9728, 2560, 13)])
+def test_part_kernel_small_m_layouts(ctx, oracle, type_id, N, K, M):
+    """M <= 16, K <= 3072 outside those: one 16-row tile and 16 tokens per
+    workgroup at any tile count, 12 blocks per row, partial last tiles."""
     _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
 
 
