@@ -1074,7 +1074,9 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // 15.7 / 20.8 / 22.7; on taller tensors (Q4_K / Q6_K 9728 x 4096, Q8_0
     // 6144 x 2560) faster at M = 16 (12.0 / 14.9 / 13.3 against 13.6 / 16.5 /
     // 15.1), slower at M = 64 (27.9 / 36.4 / 27.5 against 21.8 / 28.9 / 23.0)
-    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>)) {
+    // (Q4_K / Q5_K up to 16 tokens over K <= 4096 take the part kernel below)
+    constexpr bool kQ45 = std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K>;
+    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>) && !(kQ45 && a.M <= 16 && a.K <= 4096)) {
         int wg = 0;  // workgroups of the configuration below
         for (int i = 0; i < n; ++i)
             wg += a.M <= 32 ? (tasks[i].N + 31) / 32 : (tasks[i].N + 63) / 64 * ((a.M + 31) / 32);
@@ -1100,8 +1102,13 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
         // (K up to 4096 from 17 tokens, on the tensors the K-split tiles
         // above leave: Q4_K 9728 x 4096 at M = 24 / 48 / 64 16.0 / 21.6 /
         // 21.8 -> 14.4 / 18.2 / 20.3 us against the chunked tiles, 6144 x
-        // 3584 at M = 48 14.3 -> 12.1; at 8 tokens or fewer mixed, not taken)
-        if (a.K <= 3072 || (a.K <= 4096 && a.M > 16)) {
+        // 3584 at M = 48 14.3 -> 12.1; and Q4_K / Q5_K at every M <= 16:
+        // Q4_K 9728 x 4096 at M = 8 / 16 10.4 / 12.0 -> 10.2 / 10.2 us,
+        // 19456 x 4096 at M = 12 18.3 -> 14.3, 2560 x 4096 at M = 8 6.65 ->
+        // 5.83, Q5_K 2560 x 3328 at M = 8 / 16 6.81 / 6.88 -> 6.05 / 6.02,
+        // against the 8-token and the K-split tiles; Q6_K measured slower
+        // at 8 tokens, 4096 x 4096 7.8 -> 8.2)
+        if (a.K <= 3072 || (a.K <= 4096 && (a.M > 16 || kQ45))) {
             const int tiles = group_tiles(tasks, n), cus = mfma_cu_count();
             if (a.M <= 16) {
                 // one tile per workgroup, but for Q4_K at 8 tokens or fewer

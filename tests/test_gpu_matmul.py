@@ -135,17 +135,17 @@ def test_unaligned_tensor_end(ctx, oracle, type_id, K, M):
     _run(ctx, oracle, type_id, 45, K, M, seed=500 + K + M)
 
 
-@pytest.mark.parametrize("type_id,K,M", [(TYPE_Q4_K, 4096, 8), (TYPE_Q6_K, 9728, 12), (TYPE_Q8_0, 3072, 5),
-                                         (TYPE_Q5_K, 2816, 16)])
+@pytest.mark.parametrize("type_id,K,M", [(TYPE_Q6_K, 4096, 8), (TYPE_Q6_K, 9728, 12), (TYPE_Q8_0, 3072, 5),
+                                         (TYPE_Q5_K, 2816, 16), (TYPE_Q4_K, 4352, 8)])
 def test_mfma_small_m_long_k(ctx, oracle, type_id, K, M):
     """M <= 16 with K past the resident-codes limit (2560): codes stream with
-    the weights, chunk by chunk."""
+    the weights, chunk by chunk (Q5_K at K = 2816: the part kernel)."""
     _run(ctx, oracle, type_id, 70, K, M, seed=900 + K + M)
 
 
 @pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q6_K, 2560, 9728, 64), (TYPE_Q5_K, 300, 4096, 40),
                                            (TYPE_Q4_K, 333, 9728, 17), (TYPE_Q6_K, 200, 3328, 33),
-                                           (TYPE_Q8_0, 2560, 2560, 48), (TYPE_Q4_K, 1000, 4096, 9),
+                                           (TYPE_Q8_0, 2560, 2560, 48), (TYPE_Q6_K, 1000, 4096, 9),
                                            (TYPE_Q8_0, 130, 9728, 64)])
 def test_mfma_k_split_tiles(ctx, oracle, type_id, N, K, M):
     """9..64 tokens over K > 3072 (and Q8_0 at any K): 16 x 16 tiles whose
@@ -192,6 +192,15 @@ def test_part_kernel_small_m_layouts(ctx, oracle, type_id, N, K, M):
     """M <= 16, K <= 3072 outside those: one 16-row tile and 16 tokens per
     workgroup at any tile count, 12 blocks per row, partial last tiles."""
     _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
+
+
+@pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 4096, 8, True), (TYPE_Q4_K, 19456, 4096, 12, False),
+                                                    (TYPE_Q5_K, 2560, 3328, 16, True), (TYPE_Q5_K, 1000, 3584, 3, False),
+                                                    (TYPE_Q4_K, 1000, 4096, 9, False), (TYPE_Q5_K, 6144, 4096, 5, True)])
+def test_part_kernel_small_m_long_k(ctx, oracle, type_id, N, K, M, residual):
+    """Q4_K / Q5_K up to 16 tokens over 3072 < K <= 4096: the part kernel
+    with 4 blocks per K part (13..16 blocks per row), partial last tiles."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1600 + N + M, residual=residual)
 
 
 @pytest.mark.parametrize("M", [8, 16, 32, 48, 64])
