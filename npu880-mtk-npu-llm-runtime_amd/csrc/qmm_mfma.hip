@@ -1242,16 +1242,16 @@ int mfma_cu_count() {
     return cus[dev];
 }
 
-// 2 tokens always; 3 from 32 rows per CU and 4 from 64 over K <= 4096
-// (Q4_K 19456 x 2560 at M = 3 / 4: 13.2 / 13.5 -> 10.1 / 11.3 us, 9728 x
-// 2560 at M = 3: 7.7 -> 7.2; below, and Q5_K 6144 x 2560 at M = 3 (6.8
-// against 7.0), the MFMA kernels stay), and from 96 rows per CU at any K.
+// 2 tokens always; 3 from 32 up to 96 rows per CU over K <= 4096 (Q4_K
+// 19456 x 2560: 10.4 against 10.8 us, 9728 x 2560: 7.1 against 7.7). At 4
+// tokens, and at 3 on taller tensors, the MFMA kernels measure faster since
+// the part kernel issues its codes ahead of its first block (Q6_K 151936 x
+// 2560 at M = 3 / 4: 80.8 / 92.7 -> 74.5 / 77.3 us, Q4_K 25000 x 1024 at
+// M = 4: 13.0 -> 8.8, Q4_K 19456 x 2560 at M = 4: 11.7 -> 10.8).
 bool gemv_mt_shape(const MatArgs &a) {
     const int cus = mfma_cu_count();
     if (a.M == 2) return true;
-    if (a.M == 3 && a.K <= 4096 && a.N >= 32 * cus) return true;
-    if (a.M == 4 && a.K <= 4096 && a.N >= 64 * cus) return true;
-    return a.M >= 3 && a.M <= 4 && a.N >= 96 * cus;
+    return a.M == 3 && a.K <= 4096 && a.N >= 32 * cus && a.N < 96 * cus;
 }
 
 hipError_t launch_mfma(uint32_t type, const MatArgs *tasks, int n, const Q8KView &xk, const Q80View &x0,

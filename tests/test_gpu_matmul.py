@@ -99,12 +99,14 @@ def test_gemv_other_projection_shapes(ctx, oracle, type_id, N, K):
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 2560, 2, False), (TYPE_Q5_K, 300, 4096, 2, True),
                                                     (TYPE_Q6_K, 2560, 9728, 2, True), (TYPE_Q5_K, 4099, 3072, 2, False),
                                                     (TYPE_Q6_K, 30000, 2560, 3, True), (TYPE_Q4_K, 25000, 1024, 4, False),
-                                                    (TYPE_Q4_K, 9728, 2560, 3, True), (TYPE_Q5_K, 17000, 4096, 4, False)])
+                                                    (TYPE_Q4_K, 9728, 2560, 3, True), (TYPE_Q5_K, 17000, 4096, 4, False),
+                                                    (TYPE_Q6_K, 20000, 2560, 3, True), (TYPE_Q5_K, 8192, 4096, 3, False),
+                                                    (TYPE_Q6_K, 151936, 2560, 4, False)])
 def test_gemv_two_to_four_tokens(ctx, oracle, type_id, N, K, M, residual):
-    """2 tokens, 3 from 32 rows per CU and 4 from 64 (K <= 4096), and 3..4
-    on tensors past 96 rows per CU: the batch-1 GEMV's shape with every
-    token's row in LDS (4-, 2- and 1-row groups, ragged last group,
-    residual)."""
+    """2 tokens, and 3 from 32 up to 96 rows per CU over K <= 4096: the
+    batch-1 GEMV's shape with every token's row in LDS (4-, 2- and 1-row
+    groups, ragged last group, residual); 4 tokens and 3 on taller tensors
+    (the LM head among them) on the MFMA kernels."""
     _run(ctx, oracle, type_id, N, K, M, seed=1900 + N + M, residual=residual)
 
 
