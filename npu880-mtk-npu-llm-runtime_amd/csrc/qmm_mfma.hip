@@ -1074,9 +1074,11 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // 15.7 / 20.8 / 22.7; on taller tensors (Q4_K / Q6_K 9728 x 4096, Q8_0
     // 6144 x 2560) faster at M = 16 (12.0 / 14.9 / 13.3 against 13.6 / 16.5 /
     // 15.1), slower at M = 64 (27.9 / 36.4 / 27.5 against 21.8 / 28.9 / 23.0)
-    // (Q4_K / Q5_K up to 16 tokens over K <= 4096 take the part kernel below)
+    // (Q4_K / Q5_K over K <= 4096 take the part kernel below: 4096 x 4096
+    // at M = 24 / 40 / 64 8.3 / 10.9 / 13.0 -> 7.6 / 9.0 / 10.0 us, 2560 x
+    // 3584 8.9 / 9.3 / 12.4 -> 7.3 / 7.4 / 10.0, Q5_K 1024 x 4096 6.7 -> 6.1)
     constexpr bool kQ45 = std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K>;
-    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>) && !(kQ45 && a.M <= 16 && a.K <= 4096)) {
+    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>) && !(kQ45 && a.K <= 4096)) {
         int wg = 0;  // workgroups of the configuration below
         for (int i = 0; i < n; ++i)
             wg += a.M <= 32 ? (tasks[i].N + 31) / 32 : (tasks[i].N + 63) / 64 * ((a.M + 31) / 32);
@@ -1099,10 +1101,10 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // M = 24 / 32 9.3 -> 8.1 / 8.3, Q5_K 1024 x 2560 at M = 64 6.8 -> 5.3.
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         hipError_t e = hipErrorNotSupported;
-        // (K up to 4096 from 17 tokens, on the tensors the K-split tiles
-        // above leave: Q4_K 9728 x 4096 at M = 24 / 48 / 64 16.0 / 21.6 /
+        // (K up to 4096: from 17 tokens on the tensors the K-split tiles
+        // above leave — Q4_K 9728 x 4096 at M = 24 / 48 / 64 16.0 / 21.6 /
         // 21.8 -> 14.4 / 18.2 / 20.3 us against the chunked tiles, 6144 x
-        // 3584 at M = 48 14.3 -> 12.1; and Q4_K / Q5_K at every M <= 16:
+        // 3584 at M = 48 14.3 -> 12.1 — and Q4_K / Q5_K at every M <= 64:
         // Q4_K 9728 x 4096 at M = 8 / 16 10.4 / 12.0 -> 10.2 / 10.2 us,
         // 19456 x 4096 at M = 12 18.3 -> 14.3, 2560 x 4096 at M = 8 6.65 ->
         // 5.83, Q5_K 2560 x 3328 at M = 8 / 16 6.81 / 6.88 -> 6.05 / 6.02,

@@ -145,7 +145,7 @@ def test_mfma_small_m_long_k(ctx, oracle, type_id, K, M):
     _run(ctx, oracle, type_id, 70, K, M, seed=900 + K + M)
 
 
-@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q6_K, 2560, 9728, 64), (TYPE_Q5_K, 300, 4096, 40),
+@pytest.mark.parametrize("type_id,N,K,M", [(TYPE_Q6_K, 2560, 9728, 64), (TYPE_Q5_K, 300, 4608, 40),
                                            (TYPE_Q4_K, 333, 9728, 17), (TYPE_Q6_K, 200, 3328, 33),
                                            (TYPE_Q8_0, 2560, 2560, 48), (TYPE_Q6_K, 1000, 4096, 9),
                                            (TYPE_Q8_0, 130, 9728, 64)])
@@ -198,10 +198,13 @@ def test_part_kernel_small_m_layouts(ctx, oracle, type_id, N, K, M):
 
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 4096, 8, True), (TYPE_Q4_K, 19456, 4096, 12, False),
                                                     (TYPE_Q5_K, 2560, 3328, 16, True), (TYPE_Q5_K, 1000, 3584, 3, False),
-                                                    (TYPE_Q4_K, 1000, 4096, 9, False), (TYPE_Q5_K, 6144, 4096, 5, True)])
+                                                    (TYPE_Q4_K, 1000, 4096, 9, False), (TYPE_Q5_K, 6144, 4096, 5, True),
+                                                    (TYPE_Q5_K, 300, 4096, 40, True), (TYPE_Q4_K, 2560, 4096, 64, False),
+                                                    (TYPE_Q5_K, 1024, 3584, 24, False), (TYPE_Q4_K, 4100, 3328, 56, True)])
 def test_part_kernel_small_m_long_k(ctx, oracle, type_id, N, K, M, residual):
-    """Q4_K / Q5_K up to 16 tokens over 3072 < K <= 4096: the part kernel
-    with 4 blocks per K part (13..16 blocks per row), partial last tiles."""
+    """Q4_K / Q5_K up to 64 tokens over 3072 < K <= 4096 at any tile count:
+    the part kernel with 4 blocks per K part (13..16 blocks per row), token
+    groups, partial last tiles."""
     _run(ctx, oracle, type_id, N, K, M, seed=1600 + N + M, residual=residual)
 
 
