@@ -1128,9 +1128,17 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
                 const bool g16 = tiles <= 2 * cus && !(std::is_same_v<F, MQ6KS> && 2 * tiles > cus);
                 e = g16 ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             } else if (a.M <= 48) {
-                e = launch_part<F, 1>(tasks, n, x, s);
+                // groups of 16; Q6_K groups of 32 from 3/4 of a tile per CU
+                // (6144 x 2560 at M = 40: 13.1 -> 11.4 us, 3328 x 2560 9.3 ->
+                // 8.6; 2560 x 2560 7.6 against 8.1)
+                const bool g32 = std::is_same_v<F, MQ6KS> && 4 * tiles > 3 * cus;
+                e = g32 ? launch_part<G, 2>(tasks, n, x, s) : launch_part<F, 1>(tasks, n, x, s);
             } else if (a.M <= 64) {
-                e = 2 * tiles < cus ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
+                // groups of 32 from half a tile per CU, over K > 3072 (4
+                // blocks per K part) from 3/4 (Q4_K 2560 x 4096 at M = 64:
+                // 8.8 against 9.4 us; 4096 x 4096 9.8 against 11.1)
+                const bool g16 = a.K > 3072 ? 4 * tiles < 3 * cus : 2 * tiles < cus;
+                e = g16 ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             }
         }
         if (e != hipErrorNotSupported) return e;
