@@ -1055,6 +1055,16 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
         // (Q6_K at 17..64 tokens over K > 3072, Q4_K / Q5_K at 33..64 over
         // K >= 8192: the decoded slabs split over K, where the launcher takes them)
+        // past 64 tokens over K <= 3072, the part kernel's 32-token groups
+        // where they number at most 4.5 workgroups per CU: the slabs' 64- and
+        // 128-token tiles leave most CUs idle on short tensors (Q6_K 1024 x
+        // 2560 at M = 80..128: 11.6 -> 6.8 us, Q4_K 2560 x 2560 at M = 80 /
+        // 128 11.3 / 11.4 -> 7.3 / 8.8, Q5_K 6144 x 2560 at M = 96 16.2 ->
+        // 14.5; 9728 x 2560 at M = 80 14.8 against 17.1 keeps the slabs)
+        if (a.M > 64 && a.K <= 3072 && 2 * group_tiles(tasks, n) * ((a.M + 31) / 32) <= 9 * mfma_cu_count()) {
+            const hipError_t e = launch_part<typename Folded<F>::T, 2>(tasks, n, x, s);
+            if (e != hipErrorNotSupported) return e;
+        }
         if (a.M > 64 || (a.M > 16 && a.K > 3072 && (std::is_same_v<F, MQ6KS> || (a.M > 32 && a.K >= 8192)))) {
             const hipError_t e = launch_slab<typename Folded<F>::T>(tasks, n, x, s);
             if (e != hipErrorNotSupported) return e;

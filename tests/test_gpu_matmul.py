@@ -200,6 +200,16 @@ def test_part_kernel_small_m_layouts(ctx, oracle, type_id, N, K, M):
     _run(ctx, oracle, type_id, N, K, M, seed=1500 + N + M)
 
 
+@pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q6_K, 1024, 2560, 100, True), (TYPE_Q4_K, 2560, 2560, 80, False),
+                                                    (TYPE_Q5_K, 300, 3072, 256, True), (TYPE_Q6_K, 2560, 2560, 192, False),
+                                                    (TYPE_Q4_K, 1000, 2560, 65, True), (TYPE_Q5_K, 6144, 2560, 96, False)])
+def test_part_kernel_past_64_tokens(ctx, oracle, type_id, N, K, M, residual):
+    """65..256 tokens over K <= 3072 on tensors short enough that 32-token
+    groups number at most 4.5 workgroups per CU: the part kernel (ragged
+    last token group, scales of every token in LDS)."""
+    _run(ctx, oracle, type_id, N, K, M, seed=1650 + N + M, residual=residual)
+
+
 @pytest.mark.parametrize("type_id,N,K,M,residual", [(TYPE_Q4_K, 9728, 4096, 8, True), (TYPE_Q4_K, 19456, 4096, 12, False),
                                                     (TYPE_Q5_K, 2560, 3328, 16, True), (TYPE_Q5_K, 1000, 3584, 3, False),
                                                     (TYPE_Q4_K, 1000, 4096, 9, False), (TYPE_Q5_K, 6144, 4096, 5, True),
