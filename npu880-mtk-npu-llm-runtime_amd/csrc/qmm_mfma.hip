@@ -1053,19 +1053,25 @@ template <class F>
 static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<F>::T &x, hipStream_t s) {
     const MatArgs &a = tasks[0];
     if constexpr (std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K> || std::is_same_v<F, MQ6KS>) {
-        // (Q6_K at 17..64 tokens over K > 3072, Q4_K / Q5_K at 33..64 over
-        // K >= 8192: the decoded slabs split over K, where the launcher takes them)
-        // past 64 tokens over K <= 3072, the part kernel's 32-token groups
-        // where they number at most 4.5 workgroups per CU: the slabs' 64- and
-        // 128-token tiles leave most CUs idle on short tensors (Q6_K 1024 x
-        // 2560 at M = 80..128: 11.6 -> 6.8 us, Q4_K 2560 x 2560 at M = 80 /
-        // 128 11.3 / 11.4 -> 7.3 / 8.8, Q5_K 6144 x 2560 at M = 96 16.2 ->
-        // 14.5; 9728 x 2560 at M = 80 14.8 against 17.1 keeps the slabs)
-        if (a.M > 64 && a.K <= 3072 && 2 * group_tiles(tasks, n) * ((a.M + 31) / 32) <= 9 * mfma_cu_count()) {
+        // (Q6_K at 17..64 tokens over K > 4096, Q4_K / Q5_K at 33..64 over
+        // K >= 8192: the decoded slabs split over K, where the launcher
+        // takes them; Q6_K over K <= 4096 measured faster on the part kernel:
+        // 9728 x 3584 at M = 48 / 64 31.3 / 32.4 -> 22.0 / 22.5 us, 1024 x
+        // 3328 at M = 24 / 64 10.9 / 12.4 -> 7.3 / 7.3)
+        // past 64 tokens over K <= 4096, the part kernel's 32-token groups
+        // where they number at most 4.5 workgroups per CU (over K > 3072: 3):
+        // the slabs' 64- and 128-token tiles leave most CUs idle on short
+        // tensors (Q6_K 1024 x 2560 at M = 80..128: 11.6 -> 6.8 us, Q4_K
+        // 2560 x 2560 at M = 80 / 128 11.3 / 11.4 -> 7.3 / 8.8, Q5_K 6144 x
+        // 2560 at M = 96 16.2 -> 14.5, Q5_K 1024 x 4096 at M = 80 17.5 ->
+        // 8.1; 9728 x 2560 at M = 80 14.8 against 17.1 keeps the slabs, Q6_K
+        // 4096 x 4096 at M = 128 16.8 against 19.6)
+        const int pwg = group_tiles(tasks, n) * ((a.M + 31) / 32), pcus = mfma_cu_count();
+        if (a.M > 64 && a.K <= 4096 && (a.K <= 3072 ? 2 * pwg <= 9 * pcus : pwg <= 3 * pcus)) {
             const hipError_t e = launch_part<typename Folded<F>::T, 2>(tasks, n, x, s);
             if (e != hipErrorNotSupported) return e;
         }
-        if (a.M > 64 || (a.M > 16 && a.K > 3072 && (std::is_same_v<F, MQ6KS> || (a.M > 32 && a.K >= 8192)))) {
+        if (a.M > 64 || (a.M > 16 && a.K > 4096 && (std::is_same_v<F, MQ6KS> || (a.M > 32 && a.K >= 8192)))) {
             const hipError_t e = launch_slab<typename Folded<F>::T>(tasks, n, x, s);
             if (e != hipErrorNotSupported) return e;
         }
@@ -1087,8 +1093,12 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
     // (Q4_K / Q5_K over K <= 4096 take the part kernel below: 4096 x 4096
     // at M = 24 / 40 / 64 8.3 / 10.9 / 13.0 -> 7.6 / 9.0 / 10.0 us, 2560 x
     // 3584 8.9 / 9.3 / 12.4 -> 7.3 / 7.4 / 10.0, Q5_K 1024 x 4096 6.7 -> 6.1)
+    // (and Q6_K from 17 tokens over K <= 4096: 2560 x 4096 at M = 24 / 48
+    // 10.4 / 12.0 -> 8.5 / 9.9 us, 4096 x 4096 at M = 24 10.8 -> 9.4)
     constexpr bool kQ45 = std::is_same_v<F, MQ4K> || std::is_same_v<F, MQ5K>;
-    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>) && !(kQ45 && a.K <= 4096)) {
+    constexpr bool kPart = kQ45 || std::is_same_v<F, MQ6KS>;
+    if (a.M > 8 && a.M <= 64 && (a.K > 3072 || std::is_same_v<G, MQ80>) &&
+        !(kPart && a.K <= 4096 && (kQ45 || a.M > 16))) {
         int wg = 0;  // workgroups of the configuration below
         for (int i = 0; i < n; ++i)
             wg += a.M <= 32 ? (tasks[i].N + 31) / 32 : (tasks[i].N + 63) / 64 * ((a.M + 31) / 32);

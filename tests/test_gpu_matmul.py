@@ -273,11 +273,12 @@ def _extreme_weights(type_id, N, K, seed):
 
 
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K])
-@pytest.mark.parametrize("M", [5, 40, 512])
-def test_mfma_extreme_scales(ctx, oracle, type_id, M):
+@pytest.mark.parametrize("M,K", [(5, 1024), (40, 1024), (512, 1024), (512, 4352), (40, 4352)])
+def test_mfma_extreme_scales(ctx, oracle, type_id, M, K):
     """Extreme scales and quants through the MFMA paths (scales folded into
-    the weight operand from M > 16): the integer sums stay exact."""
-    N, K = 96, 1024
+    the weight operand from M > 16; the slab kernels over K > 4096): the
+    integer sums stay exact."""
+    N = 96
     say(f"extreme scales {NAMES[type_id]} N={N} K={K} M={M}")
     w = _extreme_weights(type_id, N, K, seed=700 + M)
     x = synth.activations(M, K, seed=701)
@@ -334,10 +335,13 @@ def test_prefill_m512_every_row_tile(ctx, oracle, name):
 
 
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0])
-@pytest.mark.parametrize("N,K,M", [(70, 2560, 65), (201, 1024, 129), (64, 4096, 200), (130, 768, 300)])
+@pytest.mark.parametrize("N,K,M", [(70, 2560, 65), (201, 1024, 129), (64, 4096, 200), (130, 768, 300),
+                                   (70, 4352, 65), (201, 4608, 129), (130, 5120, 300)])
 def test_prefill_tails(ctx, oracle, type_id, N, K, M):
-    """The prefill kernel's partial row slabs and token groups (M > 64, N and
-    M not multiples of the workgroup tile), several K."""
+    """Partial row slabs and token groups past 64 tokens (N and M not
+    multiples of the workgroup tile), several K: the part kernel's 32-token
+    groups on these short tensors over K <= 4096, the slab kernels past
+    (Q8_0: the tile kernel)."""
     _run(ctx, oracle, type_id, N, K, M, seed=3200 + N + M + type_id)
 
 
@@ -346,7 +350,7 @@ def test_prefill_q5k_decoded_slabs_under_128(ctx, oracle, M):
     """Q5_K past 64 tokens on a tensor whose 32-row decoded slabs number at
     least 5/8 of the CUs: the decoded slabs with the tokens padded to 128
     (below that height the packed slabs), with a residual."""
-    _run(ctx, oracle, TYPE_Q5_K, 5200, 2560, M, seed=3600 + M, residual=True)
+    _run(ctx, oracle, TYPE_Q5_K, 9000, 2560, M, seed=3600 + M, residual=True)
 
 
 @pytest.mark.parametrize("type_id", [TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0])
@@ -548,8 +552,8 @@ def test_prefill_eight_wave_slabs(ctx, oracle, M, K, specs, residual):
 
 @pytest.mark.parametrize("type_id,M,K,specs,res_task", [
     (TYPE_Q5_K, 256, 2560, (2048, 512, 528), 1),
-    (TYPE_Q5_K, 333, 1024, (100, 37), 0),
-    (TYPE_Q6_K, 384, 1024, (300, 45), 1),
+    (TYPE_Q5_K, 333, 1024, (4000, 1037), 0),
+    (TYPE_Q6_K, 384, 1024, (3000, 450), 1),
     (TYPE_Q6_K, 129, 4352, (2560,), None),
 ])
 def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task):
@@ -587,13 +591,13 @@ def test_prefill_decoded_slab_groups(ctx, oracle, type_id, M, K, specs, res_task
     (32, 9728, (2560,), None),
     (24, 4352, (300, 45), 1),
     (17, 9728, (130,), 0),
-    (20, 3328, (200,), None),
+    (20, 4608, (200,), None),
 ])
 def test_small_m_q6k_decoded_slabs_k_split(ctx, oracle, M, K, specs, res_task):
-    """Q6_K at 17..64 tokens over long K (16 x 32 slabs up to 32 tokens,
+    """Q6_K at 17..64 tokens over K > 4096 (16 x 32 slabs up to 32 tokens,
     16 x 64 past): decoded slabs whose four K groups walk every fourth block
     and meet in block order, steps two deep; task groups, partial row slabs,
-    a residual, K not a multiple of 4 blocks (13, 17 and 38 blocks: four
+    a residual, K not a multiple of 4 blocks (17, 18 and 38 blocks: five
     to ten steps, the transfers issued past the last block reading zeros);
     every row of every task, all tokens, against the oracle."""
     say(f"small-M Q6_K K-split decoded slabs M={M} K={K} tasks={specs}")
@@ -654,14 +658,17 @@ def test_small_m_q4k_q5k_decoded_slabs_long_k(ctx, oracle, type_id, M, K, specs,
 
 @pytest.mark.parametrize("type_id,M,K,specs,res_task", [
     (TYPE_Q4_K, 8, 2560, (9728,), None),
-    (TYPE_Q4_K, 3, 2560, (9728,), 0),
+    (TYPE_Q4_K, 6, 512, (8200, 1000), 1),
+    (TYPE_Q4_K, 5, 3072, (9000,), 0),
+    (TYPE_Q4_K, 7, 2560, (6000, 4100), 0),
     (TYPE_Q4_K, 16, 512, (4096, 1000), 1),
     (TYPE_Q5_K, 5, 3072, (6144,), None),
     (TYPE_Q5_K, 16, 2560, (4100, 33), 0),
 ])
 def test_resident_tiles_groups(ctx, oracle, type_id, M, K, specs, res_task):
-    """Q4_K / Q5_K groups at 3..16 tokens with more row tiles than CUs take
-    the resident-tile kernel (two or three row tiles per workgroup); x with
+    """Q4_K groups at up to 8 tokens on two to three row tiles per CU take
+    the resident-tile kernel (three row tiles per workgroup), the others
+    the part kernel (one tile and 16 tokens per workgroup); x with
     codes at +-127 and an all-zero block; every row of every task, all
     tokens, against the oracle. Run three times: an MFMA result read too
     early gave wrong values in random tiles from run to run."""
