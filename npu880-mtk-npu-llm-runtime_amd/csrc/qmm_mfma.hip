@@ -1156,8 +1156,11 @@ static hipError_t launch_tile(const MatArgs *tasks, int n, const typename ActOf<
             } else if (a.M <= 64) {
                 // groups of 32 from half a tile per CU, over K > 3072 (4
                 // blocks per K part) from 3/4 (Q4_K 2560 x 4096 at M = 64:
-                // 8.8 against 9.4 us; 4096 x 4096 9.8 against 11.1)
-                const bool g16 = a.K > 3072 ? 4 * tiles < 3 * cus : 2 * tiles < cus;
+                // 8.8 against 9.4 us; 4096 x 4096 9.8 against 11.1), Q6_K
+                // there past 1/4 (2560 x 4096: 13.1 -> 11.4 us, 2048 x 3584
+                // 9.0 -> 8.3; 1024 x 3328 7.3 against 8.4)
+                const bool q6 = std::is_same_v<F, MQ6KS>;
+                const bool g16 = a.K > 3072 ? (q6 ? 4 * tiles <= cus : 4 * tiles < 3 * cus) : 2 * tiles < cus;
                 e = g16 ? launch_part<F, 1>(tasks, n, x, s) : launch_part<G, 2>(tasks, n, x, s);
             }
         }

@@ -169,14 +169,15 @@ def test_mfma_wide_tiles_long_k(ctx, oracle, type_id, N, K, M):
                                                     (TYPE_Q6_K, 2560, 2560, 24, True), (TYPE_Q6_K, 1024, 2560, 20, False),
                                                     (TYPE_Q6_K, 2050, 2560, 32, False), (TYPE_Q6_K, 3330, 2560, 40, True),
                                                     (TYPE_Q6_K, 2560, 2560, 47, False), (TYPE_Q4_K, 2560, 4096, 60, True),
-                                                    (TYPE_Q4_K, 4096, 3328, 52, False)])
+                                                    (TYPE_Q4_K, 4096, 3328, 52, False), (TYPE_Q6_K, 2560, 4096, 60, True),
+                                                    (TYPE_Q6_K, 1024, 3328, 50, False)])
 def test_small_m_token_group_bounds(ctx, oracle, type_id, N, K, M, residual):
     """The part kernel where the resident tiles would hold more than three
     per CU (M <= 16), 16-token groups at 49..64 tokens on few row tiles and
     at 17..32 on up to two tiles per CU (Q6_K: up to half a tile per CU,
     else all 32 tokens per workgroup), Q6_K groups of 32 at 33..48 from 3/4
     of a tile per CU, groups of 16 at 49..64 over K > 3072 below 3/4 of a
-    tile per CU, and over K up to 4096 (4 blocks per K part) from 17 tokens
+    tile per CU (Q6_K: up to 1/4), and over K up to 4096 (4 blocks per K part) from 17 tokens
     on tall tensors."""
     _run(ctx, oracle, type_id, N, K, M, seed=4100 + N + M, residual=residual)
 
